@@ -1,0 +1,236 @@
+"""Benchmark of the MI355X backend on BASELINE.json's configs (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm] [--no-cpu]
+
+Headline (`metric`/`value`): configs[1], the mapped tiled GEMM C = A.B, 4096^3 bf16 with f32
+accumulate and bf16 output, issued through the Backend seam (fo_contraction with the mappings
+lhs m![M/8, M%8, K], rhs m![N, K], out m![M/8, M%8, N]). A "step" is one such contraction over
+inputs already resident in HBM. The other configs are measured the same way and reported under
+"configs" (RMSNorm->softmax in GB/s, attention prefill and W8A8 in TFLOP/s, MLP in us).
+
+Timing: W untimed warmups, then exactly K steps bracketed by stream synchronizations; the kernel
+time is read from HIP events recorded on the runtime's own stream (the stream every op launches on).
+The CPU baseline runs the oracle (oracle/, the C restatement of the emulator's fold) on a bounded
+sample of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "furiosa-opt_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def f32_to_bf16(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def timed(rt, fn, steps: int, warmup: int):
+    """Returns (wall ms/step, event ms/step) for `steps` launches of fn after `warmup`."""
+    for _ in range(warmup):
+        fn()
+    rt.sync()
+    t0 = time.perf_counter()
+    rt.record(0)
+    for _ in range(steps):
+        fn()
+    rt.record(1)
+    rt.sync()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = rt.elapsed_ms(0, 1) / steps
+    return wall, ev
+
+
+def traffic_from_profiles(kernel_key: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE (profiles/traffic.json,
+    written from the committed counter summaries), or None if not measured."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel_key)
+    except Exception:
+        return None
+
+
+def bench_gemm(fh, rt, steps, warmup, rng):
+    M = N = K = 4096
+    s = dict(M=M, N=N, K=K)
+    a = rt.upload(f32_to_bf16(rng.standard_normal(M * K, dtype=np.float32)))
+    b = rt.upload(f32_to_bf16(rng.standard_normal(N * K, dtype=np.float32)))
+    c = rt.alloc(M * N * 2)
+    maps = [fh.m(t, **s) for t in ("M / 8, M % 8, K", "N, K", "M / 8, M % 8, N, K", "M / 8, M % 8, N")]
+    fn = lambda: rt.contraction(c, a, b, fh.BF16, fh.BF16, *maps)
+    wall, ev = timed(rt, fn, steps, warmup)
+    flop = 2.0 * M * N * K
+    tflops = flop / (ev * 1e-3) / 1e12
+    return dict(ms=ev, wall_ms=wall, tflops=tflops, flop=flop, bytes=3 * M * N * 2)
+
+
+def bench_norm(fh, rt, steps, warmup, rng):
+    R, Cc = 8192, 4096
+    x = rt.upload(f32_to_bf16(rng.standard_normal(R * Cc, dtype=np.float32)))
+    g = rt.upload(f32_to_bf16(1.0 + 0.1 * rng.standard_normal(Cc, dtype=np.float32)))
+    out = rt.alloc(R * Cc * 2)
+    fn = lambda: rt.rmsnorm_softmax(out, x, g, R, Cc, 1e-6)
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 2 * R * Cc * 2 + Cc * 2
+    return dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+
+
+def bench_attention(fh, rt, steps, warmup, rng):
+    B, H, S, D = 4, 32, 2048, 128
+    n = B * H * S * D
+    q, k, v = (rt.upload(f32_to_bf16(rng.standard_normal(n, dtype=np.float32))) for _ in range(3))
+    out = rt.alloc(n * 2)
+    fn = lambda: rt.attention_prefill(out, q, k, v, B, H, S, D, 11.313708, True)
+    wall, ev = timed(rt, fn, steps, warmup)
+    flop = 4.0 * B * H * D * S * (S + 1) / 2
+    return dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=4 * n * 2)
+
+
+def bench_w8a8(fh, rt, steps, warmup, rng):
+    M, N, K = 2048, 8192, 8192
+    a = rt.upload(rng.integers(-127, 128, M * K, dtype=np.int8))
+    w = rt.upload(rng.integers(-127, 128, N * K, dtype=np.int8))
+    sc = rt.upload(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
+    out = rt.alloc(M * N * 2)
+    fn = lambda: rt.gemm_w8a8_dequant(out, None, a, w, sc, M, N, K)
+    wall, ev = timed(rt, fn, steps, warmup)
+    op = 2.0 * M * N * K
+    return dict(ms=ev, wall_ms=wall, tops=op / (ev * 1e-3) / 1e12, op=op, bytes=M * K + N * K + N * 4 + M * N * 2)
+
+
+def bench_mlp(fh, rt, steps, warmup, rng):
+    B, I, Hd, O = 64, 784, 128, 10
+    x = rt.upload(f32_to_bf16(rng.uniform(0, 1, B * I).astype(np.float32)))
+    w1 = rt.upload(f32_to_bf16(0.05 * rng.standard_normal(Hd * I, dtype=np.float32)))
+    b1 = rt.upload(f32_to_bf16(0.05 * rng.standard_normal(Hd, dtype=np.float32)))
+    w2 = rt.upload(f32_to_bf16(0.05 * rng.standard_normal(O * Hd, dtype=np.float32)))
+    b2 = rt.upload(f32_to_bf16(0.05 * rng.standard_normal(O, dtype=np.float32)))
+    pred = rt.alloc(B * 4)
+    fn = lambda: rt.mlp(pred, None, x, w1, b1, w2, b2, B, I, Hd, O)
+    wall, ev = timed(rt, fn, steps, warmup)
+    return dict(ms=ev, wall_ms=wall, us=ev * 1e3, flop=2.0 * B * (I * Hd + Hd * O))
+
+
+def cpu_baseline_gemm(target_s: float = 12.0):
+    """The oracle's contraction_in fold (oracle/fo_cpu.c) on a bounded row sample of the same GEMM."""
+    from oracle import emulator as emu
+
+    M = N = K = 4096
+    rng = np.random.default_rng(7)
+    a = f32_to_bf16(rng.standard_normal(M * K, dtype=np.float32))
+    b = f32_to_bf16(rng.standard_normal(N * K, dtype=np.float32))
+    rows = 4
+    t0 = time.perf_counter()
+    emu.gemm_rows(a, b, M, N, K, 0, rows)
+    dt = time.perf_counter() - t0
+    rows = int(max(4, min(M, rows * target_s / max(dt, 1e-3))))
+    t0 = time.perf_counter()
+    emu.gemm_rows(a, b, M, N, K, 0, rows)
+    dt = time.perf_counter() - t0
+    flop = 2.0 * rows * N * K
+    return dict(value=flop / dt / 1e12, unit="TFLOP/s", cores=emu.num_threads(), kind="port",
+                sample=f"{rows} of 4096 output rows of the 4096^3 bf16 contraction ({dt:.1f} s)")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this backend runs on one GPU; multi-GPU sharding is design-only (DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import furiosa_hip as fh
+
+    rt = fh.Runtime(int(os.environ.get("FO_HIP_DEVICE", "0")))
+    info = rt.info()
+    rng = np.random.default_rng(0)
+    only = set(filter(None, args.only.split(",")))
+    res = {}
+    for name, fnb in (("gemm", bench_gemm), ("norm", bench_norm), ("attention", bench_attention),
+                      ("w8a8", bench_w8a8), ("mlp", bench_mlp)):
+        if only and name not in only:
+            continue
+        res[name] = fnb(fh, rt, args.steps, args.warmup, rng)
+        print(f"# {name}: {json.dumps(res[name])}", file=sys.stderr, flush=True)
+
+    g = res.get("gemm")
+    configs = {}
+    if "norm" in res:
+        r = res["norm"]
+        configs["rmsnorm_softmax_8192x4096"] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"],
+                                                    roofline_frac=r["gbs"] / PEAK_HBM_GBS)
+    if "attention" in res:
+        r = res["attention"]
+        configs["attention_prefill_b4h32s2048d128"] = dict(value=r["tflops"], unit="TFLOP/s", ms=r["ms"],
+                                                           roofline_frac=r["tflops"] / PEAK_BF16_TFLOPS)
+    if "w8a8" in res:
+        r = res["w8a8"]
+        configs["w8a8_2048x8192x8192"] = dict(value=r["tops"], unit="TOP/s", ms=r["ms"],
+                                              roofline_frac=r["tops"] / PEAK_I8_TOPS)
+    if "mlp" in res:
+        r = res["mlp"]
+        configs["mlp_64x784x128x10"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)
+    if g:
+        configs["mapped_gemm_4096"] = dict(value=g["tflops"], unit="TFLOP/s", ms=g["ms"],
+                                           roofline_frac=g["tflops"] / PEAK_BF16_TFLOPS)
+
+    cpu = None
+    if not args.no_cpu and g:
+        cpu = cpu_baseline_gemm()
+
+    traffic = traffic_from_profiles("gemm_bf16_4096")
+    line = {
+        "metric": "mapped GEMM contraction TFLOP/s (bf16 in, f32 acc, bf16 out)",
+        "value": g["tflops"] if g else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": g["ms"] if g else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: mapped tiled GEMM 4096^3, lhs m![M/8, M%8, K], rhs m![N, K] (K-major), "
+                               "out m![M/8, M%8, N]", "M": 4096, "N": 4096, "K": 4096},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": g["tflops"] if g else None,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": (g["tflops"] / PEAK_BF16_TFLOPS) if g else None,
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "configs": configs,
+        "device": info,
+    }
+    print(json.dumps(line), flush=True)
+    rt.close()
+
+
+if __name__ == "__main__":
+    main()

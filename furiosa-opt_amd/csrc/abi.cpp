@@ -1,0 +1,617 @@
+// The C ABI (include/furiosa_hip.h): handle management, error translation, and the host-side
+// planning that turns each Backend seam call's mappings into kernel descriptors.
+#include <algorithm>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "runtime.hpp"
+
+using namespace fo;
+namespace fm = fo::mapping;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <typename F>
+int32_t guard(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return FO_OK;
+  } catch (const InvalidArg& e) {
+    g_last_error = e.what();
+    return FO_ERR_INVALID;
+  } catch (const fm::Error& e) {
+    g_last_error = e.what();
+    return FO_ERR_INVALID;
+  } catch (const HipError& e) {
+    g_last_error = e.what();
+    return FO_ERR_HIP;
+  } catch (const OomError& e) {
+    g_last_error = e.what();
+    return FO_ERR_OOM;
+  } catch (const Unsupported& e) {
+    g_last_error = e.what();
+    return FO_ERR_UNSUPPORTED;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return FO_ERR_INVALID;
+  }
+}
+
+int64_t write_str(const std::string& s, char* out, uint64_t cap) {
+  if (out && cap) {
+    size_t n = std::min<size_t>(s.size(), cap - 1);
+    std::memcpy(out, s.data(), n);
+    out[n] = 0;
+  }
+  return (int64_t)s.size();
+}
+
+fm::Factors flat(const char* json_text, const char* what) {
+  require(json_text && *json_text, std::string(what) + ": mapping is required");
+  return fm::flatten(fm::parse_json(json_text));
+}
+
+void check_rt(fo_runtime* rt) { require(rt != nullptr, "runtime is NULL"); }
+void check_buf(const fo_buffer* b, const char* what) {
+  require(b != nullptr && b->ptr != nullptr, std::string(what) + " buffer is NULL");
+}
+
+void set_device(fo_runtime* rt) { FO_HIP(hipSetDevice(rt->device)); }
+
+// The live-digit sub-odometer of a wheel list (digits >= live are padding and never folded).
+std::vector<fm::Wheel> live_only(const std::vector<fm::Wheel>& ws) {
+  std::vector<fm::Wheel> out;
+  for (auto w : ws) {
+    if (w.live <= 1) continue;
+    w.size = w.live;
+    out.push_back(w);
+  }
+  return out;
+}
+
+std::vector<fm::Wheel> part(const fm::Joint& j, int p) {
+  std::vector<fm::Wheel> out;
+  for (auto& w : j.wheels)
+    if (w.part == p) out.push_back(w);
+  return out;
+}
+
+// Largest offset a walk over the live digits can reach in memory k (strides are >= 0).
+int64_t max_live_offset(const std::vector<fm::Wheel>& ws, int k) {
+  int64_t m = 0;
+  for (auto& w : ws)
+    if (w.live > 0) m += (w.live - 1) * w.stride[k];
+  return m;
+}
+
+int64_t product(const std::vector<fm::Wheel>& ws) {
+  int64_t p = 1;
+  for (auto& w : ws) p *= w.size;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fo_last_error(void) { return g_last_error.c_str(); }
+
+int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
+  return guard([&] {
+    require(out != nullptr, "out is NULL");
+    *out = nullptr;
+    int n = 0;
+    FO_HIP(hipGetDeviceCount(&n));
+    require(device_index >= 0 && device_index < n,
+            "device index " + std::to_string(device_index) + " out of range (" + std::to_string(n) + " devices)");
+    auto* rt = new fo_runtime();
+    rt->device = device_index;
+    try {
+      FO_HIP(hipSetDevice(device_index));
+      FO_HIP(hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking));
+      for (auto& e : rt->events) FO_HIP(hipEventCreate(&e));
+      hipDeviceProp_t prop;
+      FO_HIP(hipGetDeviceProperties(&prop, device_index));
+      rt->cus = prop.multiProcessorCount;
+      rt->arch = prop.gcnArchName;
+    } catch (...) {
+      fo_runtime_free(rt);
+      throw;
+    }
+    *out = rt;
+  });
+}
+
+void fo_runtime_free(fo_runtime* rt) {
+  if (!rt) return;
+  (void)hipSetDevice(rt->device);
+  if (rt->stream) (void)hipStreamSynchronize(rt->stream);
+  for (auto& e : rt->events)
+    if (e) (void)hipEventDestroy(e);
+  if (rt->stream) (void)hipStreamDestroy(rt->stream);
+  delete rt;
+}
+
+int32_t fo_runtime_synchronize(fo_runtime* rt) {
+  return guard([&] {
+    check_rt(rt);
+    FO_HIP(hipStreamSynchronize(rt->stream));
+  });
+}
+
+int32_t fo_runtime_device_info(fo_runtime* rt, int32_t* compute_units, char* arch, uint64_t arch_cap) {
+  return guard([&] {
+    check_rt(rt);
+    if (compute_units) *compute_units = rt->cus;
+    write_str(rt->arch, arch, arch_cap);
+  });
+}
+
+int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
+  return guard([&] {
+    check_rt(rt);
+    require(out != nullptr, "out is NULL");
+    *out = nullptr;
+    set_device(rt);
+    auto* b = new fo_buffer();
+    b->bytes = bytes;
+    b->device = rt->device;
+    hipError_t e = hipMalloc(&b->ptr, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+      delete b;
+      throw OomError("hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+    }
+    FO_HIP(hipMemsetAsync(b->ptr, 0, bytes ? bytes : 1, rt->stream));
+    FO_HIP(hipStreamSynchronize(rt->stream));
+    *out = b;
+  });
+}
+
+void fo_buffer_free(fo_buffer* buf) {
+  if (!buf) return;
+  if (buf->ptr) {
+    (void)hipSetDevice(buf->device);
+    (void)hipDeviceSynchronize();
+    (void)hipFree(buf->ptr);
+  }
+  delete buf;
+}
+
+int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(src, "src");
+    require(out != nullptr, "out is NULL");
+    fo_buffer* b = nullptr;
+    int32_t st = fo_buffer_alloc(rt, src->bytes, &b);
+    if (st != FO_OK) throw OomError(g_last_error);
+    FO_HIP(hipMemcpyAsync(b->ptr, src->ptr, src->bytes, hipMemcpyDeviceToDevice, rt->stream));
+    *out = b;
+  });
+}
+
+uint64_t fo_buffer_bytes(const fo_buffer* buf) { return buf ? buf->bytes : 0; }
+
+int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    require(host != nullptr || bytes == 0, "host pointer is NULL");
+    require(bytes <= dst->bytes, "write of " + std::to_string(bytes) + " bytes exceeds the buffer");
+    set_device(rt);
+    FO_HIP(hipMemcpyAsync(dst->ptr, host, bytes, hipMemcpyHostToDevice, rt->stream));
+    FO_HIP(hipStreamSynchronize(rt->stream));
+  });
+}
+
+int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(src, "src");
+    require(host != nullptr || bytes == 0, "host pointer is NULL");
+    require(bytes <= src->bytes, "read of " + std::to_string(bytes) + " bytes exceeds the buffer");
+    set_device(rt);
+    FO_HIP(hipMemcpyAsync(host, src->ptr, bytes, hipMemcpyDeviceToHost, rt->stream));
+    FO_HIP(hipStreamSynchronize(rt->stream));
+  });
+}
+
+int32_t fo_event_record(fo_runtime* rt, int32_t slot) {
+  return guard([&] {
+    check_rt(rt);
+    require(slot >= 0 && slot < 16, "event slot out of range");
+    FO_HIP(hipEventRecord(rt->events[slot], rt->stream));
+  });
+}
+
+int32_t fo_event_elapsed_ms(fo_runtime* rt, int32_t start, int32_t end, float* ms) {
+  return guard([&] {
+    check_rt(rt);
+    require(start >= 0 && start < 16 && end >= 0 && end < 16, "event slot out of range");
+    require(ms != nullptr, "ms is NULL");
+    FO_HIP(hipEventSynchronize(rt->events[end]));
+    FO_HIP(hipEventElapsedTime(ms, rt->events[start], rt->events[end]));
+  });
+}
+
+// ---- mapping utilities -------------------------------------------------------------------------
+
+int64_t fo_mapping_parse(const char* text, const char* axes_json, char* out, uint64_t cap) {
+  int64_t len = 0;
+  int32_t st = guard([&] {
+    require(text != nullptr, "text is NULL");
+    std::map<std::string, int64_t> sizes;
+    if (axes_json && *axes_json) {
+      json::Value v = json::parse(axes_json);
+      require(v.kind == json::Value::Object, "axes must be a JSON object");
+      for (auto& kv : v.obj) sizes[kv.first] = kv.second.as_int();
+    }
+    len = write_str(fm::to_json(fm::parse_text(text, sizes)), out, cap);
+  });
+  return st == FO_OK ? len : st;
+}
+
+int32_t fo_mapping_sequence(const char* memory, const char* stream, int32_t mode, int64_t* sizes, int64_t* lives,
+                            int64_t* strides, int32_t cap) {
+  int32_t n = 0;
+  int32_t st = guard([&] {
+    require(mode >= 0 && mode <= 2, "mode must be 0 (Read), 1 (Write) or 2 (Carve)");
+    fm::Joint j = fm::sequence({flat(memory, "memory")}, {flat(stream, "stream")}, (fm::Mode)mode);
+    n = (int32_t)j.wheels.size();
+    for (int32_t i = 0; i < n && i < cap; ++i) {
+      if (sizes) sizes[i] = j.wheels[i].size;
+      if (lives) lives[i] = j.wheels[i].live;
+      if (strides) strides[i] = j.wheels[i].stride[0];
+    }
+  });
+  return st == FO_OK ? n : st;
+}
+
+int64_t fo_mapping_carve(const char* self_map, const char* piece, char* out, uint64_t cap) {
+  int64_t len = 0;
+  int32_t st = guard([&] {
+    fm::Factors c = fm::carve(flat(self_map, "self"), flat(piece, "piece"));
+    len = write_str(fm::to_json(fm::unflatten(c)), out, cap);
+  });
+  return st == FO_OK ? len : st;
+}
+
+int64_t fo_mapping_window_base(const char* base_map, const char* offset) {
+  int64_t base = 0;
+  int32_t st = guard([&] {
+    base = fm::window_base(flat(base_map, "base"), fm::parse_offset_json(offset ? offset : ""));
+  });
+  return st == FO_OK ? base : st;
+}
+
+// ---- elementwise ---------------------------------------------------------------------------------
+
+int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* src, fo_dtype src_t, uint64_t n,
+               const fo_op* op) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    require(op != nullptr, "op is NULL");
+    require(n * dtype_bytes(dst_t) <= dst->bytes && n * dtype_bytes(src_t) <= src->bytes, "map: n exceeds a buffer");
+    if (n == 0) return;
+    set_device(rt);
+    launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
+  });
+}
+
+int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* a, const fo_buffer* b,
+                    fo_dtype in_t, uint64_t n, const fo_op* op) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(a, "a");
+    check_buf(b, "b");
+    require(op != nullptr, "op is NULL");
+    require(n * dtype_bytes(dst_t) <= dst->bytes && n * dtype_bytes(in_t) <= a->bytes &&
+                n * dtype_bytes(in_t) <= b->bytes,
+            "zip_with: n exceeds a buffer");
+    if (n == 0) return;
+    set_device(rt);
+    launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
+  });
+}
+
+int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, const fo_buffer* port,
+                      const fo_buffer* tag_u8, fo_dtype t, uint64_t n, const fo_slots* slots) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(data, "data");
+    check_buf(tag_u8, "tag");
+    require(slots != nullptr, "slots is NULL");
+    require(slots->n_regs >= 0 && slots->n_regs <= 4, "n_regs must be 0..4");
+    require(t == FO_F32 || t == FO_I32, "zip3_slots: dtype must be f32 or i32");
+    int64_t eb = dtype_bytes(t);
+    require(n * eb <= dst->bytes && n * eb <= data->bytes && n <= tag_u8->bytes, "zip3_slots: n exceeds a buffer");
+    if (slots->has_port) {
+      check_buf(port, "port");
+      require(n * eb <= port->bytes, "zip3_slots: n exceeds the port buffer");
+    }
+    if (n == 0) return;
+    set_device(rt);
+    launch_zip3_slots(rt->stream, dst->ptr, data->ptr, slots->has_port ? port->ptr : nullptr,
+                      (const uint8_t*)tag_u8->ptr, t, n, *slots);
+  });
+}
+
+// ---- mapping-driven ops --------------------------------------------------------------------------
+
+int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_view,
+                     const char* dst_view, const char* src_map, const char* dst_map, const char* src_offset,
+                     const char* dst_offset, int32_t allow_broadcast) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    fm::Factors sv = flat(src_view, "src_view"), dv = flat(dst_view, "dst_view");
+    // transpose_broadcast (backend/op_prep.rs:18-28): the dst leftover after carving out src.
+    if (!allow_broadcast)
+      require(fm::is_padding(fm::carve(dv, sv)), "transpose: Dst adds axes absent from Src; pass allow_broadcast");
+    fm::Joint j = fm::sequence({sv}, {dv}, fm::Mode::Carve);
+    fm::Factors sm = src_map && *src_map ? flat(src_map, "src_map") : sv;
+    fm::Factors dm = dst_map && *dst_map ? flat(dst_map, "dst_map") : dv;
+    int64_t src_base = fm::window_base(sm, fm::parse_offset_json(src_offset ? src_offset : ""));
+    int64_t dst_base = fm::window_base(dm, fm::parse_offset_json(dst_offset ? dst_offset : ""));
+    int64_t eb = dtype_bytes(t);
+    int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
+    require(dst_base <= dst_len, "transpose: dst window starts past the buffer");
+    int64_t count = std::min<int64_t>({j.stream_size, fm::size(dv), dst_len - dst_base});
+    if (count <= 0) return;
+    require(src_base + max_live_offset(j.wheels, 0) < src_len, "transpose: the src window reads past the buffer");
+    require(count < (1ll << 31), "transpose: more than 2^31 positions");
+    set_device(rt);
+    const int mem[1] = {0};
+    launch_relayout(rt->stream, dst->ptr, src->ptr, eb, dst_base, src_base, count, to_desc<1>(j.wheels, mem));
+  });
+}
+
+int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
+                     const char* dst_map) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    fm::Factors sm = flat(src_map, "src_map"), dm = flat(dst_map, "dst_map");
+    int64_t eb = dtype_bytes(t);
+    int64_t dn = fm::size(dm);
+    require(dn * eb <= (int64_t)dst->bytes, "transmute: dst buffer smaller than dst_map");
+    require(fm::size(sm) * eb <= (int64_t)src->bytes, "transmute: src buffer smaller than src_map");
+    // Self-walks: wire position <-> live rank.
+    auto self = [](const fm::Factors& f, bool by_live) {
+      std::vector<fm::Wheel> ws;
+      auto st = fm::strides(f);
+      for (size_t i = f.size(); i-- > 0;) {
+        fm::Wheel w;
+        w.size = by_live ? f[i].count : f[i].extent;
+        w.live = f[i].count;
+        w.stride = {st[i]};
+        ws.push_back(w);
+      }
+      return ws;
+    };
+    auto dw = self(dm, false), sw = self(sm, true);
+    int64_t dlive = 1, slive = 1;
+    for (auto& x : dm) dlive *= x.count;
+    for (auto& x : sm) slive *= x.count;
+    require(slive >= dlive, "transmute: dst_map has more live elements than src_map");
+    if (dn == 0) return;
+    require(dn < (1ll << 31), "transmute: more than 2^31 positions");
+    set_device(rt);
+    const int mem[1] = {0};
+    launch_transmute(rt->stream, dst->ptr, src->ptr, eb, dn, to_desc<1>(dw, mem), to_desc<1>(sw, mem));
+  });
+}
+
+int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
+                  const char* dst_map, int32_t op, uint32_t identity, int32_t allow_broadcast) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    require(t == FO_F32 || t == FO_I32 || t == FO_BF16, "reduce: dtype must be f32, i32 or bf16");
+    require(op >= FO_RED_ADD && op <= FO_RED_ADD_SAT, "reduce: unknown op");
+    require(op != FO_RED_ADD_SAT || t == FO_I32, "reduce: saturating add is i32 only");
+    fm::Factors s = flat(src_map, "src_map"), d = flat(dst_map, "dst_map");
+    // BufStorage::reduce (buf.rs:331-376): inter = dst.carve(broadcast), residue = src.carve(inter).
+    auto bsyms = fm::broadcast_symbols(s, d);
+    require(allow_broadcast || bsyms.empty(),
+            "reduce: Dst adds axes absent from the source; pass allow_broadcast=true for reduce-then-broadcast");
+    fm::Factors bcast;
+    for (auto& x : d)
+      if (x.kind == fm::Factor::Term && std::find(bsyms.begin(), bsyms.end(), x.sym) != bsyms.end()) bcast.push_back(x);
+    fm::Factors inter = bcast.empty() ? d : fm::carve(d, bcast);
+    fm::Factors residue = fm::carve(s, inter);
+    fm::Joint j = fm::sequence({s}, {d, residue}, fm::Mode::Read);
+    auto ow = part(j, 0), rw = live_only(part(j, 1));
+    int64_t eb = dtype_bytes(t);
+    int64_t out_count = fm::size(d);
+    require(out_count * eb <= (int64_t)dst->bytes, "reduce: dst buffer smaller than dst_map");
+    require(out_count < (1ll << 31), "reduce: more than 2^31 output cells");
+    if (out_count == 0) return;
+    set_device(rt);
+    const int mem[1] = {0};
+    launch_reduce(rt->stream, dst->ptr, src->ptr, t, (int64_t)(src->bytes / eb), out_count, to_desc<1>(ow, mem),
+                  to_desc<1>(rw, mem), op, identity);
+  });
+}
+
+int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs, fo_dtype in_t,
+                       fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
+                       const char* out_map) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(out, "out");
+    check_buf(lhs, "lhs");
+    check_buf(rhs, "rhs");
+    bool ok_types = (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
+                    (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32)) || (in_t == FO_F32 && out_t == FO_F32) ||
+                    (in_t == FO_I32 && out_t == FO_I32);
+    require(ok_types, "contraction: unsupported operand/output dtype pair");
+    fm::Factors l = flat(lhs_map, "lhs_map"), r = flat(rhs_map, "rhs_map");
+    fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");
+    // contraction_in (buf.rs:401-447): contracted = pre_reduce.carve(out); one ReadPlan per operand.
+    fm::Factors contracted = fm::carve(pre, o);
+    fm::Joint j = fm::sequence({l, r}, {o, contracted}, fm::Mode::Read);
+    auto ow = part(j, 0), rw = live_only(part(j, 1));
+    int64_t ib = dtype_bytes(in_t), ob = dtype_bytes(out_t);
+    int64_t out_count = fm::size(o);
+    require(out_count * ob <= (int64_t)out->bytes, "contraction: out buffer smaller than out_map");
+    require(out_count < (1ll << 31), "contraction: more than 2^31 output cells");
+    if (out_count == 0) return;
+    int64_t lhs_len = (int64_t)(lhs->bytes / ib), rhs_len = (int64_t)(rhs->bytes / ib);
+    set_device(rt);
+
+    // MFMA path: out wheels split into rows (lhs only) and columns (rhs only), one contiguous
+    // contracted wheel, no padding, every read in bounds.
+    if (gemm_supported(in_t, out_t)) {
+      std::vector<fm::Wheel> mw, nw, bw;
+      int64_t place = 1;
+      std::vector<int64_t> mplace, nplace, bplace;
+      bool shape_ok = true;
+      for (auto& w : ow) {
+        if (w.live != w.size) shape_ok = false;
+        bool la = w.stride[0] != 0, rb = w.stride[1] != 0;
+        if (la && !rb) {
+          mw.push_back(w);
+          mplace.push_back(place);
+        } else if (!la && rb) {
+          nw.push_back(w);
+          nplace.push_back(place);
+        } else if (la && rb) {
+          bw.push_back(w);
+          bplace.push_back(place);
+        } else {
+          mw.push_back(w);  // an output axis neither operand reads: rows that repeat
+          mplace.push_back(place);
+        }
+        place *= w.size;
+      }
+      shape_ok = shape_ok && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1 && rw.size() == 1 &&
+                 rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
+      if (shape_ok) {
+        GemmDesc d;
+        d.M = mw.empty() ? 1 : mw[0].size;
+        d.N = nw.empty() ? 1 : nw[0].size;
+        d.K = rw[0].size;
+        d.batch = bw.empty() ? 1 : bw[0].size;
+        d.lda = mw.empty() ? 0 : mw[0].stride[0];
+        d.ldb = nw.empty() ? 0 : nw[0].stride[1];
+        d.ldc_m = mw.empty() ? 0 : mplace[0];
+        d.ldc_n = nw.empty() ? 0 : nplace[0];
+        d.a_batch = bw.empty() ? 0 : bw[0].stride[0];
+        d.b_batch = bw.empty() ? 0 : bw[0].stride[1];
+        d.c_batch = bw.empty() ? 0 : bplace[0];
+        int64_t amax = (d.batch - 1) * d.a_batch + (d.M - 1) * d.lda + d.K - 1;
+        int64_t bmax = (d.batch - 1) * d.b_batch + (d.N - 1) * d.ldb + d.K - 1;
+        if (amax < lhs_len && bmax < rhs_len && gemm_aligned(lhs->ptr, rhs->ptr, in_t, d)) {
+          launch_gemm(rt->stream, out->ptr, lhs->ptr, rhs->ptr, in_t, out_t, d);
+          return;
+        }
+      }
+    }
+    const int mem[2] = {0, 1};
+    launch_contraction_generic(rt->stream, out->ptr, lhs->ptr, rhs->ptr, in_t, out_t, lhs_len, rhs_len, out_count,
+                               to_desc<2>(ow, mem), to_desc<2>(rw, mem));
+  });
+}
+
+// ---- fused chains ----------------------------------------------------------------------------------
+
+int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, const fo_buffer* gain, int64_t rows,
+                           int64_t cols, float eps) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(out, "out");
+    check_buf(x, "x");
+    check_buf(gain, "gain");
+    require(rows > 0 && cols > 0, "rmsnorm_softmax: empty shape");
+    require((uint64_t)(rows * cols * 2) <= x->bytes && (uint64_t)(rows * cols * 2) <= out->bytes &&
+                (uint64_t)(cols * 2) <= gain->bytes,
+            "rmsnorm_softmax: shape exceeds a buffer");
+    set_device(rt);
+    launch_rmsnorm_softmax(rt->stream, (uint16_t*)out->ptr, (const uint16_t*)x->ptr, (const uint16_t*)gain->ptr, rows,
+                           cols, eps);
+  });
+}
+
+int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q, const fo_buffer* k,
+                             const fo_buffer* v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                             float sqrt_d, int32_t causal) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(out, "out");
+    check_buf(q, "q");
+    check_buf(k, "k");
+    check_buf(v, "v");
+    require(batch > 0 && heads > 0 && seq > 0, "attention: empty shape");
+    require(head_dim == 64 || head_dim == 128, "attention: head_dim must be 64 or 128");
+    uint64_t bytes = (uint64_t)(batch * heads * seq * head_dim * 2);
+    require(bytes <= q->bytes && bytes <= k->bytes && bytes <= v->bytes && bytes <= out->bytes,
+            "attention: shape exceeds a buffer");
+    set_device(rt);
+    launch_attention_prefill(rt->stream, (uint16_t*)out->ptr, (const uint16_t*)q->ptr, (const uint16_t*)k->ptr,
+                             (const uint16_t*)v->ptr, batch, heads, seq, head_dim, sqrt_d, causal);
+  });
+}
+
+int32_t fo_gemm_w8a8_dequant(fo_runtime* rt, fo_buffer* out, fo_buffer* acc_out, const fo_buffer* a,
+                             const fo_buffer* w, const fo_buffer* scale, int64_t m, int64_t n, int64_t k) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(out, "out");
+    check_buf(a, "a");
+    check_buf(w, "w");
+    check_buf(scale, "scale");
+    require(m > 0 && n > 0 && k > 0, "w8a8: empty shape");
+    require((uint64_t)(m * k) <= a->bytes && (uint64_t)(n * k) <= w->bytes && (uint64_t)(n * 4) <= scale->bytes &&
+                (uint64_t)(m * n * 2) <= out->bytes,
+            "w8a8: shape exceeds a buffer");
+    if (acc_out) {
+      check_buf(acc_out, "acc_out");
+      require((uint64_t)(m * n * 4) <= acc_out->bytes, "w8a8: shape exceeds acc_out");
+    }
+    set_device(rt);
+    launch_w8a8(rt->stream, (uint16_t*)out->ptr, acc_out ? (int32_t*)acc_out->ptr : nullptr, (const int8_t*)a->ptr,
+                (const int8_t*)w->ptr, (const float*)scale->ptr, m, n, k);
+  });
+}
+
+int32_t fo_mlp(fo_runtime* rt, fo_buffer* pred_i32, fo_buffer* logits, const fo_buffer* x, const fo_buffer* w1,
+               const fo_buffer* b1, const fo_buffer* w2, const fo_buffer* b2, int64_t batch, int64_t in_features,
+               int64_t hidden, int64_t out_features) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(pred_i32, "pred");
+    check_buf(x, "x");
+    check_buf(w1, "w1");
+    check_buf(b1, "b1");
+    check_buf(w2, "w2");
+    check_buf(b2, "b2");
+    require(batch > 0 && in_features > 0 && hidden > 0 && out_features > 0, "mlp: empty shape");
+    require(hidden <= 1024 && out_features <= 64, "mlp: hidden <= 1024 and out_features <= 64");
+    require((uint64_t)(batch * in_features * 2) <= x->bytes && (uint64_t)(hidden * in_features * 2) <= w1->bytes &&
+                (uint64_t)(hidden * 2) <= b1->bytes && (uint64_t)(out_features * hidden * 2) <= w2->bytes &&
+                (uint64_t)(out_features * 2) <= b2->bytes && (uint64_t)(batch * 4) <= pred_i32->bytes,
+            "mlp: shape exceeds a buffer");
+    if (logits) {
+      check_buf(logits, "logits");
+      require((uint64_t)(batch * out_features * 2) <= logits->bytes, "mlp: shape exceeds logits");
+    }
+    set_device(rt);
+    launch_mlp(rt->stream, (int32_t*)pred_i32->ptr, logits ? (uint16_t*)logits->ptr : nullptr,
+               (const uint16_t*)x->ptr, (const uint16_t*)w1->ptr, (const uint16_t*)b1->ptr, (const uint16_t*)w2->ptr,
+               (const uint16_t*)b2->ptr, batch, in_features, hidden, out_features);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,140 @@
+// Internal runtime types behind the C ABI handles, and the kernel launchers each kernel file
+// exports to the ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/furiosa_hip.h"
+#include "common.hpp"
+#include "mapping.hpp"
+
+struct fo_runtime {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t events[16] = {};
+  int cus = 0;
+  std::string arch;
+};
+
+struct fo_buffer {
+  void* ptr = nullptr;
+  uint64_t bytes = 0;
+  int device = 0;
+};
+
+namespace fo {
+
+struct InvalidArg : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct HipError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct OomError : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+struct Unsupported : std::runtime_error {
+  using std::runtime_error::runtime_error;
+};
+
+#define FO_HIP(call)                                                                              \
+  do {                                                                                            \
+    hipError_t _e = (call);                                                                       \
+    if (_e != hipSuccess)                                                                         \
+      throw ::fo::HipError(std::string(#call) + " failed: " + hipGetErrorString(_e));            \
+  } while (0)
+
+inline void require(bool cond, const std::string& what) {
+  if (!cond) throw InvalidArg(what);
+}
+
+inline int64_t dtype_bytes(fo_dtype t) {
+  switch (t) {
+    case FO_I8:
+    case FO_U8:
+      return 1;
+    case FO_I16:
+    case FO_BF16:
+      return 2;
+    case FO_I32:
+    case FO_F32:
+      return 4;
+  }
+  throw InvalidArg("unknown dtype");
+}
+
+// Host-side copy of wheels into the by-value kernel descriptor.
+template <int NMEM>
+Wheels<NMEM> to_desc(const std::vector<mapping::Wheel>& ws, const int (&mem)[NMEM]) {
+  Wheels<NMEM> d{};
+  require((int)ws.size() <= kMaxWheels, "mapping resolves to more than " + std::to_string(kMaxWheels) + " wheels");
+  d.n = (int)ws.size();
+  for (int i = 0; i < d.n; ++i) {
+    require(ws[i].size < (1ll << 31), "wheel too large for 32-bit addressing");
+    d.size[i] = (uint32_t)ws[i].size;
+    d.live[i] = (uint32_t)ws[i].live;
+    d.div[i] = FastDiv((uint32_t)ws[i].size);
+    for (int k = 0; k < NMEM; ++k) d.stride[k][i] = ws[i].stride[mem[k]];
+  }
+  return d;
+}
+
+// ---- launchers (one per kernel family) ----------------------------------------------------------
+
+// Transpose: dst[dst_base + p] = src[src_base + off(p)] for live p < count.
+void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_base, int64_t src_base,
+                     int64_t count, const Wheels<1>& w);
+// Transmute: dst live rank k <- src live rank k; dst padding zeroed.
+void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_count,
+                      const Wheels<1>& dst_self, const Wheels<1>& src_self);
+
+void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t, uint64_t n, const fo_op& op);
+void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
+                const fo_op& op);
+void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,
+                       uint64_t n, const fo_slots& slots);
+
+// Reduce over a plan: out wheels (memory strides into src) and residue wheels.
+void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,
+                   const Wheels<1>& out_w, const Wheels<1>& res_w, int op, uint32_t identity);
+
+// Generic contraction: out wheels / residue wheels with strides into (lhs, rhs).
+void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t,
+                                fo_dtype out_t, int64_t lhs_len, int64_t rhs_len, int64_t out_count,
+                                const Wheels<2>& out_w, const Wheels<2>& res_w);
+
+// MFMA GEMM for a contraction shaped C[m, n] = sum_k A[m, k] B[n, k] with k contiguous in both.
+struct GemmDesc {
+  int64_t M = 0, N = 0, K = 0;
+  int64_t batch = 1;
+  // element offsets: A(m,k) = a_batch*b + a_row(m) + k ; B(n,k) = b_batch*b + b_row(n) + k ;
+  // C(m,n) = c_batch*b + c_row(m) + c_col(n). Rows/cols are affine (stride) unless a table is given.
+  int64_t a_batch = 0, b_batch = 0, c_batch = 0;
+  int64_t lda = 0, ldb = 0, ldc_m = 0, ldc_n = 1;
+  const int64_t* a_rows = nullptr;  // device tables (nullptr = affine)
+  const int64_t* b_rows = nullptr;
+  const int64_t* c_rows = nullptr;
+  const int64_t* c_cols = nullptr;
+};
+// in_t FO_BF16 -> out FO_BF16 / FO_F32; in_t FO_I8 -> out FO_I8 / FO_I32.
+void launch_gemm(hipStream_t s, void* c, const void* a, const void* b, fo_dtype in_t, fo_dtype out_t,
+                 const GemmDesc& d);
+bool gemm_supported(fo_dtype in_t, fo_dtype out_t);
+bool gemm_aligned(const void* a, const void* b, fo_dtype in_t, const GemmDesc& d);
+
+void launch_w8a8(hipStream_t s, uint16_t* out, int32_t* acc_out, const int8_t* a, const int8_t* w, const float* scale,
+                 int64_t m, int64_t n, int64_t k);
+void launch_rmsnorm_softmax(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* gain, int64_t rows,
+                            int64_t cols, float eps);
+void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float sqrt_d, int causal);
+void launch_mlp(hipStream_t s, int32_t* pred, uint16_t* logits, const uint16_t* x, const uint16_t* w1,
+                const uint16_t* b1, const uint16_t* w2, const uint16_t* b2, int64_t batch, int64_t in_f,
+                int64_t hidden, int64_t out_f);
+
+}  // namespace fo

@@ -1,0 +1,299 @@
+"""Python binding of the MI355X backend's C ABI (include/furiosa_hip.h), over ctypes.
+
+This is the harness the tests and the benchmark drive the library through; a Rust `Hip: Backend`
+would bind the same header with bindgen. Nothing here computes: every call goes to
+`libfuriosa_hip.so`, and importing raises if the library has not been built.
+
+Mappings are passed as `m![...]` text plus axis sizes (parsed by the library into MappingSerde
+JSON) or as MappingSerde JSON directly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+from pathlib import Path
+from typing import Dict, Optional, Sequence
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("FO_HIP_LIB", _HERE.parent / "libfuriosa_hip.so"))
+
+if not LIB_PATH.exists():
+    raise ImportError(
+        f"{LIB_PATH} is not built; run `python furiosa-opt_amd/build.py` (or __graft_entry__.build())"
+    )
+
+_lib = C.CDLL(str(LIB_PATH))
+
+# ---- dtypes / ops (mirrors furiosa_hip.h) -------------------------------------------------------
+I8, U8, I16, I32, BF16, F32 = 0, 1, 2, 3, 4, 5
+NP_DTYPE = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32}
+NAMES = {"i8": I8, "u8": U8, "i16": I16, "i32": I32, "bf16": BF16, "f32": F32}
+
+OP = dict(
+    CAST=0, CAST_RELU=1, EXP=10, NEG_EXP=11, SQRT=12, TANH=13, SIGMOID=14, LOG=15, SIN=16, COS=17,
+    ADD_F=30, SUB_F=31, MUL_F=32, DIV_F=33, CLIP_ADD=40, CLIP_MIN=41, CLIP_MAX=42, CLIP_ABS_MIN=43,
+    CLIP_ABS_MAX=44, FMA_F=50, FXP_TO_FP=60, FP_TO_FXP=61, ADD_FXP=70, ADD_FXP_SAT=71, SUB_FXP=72,
+    SUB_FXP_SAT=73, MUL_FXP=74, MUL_INT=75, MIN_I=76, MAX_I=77, SHL=78, LSHR=79, ASHR=80,
+)
+RHS_IMM, SWAP = 1, 2
+RED = dict(ADD=0, MAX=1, MIN=2, MUL=3, ADD_SAT=4)
+
+
+class FoOp(C.Structure):
+    _fields_ = [("code", C.c_int32), ("flags", C.c_uint32), ("imm0", C.c_uint32), ("imm1", C.c_uint32)]
+
+
+class FoSlots(C.Structure):
+    _fields_ = [
+        ("op", FoOp),
+        ("n_regs", C.c_int32),
+        ("reg_guard", C.c_uint32 * 4),
+        ("reg_operand0", C.c_uint32 * 4),
+        ("reg_operand1", C.c_uint32 * 4),
+        ("has_port", C.c_int32),
+        ("port_guard", C.c_uint32),
+        ("port_operand1", C.c_uint32),
+    ]
+
+
+_P = C.c_void_p
+_sig = {
+    "fo_last_error": (C.c_char_p, []),
+    "fo_runtime_init": (C.c_int32, [C.c_int32, C.POINTER(_P)]),
+    "fo_runtime_free": (None, [_P]),
+    "fo_runtime_synchronize": (C.c_int32, [_P]),
+    "fo_runtime_device_info": (C.c_int32, [_P, C.POINTER(C.c_int32), C.c_char_p, C.c_uint64]),
+    "fo_buffer_alloc": (C.c_int32, [_P, C.c_uint64, C.POINTER(_P)]),
+    "fo_buffer_free": (None, [_P]),
+    "fo_buffer_clone": (C.c_int32, [_P, _P, C.POINTER(_P)]),
+    "fo_buffer_bytes": (C.c_uint64, [_P]),
+    "fo_write": (C.c_int32, [_P, _P, C.c_uint64, _P]),
+    "fo_read": (C.c_int32, [_P, _P, _P, C.c_uint64]),
+    "fo_event_record": (C.c_int32, [_P, C.c_int32]),
+    "fo_event_elapsed_ms": (C.c_int32, [_P, C.c_int32, C.c_int32, C.POINTER(C.c_float)]),
+    "fo_mapping_parse": (C.c_int64, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_uint64]),
+    "fo_mapping_sequence": (
+        C.c_int32,
+        [C.c_char_p, C.c_char_p, C.c_int32, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_int32],
+    ),
+    "fo_mapping_carve": (C.c_int64, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_uint64]),
+    "fo_mapping_window_base": (C.c_int64, [C.c_char_p, C.c_char_p]),
+    "fo_map": (C.c_int32, [_P, _P, C.c_int32, _P, C.c_int32, C.c_uint64, C.POINTER(FoOp)]),
+    "fo_zip_with": (C.c_int32, [_P, _P, C.c_int32, _P, _P, C.c_int32, C.c_uint64, C.POINTER(FoOp)]),
+    "fo_zip3_slots": (C.c_int32, [_P, _P, _P, _P, _P, C.c_int32, C.c_uint64, C.POINTER(FoSlots)]),
+    "fo_transpose": (
+        C.c_int32,
+        [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int32],
+    ),
+    "fo_reduce": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_int32, C.c_uint32, C.c_int32]),
+    "fo_contraction": (
+        C.c_int32,
+        [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p],
+    ),
+    "fo_transmute": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p]),
+    "fo_rmsnorm_softmax": (C.c_int32, [_P, _P, _P, _P, C.c_int64, C.c_int64, C.c_float]),
+    "fo_attention_prefill": (
+        C.c_int32,
+        [_P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int32],
+    ),
+    "fo_gemm_w8a8_dequant": (C.c_int32, [_P, _P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64]),
+    "fo_mlp": (
+        C.c_int32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64],
+    ),
+}
+for _name, (_res, _args) in _sig.items():
+    _f = getattr(_lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+EXPORTED = tuple(_sig)
+
+
+class FoError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[{status}] {msg}")
+        self.status = status
+
+
+def _check(st: int):
+    if st < 0:
+        raise FoError(st, _lib.fo_last_error().decode())
+    return st
+
+
+def _b(s: Optional[str]) -> Optional[bytes]:
+    return None if s is None else s.encode()
+
+
+# ---- mapping utilities (host only) ----------------------------------------------------------------
+
+
+def m(text: str, **sizes: int) -> str:
+    """`m![text]` with axis sizes -> MappingSerde JSON (parsed by the library)."""
+    axes = json.dumps(sizes).encode()
+    n = _check(_lib.fo_mapping_parse(text.encode(), axes, None, 0))
+    buf = C.create_string_buffer(n + 1)
+    _check(_lib.fo_mapping_parse(text.encode(), axes, buf, n + 1))
+    return buf.value.decode()
+
+
+def sequence(memory: str, stream: str, mode: int = 0):
+    """Wheels (size, live, stride) innermost-first of sequence([memory],[stream],mode)."""
+    cap = 64
+    s, l, st = (C.c_int64 * cap)(), (C.c_int64 * cap)(), (C.c_int64 * cap)()
+    n = _check(_lib.fo_mapping_sequence(memory.encode(), stream.encode(), mode, s, l, st, cap))
+    return [(s[i], l[i], st[i]) for i in range(n)]
+
+
+def carve(self_map: str, piece: str) -> str:
+    n = _check(_lib.fo_mapping_carve(self_map.encode(), piece.encode(), None, 0))
+    buf = C.create_string_buffer(n + 1)
+    _check(_lib.fo_mapping_carve(self_map.encode(), piece.encode(), buf, n + 1))
+    return buf.value.decode()
+
+
+def window_base(base_map: str, offset: Optional[Dict[str, int]]) -> int:
+    return _check(_lib.fo_mapping_window_base(base_map.encode(), _b(json.dumps(offset or {}))))
+
+
+# ---- runtime / buffers -------------------------------------------------------------------------------
+
+
+class Runtime:
+    def __init__(self, device: int = 0):
+        h = _P()
+        _check(_lib.fo_runtime_init(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            _lib.fo_runtime_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sync(self):
+        _check(_lib.fo_runtime_synchronize(self.h))
+
+    def info(self):
+        cus = C.c_int32()
+        arch = C.create_string_buffer(128)
+        _check(_lib.fo_runtime_device_info(self.h, C.byref(cus), arch, 128))
+        return {"compute_units": cus.value, "arch": arch.value.decode()}
+
+    def alloc(self, nbytes: int) -> "Buffer":
+        return Buffer(self, nbytes)
+
+    def upload(self, arr: np.ndarray) -> "Buffer":
+        arr = np.ascontiguousarray(arr)
+        b = Buffer(self, arr.nbytes)
+        _check(_lib.fo_write(self.h, arr.ctypes.data, arr.nbytes, b.h))
+        return b
+
+    def record(self, slot: int):
+        _check(_lib.fo_event_record(self.h, slot))
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        _check(_lib.fo_event_elapsed_ms(self.h, a, b, C.byref(ms)))
+        return ms.value
+
+    # -- seam ops --
+    def transpose(self, dst: "Buffer", src: "Buffer", dtype: int, src_view: str, dst_view: str,
+                  src_map: Optional[str] = None, dst_map: Optional[str] = None,
+                  src_offset: Optional[Dict[str, int]] = None, dst_offset: Optional[Dict[str, int]] = None,
+                  allow_broadcast: bool = False):
+        _check(_lib.fo_transpose(self.h, dst.h, src.h, dtype, src_view.encode(), dst_view.encode(), _b(src_map),
+                                 _b(dst_map), _b(json.dumps(src_offset) if src_offset else None),
+                                 _b(json.dumps(dst_offset) if dst_offset else None), int(allow_broadcast)))
+
+    def map(self, dst: "Buffer", dst_t: int, src: "Buffer", src_t: int, n: int, op: FoOp):
+        _check(_lib.fo_map(self.h, dst.h, dst_t, src.h, src_t, n, C.byref(op)))
+
+    def zip_with(self, dst: "Buffer", dst_t: int, a: "Buffer", b: "Buffer", in_t: int, n: int, op: FoOp):
+        _check(_lib.fo_zip_with(self.h, dst.h, dst_t, a.h, b.h, in_t, n, C.byref(op)))
+
+    def zip3_slots(self, dst: "Buffer", data: "Buffer", port: Optional["Buffer"], tag: "Buffer", dtype: int, n: int,
+                   slots: FoSlots):
+        _check(_lib.fo_zip3_slots(self.h, dst.h, data.h, port.h if port else None, tag.h, dtype, n, C.byref(slots)))
+
+    def reduce(self, dst: "Buffer", src: "Buffer", dtype: int, src_map: str, dst_map: str, op: int, identity_bits: int,
+               allow_broadcast: bool = False):
+        _check(_lib.fo_reduce(self.h, dst.h, src.h, dtype, src_map.encode(), dst_map.encode(), op, identity_bits,
+                              int(allow_broadcast)))
+
+    def contraction(self, out: "Buffer", lhs: "Buffer", rhs: "Buffer", in_t: int, out_t: int, lhs_map: str,
+                    rhs_map: str, pre_reduce: str, out_map: str):
+        _check(_lib.fo_contraction(self.h, out.h, lhs.h, rhs.h, in_t, out_t, lhs_map.encode(), rhs_map.encode(),
+                                   pre_reduce.encode(), out_map.encode()))
+
+    def transmute(self, dst: "Buffer", src: "Buffer", dtype: int, src_map: str, dst_map: str):
+        _check(_lib.fo_transmute(self.h, dst.h, src.h, dtype, src_map.encode(), dst_map.encode()))
+
+    # -- fused chains --
+    def rmsnorm_softmax(self, out: "Buffer", x: "Buffer", gain: "Buffer", rows: int, cols: int, eps: float):
+        _check(_lib.fo_rmsnorm_softmax(self.h, out.h, x.h, gain.h, rows, cols, eps))
+
+    def attention_prefill(self, out, q, k, v, batch, heads, seq, head_dim, sqrt_d, causal=True):
+        _check(_lib.fo_attention_prefill(self.h, out.h, q.h, k.h, v.h, batch, heads, seq, head_dim, sqrt_d,
+                                         int(causal)))
+
+    def gemm_w8a8_dequant(self, out, acc_out, a, w, scale, m_, n_, k_):
+        _check(_lib.fo_gemm_w8a8_dequant(self.h, out.h, acc_out.h if acc_out else None, a.h, w.h, scale.h, m_, n_,
+                                         k_))
+
+    def mlp(self, pred, logits, x, w1, b1, w2, b2, batch, in_f, hidden, out_f):
+        _check(_lib.fo_mlp(self.h, pred.h, logits.h if logits else None, x.h, w1.h, b1.h, w2.h, b2.h, batch, in_f,
+                           hidden, out_f))
+
+
+class Buffer:
+    def __init__(self, rt: Runtime, nbytes: int):
+        h = _P()
+        _check(_lib.fo_buffer_alloc(rt.h, nbytes, C.byref(h)))
+        self.h = h
+        self.rt = rt
+        self.nbytes = nbytes
+
+    def free(self):
+        if self.h:
+            _lib.fo_buffer_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def write(self, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        _check(_lib.fo_write(self.rt.h, arr.ctypes.data, arr.nbytes, self.h))
+
+    def read(self, dtype, count: Optional[int] = None) -> np.ndarray:
+        dt = np.dtype(NP_DTYPE[dtype] if isinstance(dtype, int) else dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        _check(_lib.fo_read(self.rt.h, self.h, out.ctypes.data, out.nbytes))
+        return out
+
+
+def op(code: str, flags: int = 0, imm0=0, imm1=0) -> FoOp:
+    """An elementwise op descriptor; float immediates are passed as their f32 bit patterns."""
+    def bits(v):
+        if isinstance(v, float):
+            return int(np.float32(v).view(np.uint32))
+        return int(np.int64(v) & 0xFFFFFFFF)
+    return FoOp(OP[code], flags, bits(imm0), bits(imm1))
+
+
+def f32_bits(v: float) -> int:
+    return int(np.float32(v).view(np.uint32))

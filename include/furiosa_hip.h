@@ -1,0 +1,263 @@
+/*
+ * furiosa_hip.h -- C ABI of the MI355X (gfx950) execution backend for furiosa-opt's storage ops.
+ *
+ * This is the drop-in boundary. In furiosa-opt every tensor operation lands in one of the methods
+ * of `trait Backend` (furiosa-opt-std/src/backend/mod.rs:41-248), implemented today by the CPU
+ * emulator `Cpu` (backend/cpu.rs:20-158) over `BufStorage` (storage/buf.rs) and by `Npu`
+ * (backend/npu/backend.rs:18-156) over the closed NPU runtime. A third `Hip` backend binds this
+ * header with bindgen, the way furiosa-opt-std/build.rs:31-38 binds
+ * vendor/x86_64-unknown-linux-gnu/device_runtime.h, and forwards each `Backend` method here.
+ *
+ * Conventions (modelled on device_runtime.h:54-233):
+ *   - opaque handles; every *_free(NULL) is a no-op;
+ *   - int32 status: FO_OK (0) or a negative FO_ERR_* code; fo_last_error() returns a thread-local
+ *     message for the last failure on the calling thread;
+ *   - a storage is the dense wire image of its mapping (element i at position i, padding
+ *     included), exactly BufStorage's packed layout (buf.rs:17-29) for byte-multiple dtypes;
+ *   - mappings cross the boundary as MappingSerde JSON (furiosa-mapping-types/src/lib.rs:433-543,
+ *     serde's externally tagged enum), the form `serde_json::to_string(&M::to_value())` produces;
+ *   - partial-view offsets (`&Index`) cross as the finalized coordinates, a JSON object
+ *     {"AXIS": coordinate, ...}, i.e. `Index::finalize()` (furiosa-mapping/src/lib.rs:214-243);
+ *     NULL or "" means the empty offset;
+ *   - closures (`impl Fn`) cannot cross a C ABI: each engine closure is named by an op descriptor
+ *     (fo_op, fo_slots, fo_reduce_op), the finite sets of engine/vector/op/mod.rs and cast.rs;
+ *   - every op is enqueued on the runtime's single HIP stream; calls that return host-visible data
+ *     (fo_read) complete before returning. Ops on one runtime are serialized in call order.
+ */
+#ifndef FURIOSA_HIP_H
+#define FURIOSA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------------------------- */
+#define FO_OK 0
+#define FO_ERR_INVALID -1   /* bad argument, ill-formed mapping or descriptor (the reference panics) */
+#define FO_ERR_HIP -2       /* a HIP runtime call failed */
+#define FO_ERR_OOM -3       /* device allocation failed */
+#define FO_ERR_UNSUPPORTED -4
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* fo_last_error(void);
+
+/* ---- element types (scalar.rs:262-375 for bf16; the byte-multiple subset of `Scalar`) ------- */
+typedef enum fo_dtype {
+  FO_I8 = 0,
+  FO_U8 = 1,
+  FO_I16 = 2,
+  FO_I32 = 3,
+  FO_BF16 = 4,
+  FO_F32 = 5
+} fo_dtype;
+
+/* ---- runtime and buffers ------------------------------------------------------------------ */
+typedef struct fo_runtime fo_runtime;
+typedef struct fo_buffer fo_buffer;
+
+/* Binds HIP device `device_index` and creates the runtime's stream.
+ * Replaces the NPU runtime acquisition (backend/npu/ffi.rs:76-123) and `Backend::bind_device`
+ * (backend/mod.rs:247). */
+int32_t fo_runtime_init(int32_t device_index, fo_runtime** out);
+void fo_runtime_free(fo_runtime* rt);
+int32_t fo_runtime_synchronize(fo_runtime* rt);
+/* Device properties for reporting: compute units and the gfx architecture name. */
+int32_t fo_runtime_device_info(fo_runtime* rt, int32_t* compute_units, char* arch, uint64_t arch_cap);
+
+/* Device allocation of `bytes` (zero-filled), the storage of an `HbmTensor`.
+ * Replaces Backend::alloc_hbm / zeroed (backend/mod.rs:60-66, cpu.rs:31-35). */
+int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out);
+void fo_buffer_free(fo_buffer* buf);
+/* Device-to-device copy into a new buffer (Storage: Clone). */
+int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out);
+uint64_t fo_buffer_bytes(const fo_buffer* buf);
+/* Host -> device (Backend::to_hbm, backend/mod.rs:236-239; NPU: furiosa_write, device_runtime.h). */
+int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst);
+/* Device -> host, completes before returning (Backend::from_hbm, backend/mod.rs:240-243). */
+int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes);
+
+/* Stream-ordered timing on the runtime's stream: record event `slot` (0..15), and read the
+ * elapsed milliseconds between two recorded slots (synchronizes on `end`). */
+int32_t fo_event_record(fo_runtime* rt, int32_t slot);
+int32_t fo_event_elapsed_ms(fo_runtime* rt, int32_t start, int32_t end, float* ms);
+
+/* ---- mapping utilities (host only; no device needed) --------------------------------------- */
+/* Parses `m![text]` (grammar furiosa-mapping-macro/src/parser/parser.lalrpop:37-82) with the axis
+ * sizes in `axes_json` ({"A": 8, ...}) into MappingSerde JSON. Returns the JSON length, or a
+ * negative status; writes at most `cap` bytes (NUL-terminated when it fits). */
+int64_t fo_mapping_parse(const char* text, const char* axes_json, char* out, uint64_t cap);
+/* Resolves `memory` against `stream` (sequence([memory],[stream],mode), furiosa-mapping/src/lib.rs:
+ * 107-116; mode 0 Read, 1 Write, 2 Carve) into odometer wheels, innermost first: wheel i has
+ * `sizes[i]` digits, the first `lives[i]` of which are live in the stream, and memory stride
+ * `strides[i]` (0 = broadcast). Offset of stream position p = sum(digit_i * stride_i)
+ * (SequencerIter, furiosa-mapping-types/src/lib.rs:875-988). Returns the wheel count or a
+ * negative status; at most `cap` wheels are written. */
+int32_t fo_mapping_sequence(const char* memory, const char* stream, int32_t mode, int64_t* sizes,
+                            int64_t* lives, int64_t* strides, int32_t cap);
+/* MappingExt::carve (furiosa-mapping/src/lib.rs:154-167) as MappingSerde JSON. */
+int64_t fo_mapping_carve(const char* self_map, const char* piece, char* out, uint64_t cap);
+/* window_base (storage/buf.rs:760-781): wire position of the offset's cell in `base_map`. */
+int64_t fo_mapping_window_base(const char* base_map, const char* offset);
+
+/* ---- elementwise op descriptors (engine/vector/op/semantics.rs, cast.rs) --------------------- */
+typedef enum fo_op_code {
+  /* casts: src dtype -> dst dtype with cast.rs rules (bf16<->f32 NaN canonicalisation and subnormal
+   * flush, float/bf16.rs:16-40; i32->i8/i16 wrap `as`; i8/i16->i32 sign extension) */
+  FO_OP_CAST = 0,
+  FO_OP_CAST_RELU = 1, /* f32 -> bf16, CommitCast::cast_relu (cast.rs:127-136) */
+  /* FpUnaryOp (semantics.rs:75-90), f32 -> f32 */
+  FO_OP_EXP = 10,
+  FO_OP_NEG_EXP = 11,
+  FO_OP_SQRT = 12,
+  FO_OP_TANH = 13,
+  FO_OP_SIGMOID = 14,
+  FO_OP_LOG = 15,
+  FO_OP_SIN = 16,
+  FO_OP_COS = 17,
+  /* FpBinaryOp (semantics.rs:93-102), f32 x f32 -> f32 */
+  FO_OP_ADD_F = 30,
+  FO_OP_SUB_F = 31,
+  FO_OP_MUL_F = 32,
+  FO_OP_DIV_F = 33,
+  /* ClipBinaryOpF32 (semantics.rs:133-143) */
+  FO_OP_CLIP_ADD = 40,
+  FO_OP_CLIP_MIN = 41,
+  FO_OP_CLIP_MAX = 42,
+  FO_OP_CLIP_ABS_MIN = 43,
+  FO_OP_CLIP_ABS_MAX = 44,
+  /* FpTernaryOp::FmaF (semantics.rs:105-111): a * b + c in one rounding */
+  FO_OP_FMA_F = 50,
+  /* FxpToFp / FpToFxp (semantics.rs:149-163, float/mod.rs:22-82); imm0 = integer width */
+  FO_OP_FXP_TO_FP = 60,
+  FO_OP_FP_TO_FXP = 61,
+  /* FxpBinaryOp and ClipBinaryOpI32 (semantics.rs:41-70, 118-130), i32 x i32 -> i32 */
+  FO_OP_ADD_FXP = 70,
+  FO_OP_ADD_FXP_SAT = 71,
+  FO_OP_SUB_FXP = 72,
+  FO_OP_SUB_FXP_SAT = 73,
+  FO_OP_MUL_FXP = 74,
+  FO_OP_MUL_INT = 75,
+  FO_OP_MIN_I = 76,
+  FO_OP_MAX_I = 77,
+  FO_OP_SHL = 78,
+  FO_OP_LSHR = 79,
+  FO_OP_ASHR = 80
+} fo_op_code;
+
+/* flags */
+#define FO_OP_RHS_IMM 1u  /* binary/ternary: the rhs operand is `imm0` (a register / constant) */
+#define FO_OP_SWAP 2u     /* BinaryArgMode::Mode10: op(rhs, data) instead of op(data, rhs) */
+
+typedef struct fo_op {
+  int32_t code;   /* fo_op_code */
+  uint32_t flags; /* FO_OP_* flags */
+  uint32_t imm0;  /* raw 32-bit pattern (f32 or i32) of an immediate rhs, or the int width */
+  uint32_t imm1;  /* raw 32-bit pattern of the ternary third operand when immediate */
+} fo_op;
+
+/* Backend::map (backend/mod.rs:92): dst[i] = op(src[i]) for i < n (unary, cast, or binary with an
+ * immediate rhs). */
+int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* src, fo_dtype src_t,
+               uint64_t n, const fo_op* op);
+/* Backend::zip_with (backend/mod.rs:96-100): dst[i] = op(a[i], b[i]). */
+int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* a, const fo_buffer* b,
+                    fo_dtype in_t, uint64_t n, const fo_op* op);
+
+/* The vector engine's tag-guarded slot pass, apply_slots (engine/vector/tensor/vector_tensor.rs:
+ * 892-938), carried by Backend::zip3_with (backend/mod.rs:107-112): each cell takes the first
+ * register slot whose guard admits its execution id `tag[i]` (combine(data, reg0, reg1)), else
+ * the port slot if its guard admits (combine(data, port[i], port_operand1)), else passes through.
+ * A guard is the 16-bit set of admitted 4-bit execution ids (TagGuard::admits,
+ * furiosa-opt-common-ir/src/lib.rs:250-260). `combine` is `op` (binary, or FO_OP_FMA_F). */
+typedef struct fo_slots {
+  fo_op op;
+  int32_t n_regs;         /* 0..4 register slots, in priority order */
+  uint32_t reg_guard[4];  /* admitted-id masks */
+  uint32_t reg_operand0[4];
+  uint32_t reg_operand1[4];
+  int32_t has_port;       /* 1: the port slot reads `port` */
+  uint32_t port_guard;
+  uint32_t port_operand1;
+} fo_slots;
+
+int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, const fo_buffer* port,
+                      const fo_buffer* tag_u8, fo_dtype t, uint64_t n, const fo_slots* slots);
+
+/* ---- mapping-driven storage ops ------------------------------------------------------------ */
+/* Backend::transpose (backend/mod.rs:121-129; BufStorage::transpose, storage/buf.rs:257-313):
+ * writes every live cell of the dst window from the src cell with equal coordinates.
+ * `src_view`/`dst_view` are the Src / Dst type mappings; `src_map`/`dst_map` the storages' base
+ * mappings used to place partial-view offsets (NULL = the view itself). */
+int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_view,
+                     const char* dst_view, const char* src_map, const char* dst_map, const char* src_offset,
+                     const char* dst_offset, int32_t allow_broadcast);
+
+typedef enum fo_reduce_op {
+  FO_RED_ADD = 0,     /* IntraSliceReduceOp*::Add */
+  FO_RED_MAX = 1,
+  FO_RED_MIN = 2,
+  FO_RED_MUL = 3,
+  FO_RED_ADD_SAT = 4  /* i32 saturating add */
+} fo_reduce_op;
+
+/* Backend::reduce (backend/mod.rs:142-147; BufStorage::reduce, storage/buf.rs:331-376): every dst
+ * cell folds its residue block of `src` left to right from `identity` (raw bits of one element of
+ * type t). dtype: FO_F32, FO_I32 or FO_BF16 (bf16 folds round each step, `half` arithmetic). */
+int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
+                  const char* dst_map, int32_t op, uint32_t identity, int32_t allow_broadcast);
+
+/* Backend::contraction / contraction_prewidened (backend/mod.rs:173-191; BufStorage::contraction_in,
+ * storage/buf.rs:401-447): out[o] = narrow(sum_r widen(lhs[..]) * widen(rhs[..])) over the axes of
+ * `pre_reduce` absent from `out_map`.
+ *   in_t = FO_BF16: accumulate f32; out_t FO_BF16 (contraction: one RNE narrow per cell) or FO_F32
+ *                   (the widened operand path: contract_outer's map(widen) then
+ *                   contraction_prewidened, engine/contraction/outer/mod.rs:124-164);
+ *   in_t = FO_I8:   accumulate i32; out_t FO_I8 (narrow wraps `as i8`) or FO_I32;
+ *   in_t = FO_F32 / FO_I32: contraction_prewidened, out_t == in_t. */
+int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs, fo_dtype in_t,
+                       fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
+                       const char* out_map);
+
+/* Backend::transmute (backend/mod.rs:228-232; BufStorage::transmute, storage/buf.rs:592-601):
+ * compacts src's live cells (wire order) into dst's live cells (wire order); dst padding is 0. */
+int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
+                     const char* dst_map);
+
+/* ---- fused chains (each equals a sequence of the seam ops above; fused as a performance
+ * contract, with the rounding points of the reference kernels) ------------------------------- */
+
+/* RMSNorm then row softmax over `rows` x `cols` bf16 (transformer/kernel/rmsnorm.rs:9-78 rounding
+ * points, then a VE softmax): per row ms = sum(x^2)/cols + eps; r = sqrt(ms);
+ * y = bf16((x*g)/r); m = max(y); e = exp(y-m); out = bf16(e / sum(e)). */
+int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, const fo_buffer* gain, int64_t rows,
+                           int64_t cols, float eps);
+
+/* Causal attention prefill, Q/K/V/O laid out m![B, H, S, D] bf16 (the QK^T / softmax / PV chain of
+ * transformer/kernel/attention.rs:32-392): s = bf16(f32(q.k) / sqrt_d); p = exp(s - m);
+ * o = bf16(sum bf16(p) * v); out = bf16(o / (sum p + 6.25e-8)). `sqrt_d` is the divisor
+ * (attention.rs:10 uses 11.313708 for D = 128). */
+int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q, const fo_buffer* k,
+                             const fo_buffer* v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                             float sqrt_d, int32_t causal);
+
+/* W8A8 contraction: acc[m,n] = sum_k a[m,k] * w[n,k] (i8 x i8 -> i32, exact), then
+ * out[m,n] = bf16(fixedpoint_to_float(acc, 31) * scale[n]) (float/mod.rs:36-62; the VE FxpToFp
+ * then MulF, then the Cast Engine narrow). `acc_out` (i32, optional, may be NULL) receives acc. */
+int32_t fo_gemm_w8a8_dequant(fo_runtime* rt, fo_buffer* out, fo_buffer* acc_out, const fo_buffer* a,
+                             const fo_buffer* w, const fo_buffer* scale, int64_t m, int64_t n, int64_t k);
+
+/* MLP classifier (furiosa-opt-examples/src/mnist/mod.rs:8-192 rounding points):
+ * h = bf16(x.W1); h = bf16(max(h + b1, 0)); y = bf16(h.W2); y = bf16(y + b2); pred = argmax(y)
+ * (last maximum wins on ties, tests/mnist_tests.rs:41-48). W1 is [hidden, in], W2 [out, hidden]
+ * (torch Linear layout, as mnist.safetensors stores them). `logits` (bf16, optional) receives y. */
+int32_t fo_mlp(fo_runtime* rt, fo_buffer* pred_i32, fo_buffer* logits, const fo_buffer* x, const fo_buffer* w1,
+               const fo_buffer* b1, const fo_buffer* w2, const fo_buffer* b2, int64_t batch, int64_t in_features,
+               int64_t hidden, int64_t out_features);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FURIOSA_HIP_H */

@@ -1,0 +1,165 @@
+"""GPU parity of the fused chains at the configs of BASELINE.json, through the C ABI.
+
+Small shapes are compared whole against the oracle; the full config shapes are compared on a
+seeded sample of rows / queries the oracle finishes in seconds, plus properties that hold at any
+size (softmax rows sum to one, i32 accumulators exact, argmax bit-exact).
+Tolerance for bf16 outputs: |got - ref| <= 1e-2 |ref| + 1e-2 rms(ref).
+"""
+import numpy as np
+import pytest
+
+import furiosa_hip as fh
+from oracle import emulator as emu
+from test_gpu_storage import close
+
+pytestmark = pytest.mark.gpu
+
+SQRT_HEAD_DIM = np.float32(11.313708)  # attention.rs:10
+
+
+def bf16(rng, n, scale=1.0, loc=0.0):
+    return emu.f32_to_bf16((rng.standard_normal(n) * scale + loc).astype(np.float32))
+
+
+# ---- RMSNorm -> softmax ------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(64, 4096), (37, 1024), (5, 1000), (16, 8192)])
+def test_rmsnorm_softmax_small(rt, shape):
+    rows, cols = shape
+    rng = np.random.default_rng(30)
+    x, g = bf16(rng, rows * cols), bf16(rng, cols, 0.1, 1.0)
+    want = emu.rmsnorm_softmax(x, g, rows, cols, 1e-6)
+    out = rt.alloc(rows * cols * 2)
+    rt.rmsnorm_softmax(out, rt.upload(x), rt.upload(g), rows, cols, 1e-6)
+    close(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want))
+
+
+def test_rmsnorm_softmax_config(rt):
+    rows, cols = 8192, 4096
+    rng = np.random.default_rng(31)
+    x, g = bf16(rng, rows * cols), bf16(rng, cols, 0.1, 1.0)
+    out = rt.alloc(rows * cols * 2)
+    rt.rmsnorm_softmax(out, rt.upload(x), rt.upload(g), rows, cols, 1e-6)
+    y = emu.bf16_to_f32(out.read(np.uint16)).reshape(rows, cols)
+    assert np.all(np.abs(y.sum(axis=1, dtype=np.float64) - 1.0) < 2e-2)  # every row a distribution
+    sample = rng.choice(rows, 48, replace=False)
+    xs = x.reshape(rows, cols)[sample].reshape(-1)
+    want = emu.bf16_to_f32(emu.rmsnorm_softmax(xs, g, len(sample), cols, 1e-6)).reshape(len(sample), cols)
+    close(y[sample], want)
+
+
+# ---- attention prefill ------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 256, 128), (2, 1, 200, 64), (1, 1, 64, 128), (1, 3, 333, 128)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_small(rt, shape, causal):
+    b, h, s, d = shape
+    rng = np.random.default_rng(32)
+    q, k, v = (bf16(rng, b * h * s * d) for _ in range(3))
+    sd = np.float32(np.sqrt(d)) if d != 128 else SQRT_HEAD_DIM
+    want = emu.attention_prefill(q, k, v, b * h, s, d, float(sd), causal)
+    out = rt.alloc(b * h * s * d * 2)
+    rt.attention_prefill(out, rt.upload(q), rt.upload(k), rt.upload(v), b, h, s, d, float(sd), causal)
+    close(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want))
+
+
+def test_attention_config_sampled(rt):
+    b, h, s, d = 4, 32, 2048, 128
+    rng = np.random.default_rng(33)
+    q, k, v = (bf16(rng, b * h * s * d) for _ in range(3))
+    out = rt.alloc(b * h * s * d * 2)
+    rt.attention_prefill(out, rt.upload(q), rt.upload(k), rt.upload(v), b, h, s, d, float(SQRT_HEAD_DIM), True)
+    got = emu.bf16_to_f32(out.read(np.uint16)).reshape(b * h, s, d)
+    assert np.isfinite(got).all()
+    heads = [0, 77]
+    for hh in heads:
+        sl = slice(hh * s * d, (hh + 1) * s * d)
+        want = emu.attention_prefill(q[sl], k[sl], v[sl], 1, s, d, float(SQRT_HEAD_DIM), True, s - 64, s)
+        w = emu.bf16_to_f32(want).reshape(s, d)[s - 64:]
+        close(got[hh, s - 64:], w)
+        want0 = emu.attention_prefill(q[sl], k[sl], v[sl], 1, s, d, float(SQRT_HEAD_DIM), True, 0, 64)
+        close(got[hh, :64], emu.bf16_to_f32(want0).reshape(s, d)[:64])
+
+
+# ---- W8A8 ------------------------------------------------------------------------------------------------
+
+
+def test_w8a8_small_exact_acc(rt):
+    m, n, k = 96, 160, 256
+    rng = np.random.default_rng(34)
+    a = rng.integers(-127, 128, m * k).astype(np.int8)
+    w = rng.integers(-127, 128, n * k).astype(np.int8)
+    scale = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    want, acc = emu.w8a8(a, w, scale, m, n, k)
+    out, accb = rt.alloc(m * n * 2), rt.alloc(m * n * 4)
+    rt.gemm_w8a8_dequant(out, accb, rt.upload(a), rt.upload(w), rt.upload(scale), m, n, k)
+    assert np.array_equal(accb.read(np.int32), acc)
+    assert np.array_equal(out.read(np.uint16), want)  # exact acc -> exact dequant and narrow
+
+
+def test_w8a8_config_sampled_rows(rt):
+    m, n, k = 2048, 8192, 8192
+    rng = np.random.default_rng(35)
+    a = rng.integers(-127, 128, m * k, dtype=np.int8)
+    w = rng.integers(-127, 128, n * k, dtype=np.int8)
+    scale = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    out, accb = rt.alloc(m * n * 2), rt.alloc(m * n * 4)
+    rt.gemm_w8a8_dequant(out, accb, rt.upload(a), rt.upload(w), rt.upload(scale), m, n, k)
+    got_acc = accb.read(np.int32).reshape(m, n)
+    got = out.read(np.uint16).reshape(m, n)
+    for r0 in (0, 1337, m - 2):
+        want, acc = emu.w8a8(a, w, scale, m, n, k, r0, r0 + 2)
+        assert np.array_equal(got_acc[r0:r0 + 2], acc.reshape(m, n)[r0:r0 + 2])
+        assert np.array_equal(got[r0:r0 + 2], want.reshape(m, n)[r0:r0 + 2])
+    # linearity: the column sums of acc equal (sum over rows of a) . w, exactly in int64
+    colsum = got_acc.astype(np.int64).sum(axis=0)
+    asum = a.reshape(m, k).astype(np.int64).sum(axis=0)
+    assert np.array_equal(colsum, w.reshape(n, k).astype(np.int64) @ asum)
+
+
+# ---- mapped GEMM through the seam -------------------------------------------------------
+
+
+def test_mapped_gemm_config_sampled(rt):
+    M = N = K = 4096
+    s = dict(M=M, N=N, K=K)
+    rng = np.random.default_rng(36)
+    a, b = bf16(rng, M * K), bf16(rng, N * K)
+    out = rt.alloc(M * N * 2)
+    rt.contraction(out, rt.upload(a), rt.upload(b), fh.BF16, fh.BF16, fh.m("M / 8, M % 8, K", **s), fh.m("N, K", **s),
+                   fh.m("M / 8, M % 8, N, K", **s), fh.m("M / 8, M % 8, N", **s))
+    got = emu.bf16_to_f32(out.read(np.uint16)).reshape(M, N)
+    for r0 in (0, 2049, M - 3):
+        want = emu.bf16_to_f32(emu.gemm_rows(a, b, M, N, K, r0, r0 + 3)).reshape(3, N)
+        close(got[r0:r0 + 3], want)
+
+
+# ---- MLP classifier ----------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("shape", [(64, 784, 128, 10), (1, 800, 256, 16), (7, 33, 40, 3)])
+def test_mlp_exact(rt, shape):
+    batch, in_f, hid, out_f = shape
+    rng = np.random.default_rng(37)
+    x = emu.f32_to_bf16(rng.uniform(0, 1, batch * in_f).astype(np.float32))
+    w1, b1 = bf16(rng, hid * in_f, 0.05), bf16(rng, hid, 0.05)
+    w2, b2 = bf16(rng, out_f * hid, 0.05), bf16(rng, out_f, 0.05)
+    pred, logits = emu.mlp(x, w1, b1, w2, b2, batch, in_f, hid, out_f)
+    pb, lb = rt.alloc(batch * 4), rt.alloc(batch * out_f * 2)
+    rt.mlp(pb, lb, *(rt.upload(t) for t in (x, w1, b1, w2, b2)), batch, in_f, hid, out_f)
+    assert np.array_equal(lb.read(np.uint16), logits)
+    assert np.array_equal(pb.read(np.int32), pred)
+
+
+def test_mlp_argmax_ties_take_the_last(rt):
+    # all logits equal (zero weights, equal biases): max_by keeps the last index.
+    batch, in_f, hid, out_f = 2, 16, 8, 10
+    z = np.zeros
+    x = emu.f32_to_bf16(np.ones(batch * in_f, np.float32))
+    b2 = emu.f32_to_bf16(np.full(out_f, 0.5, np.float32))
+    pb = rt.alloc(batch * 4)
+    rt.mlp(pb, None, rt.upload(x), rt.upload(z(hid * in_f, np.uint16)), rt.upload(z(hid, np.uint16)),
+           rt.upload(z(out_f * hid, np.uint16)), rt.upload(b2), batch, in_f, hid, out_f)
+    assert pb.read(np.int32).tolist() == [out_f - 1] * batch

@@ -1,0 +1,355 @@
+"""GPU parity of the Backend seam ops (transpose, map/zip/zip3, reduce, contraction, transmute)
+against the oracle, through the C ABI. Integer, byte and layout work must match bit for bit; so
+must every f32/bf16 result the GPU folds in the emulator's order (generic contraction, thread-per-
+cell reduce, IEEE elementwise ops). Reassociated float folds use the bf16 tolerance
+|got - ref| <= 1e-2 |ref| + 1e-2 rms(ref).
+"""
+import numpy as np
+import pytest
+
+import furiosa_hip as fh
+from oracle import emulator as emu
+from oracle import mapping_ref as mr
+from test_mapping_resolver import PAIRS
+from test_oracle_golden import SEQ_TABLES
+
+pytestmark = pytest.mark.gpu
+
+I8, I16, I32, BF16, F32 = fh.I8, fh.I16, fh.I32, fh.BF16, fh.F32
+
+
+def close(got, ref, rel=1e-2):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref ** 2)) if ref.size else 0.0
+    err = np.abs(got - ref)
+    bad = err > rel * np.abs(ref) + rel * rms
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; worst {err.max()}"
+
+
+def rand_words(rng, n, dtype):
+    if dtype == np.uint16:
+        return emu.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+    info = np.iinfo(dtype)
+    return rng.integers(info.min, info.max, n, endpoint=True).astype(dtype)
+
+
+def run_transpose(rt, sizes, src_t, dst_t, dtype, npdt, seed=0, **kw):
+    rng = np.random.default_rng(seed)
+    so, do = mr.parse(src_t, sizes), mr.parse(dst_t, sizes)
+    src = rand_words(rng, mr.size(so), npdt)
+    init = rand_words(rng, mr.size(do), npdt)
+    want = emu.transpose(init, src, so, do)
+    s, d = rt.upload(src), rt.upload(init)
+    rt.transpose(d, s, dtype, fh.m(src_t, **sizes), fh.m(dst_t, **sizes), **kw)
+    got = d.read(npdt)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", PAIRS, ids=[f"{c[1]} -> {c[2]}" for c in PAIRS])
+@pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16), (I32, np.int32)], ids=["i8", "bf16", "i32"])
+def test_transpose_pairs(rt, case, dt):
+    sizes, a, b = case
+    run_transpose(rt, sizes, a, b, dt[0], dt[1])
+
+
+@pytest.mark.parametrize("case", SEQ_TABLES, ids=[c[2] for c in SEQ_TABLES])
+def test_transpose_doc_tables(rt, case):
+    sizes, mem, stream, _ = case
+    run_transpose(rt, sizes, mem, stream, BF16, np.uint16, allow_broadcast=True)
+
+
+def test_transpose_broadcast_requires_flag(rt):
+    s = dict(A=16, T=4, P=4)
+    src, dst = rt.alloc(64), rt.alloc(4 * 16 * 4 * 4)
+    with pytest.raises(fh.FoError, match="allow_broadcast"):
+        rt.transpose(dst, src, I32, fh.m("A", **s), fh.m("T, A, P", **s))
+
+
+def test_transpose_large_tiled(rt):
+    # buf.rs:1038-1059 at MI355X scale: a 4096 x 4096 bf16 relayout takes the LDS-tiled path.
+    n = 4096
+    rng = np.random.default_rng(3)
+    a = rng.integers(0, 65535, n * n, dtype=np.uint16)
+    s, d = rt.upload(a), rt.alloc(n * n * 2)
+    sz = dict(R=n, C=n)
+    rt.transpose(d, s, BF16, fh.m("R, C", **sz), fh.m("C, R", **sz))
+    assert np.array_equal(d.read(np.uint16), a.reshape(n, n).T.reshape(-1))
+
+
+def test_transpose_partial_view_offsets(rt):
+    # A tile view (mapping-expressions.md:383-398): base m![A, B], view m![A, B / 32 = 2 # 16, B % 32]
+    # at offset B = 64, copied into a compact m![A, B / 32 = 2, B % 32].
+    s = dict(A=8, B=512)
+    base_o, view_o, dst_o = (mr.parse(t, s) for t in ("A, B", "A, B / 32 = 2 # 16, B % 32", "A, B / 32 = 2, B % 32"))
+    rng = np.random.default_rng(5)
+    src = rng.integers(-2 ** 31, 2 ** 31 - 1, 8 * 512, dtype=np.int64).astype(np.int32)
+    want = emu.transpose(np.zeros(8 * 64, np.int32), src, view_o, dst_o, src_map=base_o, src_offset={"B": 64})
+    assert np.array_equal(want.reshape(8, 64), src.reshape(8, 512)[:, 64:128])
+    sb, db = rt.upload(src), rt.alloc(8 * 64 * 4)
+    rt.transpose(db, sb, I32, fh.m("A, B / 32 = 2 # 16, B % 32", **s), fh.m("A, B / 32 = 2, B % 32", **s),
+                 src_map=fh.m("A, B", **s), src_offset={"B": 64})
+    assert np.array_equal(db.read(np.int32), want)
+
+
+def test_transpose_dst_padding_is_left_untouched(rt):
+    s = dict(A=6, B=5)
+    run_transpose(rt, s, "A, B", "B # 8, A # 7", I16, np.int16, seed=9)
+
+
+# ---- elementwise ---------------------------------------------------------------------------------
+
+EXACT_UNARY = ["SQRT"]
+APPROX_UNARY = ["EXP", "NEG_EXP", "TANH", "SIGMOID", "LOG", "SIN", "COS"]
+BINARY = ["ADD_F", "SUB_F", "MUL_F", "DIV_F", "CLIP_ADD", "CLIP_MIN", "CLIP_MAX", "CLIP_ABS_MIN", "CLIP_ABS_MAX"]
+IBINARY = ["ADD_FXP", "ADD_FXP_SAT", "SUB_FXP", "SUB_FXP_SAT", "MUL_FXP", "MUL_INT", "MIN_I", "MAX_I", "SHL", "LSHR",
+           "ASHR"]
+
+
+def gpu_map(rt, x, src_t, dst_t, op):
+    s = rt.upload(x)
+    d = rt.alloc(len(x) * np.dtype(fh.NP_DTYPE[dst_t]).itemsize)
+    rt.map(d, dst_t, s, src_t, len(x), op)
+    return d.read(dst_t)
+
+
+@pytest.mark.parametrize("name", EXACT_UNARY + APPROX_UNARY)
+def test_fp_unary(rt, name):
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(100_003) * 3).astype(np.float32)
+    if name in ("SQRT", "LOG"):
+        x = np.abs(x) + 1e-3
+    want = emu.map_(x, F32, F32, fh.OP[name])
+    got = gpu_map(rt, x, F32, F32, fh.op(name))
+    if name in EXACT_UNARY:
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    else:  # libm vs ROCm ocml: both faithfully rounded
+        ulp = np.abs(np.spacing(want.astype(np.float32)))
+        assert np.all(np.abs(got - want) <= 2 * ulp + 1e-30)
+
+
+@pytest.mark.parametrize("name", BINARY)
+def test_fp_binary_tensor_and_immediate(rt, name):
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal(65_537).astype(np.float32)
+    b = rng.standard_normal(65_537).astype(np.float32)
+    want = emu.zip_(a, b, F32, F32, fh.OP[name])
+    da, db = rt.upload(a), rt.upload(b)
+    out = rt.alloc(a.nbytes)
+    rt.zip_with(out, F32, da, db, F32, len(a), fh.op(name))
+    assert np.array_equal(out.read(F32).view(np.uint32), want.view(np.uint32))
+    imm = np.float32(0.3125)
+    want = emu.map_(a, F32, F32, fh.OP[name], fh.SWAP, fh.f32_bits(imm))
+    got = gpu_map(rt, a, F32, F32, fh.op(name, fh.RHS_IMM | fh.SWAP, float(imm)))
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", IBINARY)
+def test_fxp_binary(rt, name):
+    rng = np.random.default_rng(13)
+    a = rng.integers(-2 ** 31, 2 ** 31 - 1, 50_000, dtype=np.int64).astype(np.int32)
+    b = rng.integers(-2 ** 31, 2 ** 31 - 1, 50_000, dtype=np.int64).astype(np.int32)
+    if name in ("SHL", "LSHR", "ASHR"):
+        b = (b & 31).astype(np.int32)
+    want = emu.zip_(a, b, I32, I32, fh.OP[name])
+    da, db = rt.upload(a), rt.upload(b)
+    out = rt.alloc(a.nbytes)
+    rt.zip_with(out, I32, da, db, I32, len(a), fh.op(name))
+    assert np.array_equal(out.read(I32), want)
+
+
+def test_fma_and_fixed_point_conversions(rt):
+    rng = np.random.default_rng(14)
+    a = rng.standard_normal(40_000).astype(np.float32)
+    b = rng.standard_normal(40_000).astype(np.float32)
+    want = emu.zip_(a, b, F32, F32, fh.OP["FMA_F"], 0, fh.f32_bits(0.75))
+    da, db = rt.upload(a), rt.upload(b)
+    out = rt.alloc(a.nbytes)
+    rt.zip_with(out, F32, da, db, F32, len(a), fh.op("FMA_F", 0, 0, 0.75))
+    assert np.array_equal(out.read(F32).view(np.uint32), want.view(np.uint32))
+    i = rng.integers(-2 ** 31, 2 ** 31 - 1, 40_000, dtype=np.int64).astype(np.int32)
+    for w in (31, 16, 0):
+        want = emu.map_(i, I32, F32, fh.OP["FXP_TO_FP"], 0, w)
+        got = gpu_map(rt, i, I32, F32, fh.op("FXP_TO_FP", 0, w))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        want = emu.map_(a, F32, I32, fh.OP["FP_TO_FXP"], 0, w)
+        got = gpu_map(rt, a, F32, I32, fh.op("FP_TO_FXP", 0, w))
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("pair", [(F32, BF16, "CAST"), (BF16, F32, "CAST"), (F32, BF16, "CAST_RELU"), (I32, I8, "CAST"),
+                                  (I8, I32, "CAST"), (I32, I16, "CAST"), (I16, I32, "CAST")])
+def test_casts(rt, pair):
+    src_t, dst_t, name = pair
+    rng = np.random.default_rng(15)
+    n = 70_001
+    if src_t == F32:
+        x = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)  # every class
+    elif src_t == BF16:
+        x = rng.integers(0, 2 ** 16, n, dtype=np.uint32).astype(np.uint16)
+    else:
+        x = rand_words(rng, n, fh.NP_DTYPE[src_t])
+    want = emu.map_(x, src_t, dst_t, fh.OP[name])
+    got = gpu_map(rt, x, src_t, dst_t, fh.op(name))
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_zip3_slots(rt):
+    # apply_slots (vector_tensor.rs:892-938): first admitting register slot wins, then the port slot.
+    rng = np.random.default_rng(16)
+    n = 30_000
+    data = rng.standard_normal(n).astype(np.float32)
+    port = rng.standard_normal(n).astype(np.float32)
+    tag = rng.integers(0, 16, n, dtype=np.uint8)
+    guards = [0b0000000000001111, 0b0000000011111100]
+    op0 = [fh.f32_bits(2.0), fh.f32_bits(-1.5)]
+    op1 = [0, 0]
+    want = emu.zip3_slots(data, port, tag, F32, fh.OP["MUL_F"], 0, guards, op0, op1, True, 0xF0F0, 0)
+    sl = fh.FoSlots()
+    sl.op = fh.op("MUL_F")
+    sl.n_regs = 2
+    for k in range(2):
+        sl.reg_guard[k], sl.reg_operand0[k], sl.reg_operand1[k] = guards[k], op0[k], op1[k]
+    sl.has_port, sl.port_guard, sl.port_operand1 = 1, 0xF0F0, 0
+    out = rt.alloc(n * 4)
+    rt.zip3_slots(out, rt.upload(data), rt.upload(port), rt.upload(tag), F32, n, sl)
+    assert np.array_equal(out.read(F32).view(np.uint32), want.view(np.uint32))
+
+
+# ---- reduce ----------------------------------------------------------------------------------------
+
+REDUCES = [
+    (dict(K=8, M=4), "K, M", "K / 2, M", False),
+    (dict(A=4, B=2), "A", "A / 2, B", True),
+    (dict(R=256, C=512), "R, C", "C", False),
+    (dict(R=64, C=3000), "R, C", "R", False),          # few cells, long residue: wave path
+    (dict(A=6, B=40, C=7), "B, A # 8, C", "C, A", False),
+    (dict(B=16384, S=4), "B, S", "B", False),
+]
+
+
+@pytest.mark.parametrize("case", REDUCES, ids=[f"{c[1]} -> {c[2]}" for c in REDUCES])
+@pytest.mark.parametrize("dt", ["i32", "f32", "bf16"])
+@pytest.mark.parametrize("opname", ["ADD", "MAX"])
+def test_reduce(rt, case, dt, opname):
+    sizes, s_t, d_t, bc = case
+    so, do = mr.parse(s_t, sizes), mr.parse(d_t, sizes)
+    rng = np.random.default_rng(17)
+    n = mr.size(so)
+    t = fh.NAMES[dt]
+    if dt == "i32":
+        src = rng.integers(-1000, 1000, n).astype(np.int32)
+        ident = 0 if opname == "ADD" else 0x80000000
+    elif dt == "f32":
+        src = rng.standard_normal(n).astype(np.float32)
+        ident = fh.f32_bits(0.0) if opname == "ADD" else fh.f32_bits(-np.inf)
+    else:
+        src = emu.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+        ident = 0 if opname == "ADD" else 0xFF80
+    want = emu.reduce(src, t, so, do, fh.RED[opname], ident)
+    out = rt.alloc(mr.size(do) * src.itemsize)
+    rt.reduce(out, rt.upload(src), t, fh.m(s_t, **sizes), fh.m(d_t, **sizes), fh.RED[opname], ident, bc)
+    got = out.read(t)
+    live = mr.liveness(do)
+    n_out = mr.size(do)
+    wave_path = n_out < 16384 and len(src) // max(n_out, 1) >= 64
+    if dt == "i32" or opname == "MAX" or not wave_path:
+        assert np.array_equal(got[live].view(np.uint8), want[live].view(np.uint8))
+    else:
+        g = got if dt == "f32" else emu.bf16_to_f32(got)
+        w = want if dt == "f32" else emu.bf16_to_f32(want)
+        tol = 1e-4 if dt == "f32" else 5e-2
+        close(g[live], w[live], rel=tol)
+
+
+def test_reduce_rejects_unrequested_broadcast(rt):
+    s = dict(A=4, B=2)
+    with pytest.raises(fh.FoError, match="allow_broadcast"):
+        rt.reduce(rt.alloc(32), rt.alloc(16), I32, fh.m("A", **s), fh.m("A / 2, B", **s), 0, 0, False)
+
+
+# ---- contraction ----------------------------------------------------------------------------------
+
+CONTRACTIONS = [
+    (dict(M=2, K=3, N=2), "M, K", "K, N", "M, K, N", "M, N"),
+    (dict(M=2, K=3, N=2), "M, K", "K, N", "M, K, N", "N, M"),
+    (dict(M=2, K=2, N=2), "M, K = 2 # 4", "K = 2 # 4, N", "M, K = 2 # 4, N", "M, N"),
+    (dict(M=24, K=40, N=20), "K, M", "N, K", "M, N, K", "N, M"),
+    (dict(B=3, M=16, K=24, N=8), "B, M, K", "B, K, N", "B, M, N, K", "M, B, N"),
+    (dict(M=16, K=32, N=8, G=3), "M, K", "K, N", "G, M, N, K", "G, M, N"),  # output axis neither reads
+    (dict(M=64, K=100, N=5), "M / 8, M % 8, K", "N, K", "M / 8, M % 8, N, K", "M / 8, M % 8, N"),
+]
+
+
+@pytest.mark.parametrize("case", CONTRACTIONS, ids=[f"{c[1]}.{c[2]}->{c[4]}" for c in CONTRACTIONS])
+@pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I8), (I8, I32), (F32, F32), (I32, I32)],
+                         ids=["bf16", "bf16w", "i8", "i8w", "f32", "i32"])
+def test_contraction_generic_exact(rt, case, types):
+    sizes, l_t, r_t, p_t, o_t = case
+    in_t, out_t = types
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
+    rng = np.random.default_rng(18)
+    npin = fh.NP_DTYPE[in_t]
+    if in_t == BF16:
+        lhs = emu.f32_to_bf16(rng.standard_normal(mr.size(lo)).astype(np.float32))
+        rhs = emu.f32_to_bf16(rng.standard_normal(mr.size(ro)).astype(np.float32))
+    elif in_t == F32:
+        lhs = rng.standard_normal(mr.size(lo)).astype(np.float32)
+        rhs = rng.standard_normal(mr.size(ro)).astype(np.float32)
+    else:
+        lhs = rng.integers(-127, 128, mr.size(lo)).astype(npin)
+        rhs = rng.integers(-127, 128, mr.size(ro)).astype(npin)
+    want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
+    out = rt.alloc(mr.size(oo) * np.dtype(fh.NP_DTYPE[out_t]).itemsize)
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    got = out.read(out_t)
+    live = mr.liveness(oo)
+    assert np.array_equal(got[live].view(np.uint8), want[live].view(np.uint8))
+
+
+MFMA_CASES = [
+    (dict(M=256, K=512, N=384), "M / 8, M % 8, K", "N, K", "M / 8, M % 8, N, K", "M / 8, M % 8, N"),
+    (dict(M=200, K=96, N=136), "M, K", "N, K", "M, N, K", "M, N"),       # ragged tiles
+    (dict(M=128, K=256, N=96), "M, K", "N, K", "M, N, K", "N, M"),       # reordered output
+    (dict(B=4, M=64, K=128, N=64), "B, M, K", "B, N, K", "B, M, N, K", "B, M, N"),  # batched
+]
+
+
+@pytest.mark.parametrize("case", MFMA_CASES, ids=[f"{c[1]}.{c[2]}->{c[4]}" for c in MFMA_CASES])
+@pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I32), (I8, I8)], ids=["bf16", "bf16w", "i8w", "i8"])
+def test_contraction_mfma(rt, case, types):
+    sizes, l_t, r_t, p_t, o_t = case
+    in_t, out_t = types
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
+    rng = np.random.default_rng(19)
+    if in_t == BF16:
+        lhs = emu.f32_to_bf16(rng.standard_normal(mr.size(lo)).astype(np.float32))
+        rhs = emu.f32_to_bf16(rng.standard_normal(mr.size(ro)).astype(np.float32))
+    else:
+        lhs = rng.integers(-127, 128, mr.size(lo)).astype(np.int8)
+        rhs = rng.integers(-127, 128, mr.size(ro)).astype(np.int8)
+    want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
+    out = rt.alloc(mr.size(oo) * np.dtype(fh.NP_DTYPE[out_t]).itemsize)
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    got = out.read(out_t)
+    if in_t == I8:
+        assert np.array_equal(got, want)
+    elif out_t == F32:
+        close(got, want, rel=1e-3)
+    else:
+        close(emu.bf16_to_f32(got), emu.bf16_to_f32(want))
+
+
+# ---- transmute --------------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("maps", [("A # 8, B", "A, B"), ("A, B # 6", "B, A # 9"), ("A = 3 # 4, B # 8", "A = 3, B")])
+def test_transmute(rt, maps):
+    s = dict(A=6, B=5)
+    so, do = mr.parse(maps[0], s), mr.parse(maps[1], s)
+    rng = np.random.default_rng(20)
+    src = rng.integers(-100, 100, mr.size(so)).astype(np.int32)
+    want = emu.transmute(src, so, do)
+    out = rt.alloc(mr.size(do) * 4)
+    rt.transmute(out, rt.upload(src), I32, fh.m(maps[0], **s), fh.m(maps[1], **s))
+    assert np.array_equal(out.read(I32), want)
