@@ -42,6 +42,8 @@ CFLAGS = [
     "-Xclang",
     "-packed-fp32-ops",
     "-Wno-unused-result",
+    # every multiply and add rounds on its own, as Rust computes them (FMA only where written)
+    "-ffp-contract=off",
 ]
 
 

@@ -74,6 +74,24 @@ FO_HD float fixedpoint_to_float(int32_t input, uint32_t int_width) {
   return bits_f32((sign << 31) | ((expo & 0xffu) << 23) | mant);
 }
 
+// Correctly rounded f32 square root (what Rust's f32::sqrt returns). The hardware square root is
+// faithful, not correctly rounded, so the candidate is fixed up exactly: r is correct iff
+// (r - ulp/2)^2 <= x <= (r + ulp/2)^2, and those squares are exact in f64 (2 x 25 bits < 53).
+// A square root of an f32 is never a rounding midpoint, so no tie case exists.
+FO_HD float sqrt_rn(float x) {
+  if (!(x > 0.0f) || x == __builtin_inff()) return __builtin_sqrtf(x);  // 0, negative, NaN, inf
+  float r = (float)__builtin_sqrt((double)x);
+  uint32_t rb = f32_bits(r);
+  double half = (double)(bits_f32(rb + 1) - r) * 0.5;  // half ulp above r
+  double xd = (double)x;
+  double hi = (double)r + half;
+  double lo_half = (double)(r - bits_f32(rb - 1)) * 0.5;  // half ulp below r (smaller at a binade edge)
+  double lo = (double)r - lo_half;
+  if (lo * lo > xd) return bits_f32(rb - 1);
+  if (hi * hi < xd) return bits_f32(rb + 1);
+  return r;
+}
+
 // float_to_fixedpoint (float/mod.rs:22-34): round half away from zero (f64::round), clamp.
 FO_HD int32_t float_to_fixedpoint(float input, uint32_t int_width) {
   if (input != input) return (f32_bits(input) >> 31) ? INT32_MIN : INT32_MAX;

@@ -54,7 +54,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax(uint16_t* __restrict__ 
   ss = wave_sum(ss);
   // ms = ss / cols (vector_fp_div), ms + eps (vector_clip Add), r = sqrt (FpUnaryOp::Sqrt)
   float ms = __fadd_rn(__fdiv_rn(ss, cols_f), eps);
-  float r = __fsqrt_rn(ms);
+  float r = sqrt_rn(ms);
   float mx = -INFINITY;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax_any(uint16_t* __restric
     ss = __fadd_rn(ss, __fmul_rn(f, f));
   }
   ss = wave_sum(ss);
-  float r = __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), eps));
+  float r = sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)cols), eps));
   float mx = -INFINITY;
   for (int64_t i = lane; i < cols; i += 64) {
     float y = bf16_to_f32(f32_to_bf16(__fdiv_rn(__fmul_rn(bf16_to_f32(xr[i]), bf16_to_f32(gain[i])), r)));

@@ -344,7 +344,7 @@ __device__ __forceinline__ uint32_t unary_op(int code, uint32_t a, uint32_t imm)
     case FO_OP_NEG_EXP:
       return f32_bits(expf(-x));
     case FO_OP_SQRT:
-      return f32_bits(__fsqrt_rn(x));
+      return f32_bits(sqrt_rn(x));
     case FO_OP_TANH:
       return f32_bits(tanhf(x));
     case FO_OP_SIGMOID:
@@ -589,8 +589,9 @@ void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_
   int64_t total = 1;
   for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
   require(total < (1ll << 31), "reduce: residue larger than 2^31");
-  // Thread-per-cell keeps the emulator's exact fold order; use it whenever it fills the GPU.
-  if (out_count >= 16384 || total < 64) {
+  // Thread-per-cell keeps the emulator's exact fold order; use it whenever it fills the GPU, and
+  // always for bf16, whose per-step rounding makes any regrouping visible.
+  if (out_count >= 16384 || total < 64 || std::is_same<Tag, Bf16Red>::value) {
     hipLaunchKernelGGL(k_reduce_thread<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
                        (uint32_t)out_count, ow, rw, op, identity);
   } else {

@@ -59,7 +59,7 @@ def _load():
         "ref_zip": (None, [P, C.c_int, P, P, C.c_int, I64, C.c_int, U32, U32]),
         "ref_zip3_slots": (None, [P, P, P, P, C.c_int, I64, C.c_int, U32, C.c_int, P, P, P, C.c_int, U32, U32]),
         "ref_rmsnorm_softmax": (None, [P, P, P, I64, I64, F]),
-        "ref_attention_prefill": (None, [P, P, P, P, I64, I64, I64, F, C.c_int, I64, I64]),
+        "ref_attention_prefill": (None, [P, P, P, P, I64, I64, I64, F, C.c_int, I64, I64, C.c_int]),
         "ref_w8a8": (None, [P, P, P, P, P, I64, I64, I64, I64, I64]),
         "ref_mlp": (None, [P, P, P, P, P, P, P, I64, I64, I64, I64]),
         "ref_num_threads": (C.c_int, []),
@@ -236,13 +236,15 @@ def rmsnorm_softmax(x: np.ndarray, g: np.ndarray, rows: int, cols: int, eps: flo
 
 
 def attention_prefill(q, k, v, bh: int, seq: int, d: int, sqrt_d: float, causal: bool = True, q_begin: int = 0,
-                      q_end: Optional[int] = None) -> np.ndarray:
+                      q_end: Optional[int] = None, causal_max: bool = False) -> np.ndarray:
+    """`causal_max=False` is the reference's semantics (row max over every key before masking);
+    `causal_max=True` takes the max over the unmasked keys only."""
     if seq > 8192:
         raise ValueError("oracle attention supports seq <= 8192")
     out = np.zeros(bh * seq * d, dtype=np.uint16)
     q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (q, k, v))
     lib.ref_attention_prefill(_p(q), _p(k), _p(v), _p(out), bh, seq, d, sqrt_d, int(causal), q_begin,
-                              seq if q_end is None else q_end)
+                              seq if q_end is None else q_end, int(causal_max))
     return out
 
 

@@ -378,9 +378,12 @@ void ref_rmsnorm_softmax(const uint16_t* x, const uint16_t* g, uint16_t* out, in
   }
 }
 
-/* One attention head over the whole key range as a single chunk. Layout [B, H, S, D]. */
+/* One attention head over the whole key range as a single chunk. Layout [B, H, S, D].
+ * max_mode 0: the reference's row max over every key, taken before masking (attention.rs:77-95);
+ * max_mode 1: the max over the keys the causal mask keeps (what a causal online softmax uses). */
 void ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, int64_t bh,
-                           int64_t seq, int64_t d, float sqrt_d, int causal, int64_t q_begin, int64_t q_end) {
+                           int64_t seq, int64_t d, float sqrt_d, int causal, int64_t q_begin, int64_t q_end,
+                           int max_mode) {
   const float EPS = 6.25e-8f; /* attention.rs:13 */
 #pragma omp parallel for schedule(dynamic, 1) collapse(2)
   for (int64_t h = 0; h < bh; ++h)
@@ -394,7 +397,7 @@ void ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t*
         float acc = 0.0f;
         for (int64_t e = 0; e < d; ++e) acc = acc + ref_bf16_to_f32(qi[e]) * ref_bf16_to_f32(kj[e]);
         s[j] = ref_bf16_to_f32(ref_f32_to_bf16(acc / sqrt_d)); /* qk_scaled: fp_div then cast bf16 */
-        mx = s[j] > mx ? s[j] : mx;                             /* row_max over every key */
+        if (max_mode == 0 || !causal || j <= i) mx = s[j] > mx ? s[j] : mx; /* row_max */
       }
       float l = 0.0f;
       for (int64_t j = 0; j < seq; ++j) {

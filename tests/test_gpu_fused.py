@@ -3,7 +3,19 @@
 Small shapes are compared whole against the oracle; the full config shapes are compared on a
 seeded sample of rows / queries the oracle finishes in seconds, plus properties that hold at any
 size (softmax rows sum to one, i32 accumulators exact, argmax bit-exact).
-Tolerance for bf16 outputs: |got - ref| <= 1e-2 |ref| + 1e-2 rms(ref).
+
+Tolerance for a single bf16 narrow after f32 accumulation: |got - ref| <= 1e-2 |ref| + 1e-2 rms(ref)
+(`close`). The RMSNorm->softmax and attention chains narrow to bf16 twice in sequence (y then the
+softmax output; o then o / l), and their f32 reductions are reassociated on the GPU -- which the
+emulator's own contract allows (BufStorage::reduce, storage/buf.rs:316-330) -- so an intermediate
+that differs in its last f32 bits can move the output by up to one bf16 ulp per narrow. Those
+chains use `close_chain`: per element max(1e-2 |ref| + 1e-2 rms(ref), 2 ulp_bf16(ref)), except a
+stated fraction of elements, which must still lie within 8 ulps. The exceptions have one known
+cause each: in RMSNorm a reassociated sum of squares can flip an intermediate bf16 y, and exp
+amplifies one y ulp by e^(|y| 2^-8); in attention the reference's max is taken over every key
+before masking (attention.rs:77-95) while the kernel keeps the causal running max, so bf16(p)
+rounds at a different scale. Against the oracle's causal-max mode the attention kernel is held to
+the plain 2-ulp bound.
 """
 import numpy as np
 import pytest
@@ -13,6 +25,36 @@ from oracle import emulator as emu
 from test_gpu_storage import close
 
 pytestmark = pytest.mark.gpu
+
+
+def bf16_ulp(v):
+    a = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 2.0 ** -126)))
+    return 2.0 ** (np.maximum(e, -126) - 7)
+
+
+def close_chain(got, ref, frac_beyond=0.0, hard_ulps=8, hard_abs=0.0):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    rms = np.sqrt(np.mean(ref ** 2)) if ref.size else 0.0
+    err = np.abs(got - ref)
+    base = 1e-2 * np.abs(ref) + 1e-2 * rms
+    ulp = bf16_ulp(ref)
+    beyond = err > np.maximum(base, 2 * ulp)
+    hard = err > np.maximum(np.maximum(base, hard_ulps * ulp), hard_abs)
+    assert not hard.any(), f"{hard.sum()} of {hard.size} beyond {hard_ulps} ulps; worst {err.max()}"
+    assert beyond.mean() <= frac_beyond, f"{beyond.sum()} of {beyond.size} beyond 2 ulps (allowed {frac_beyond})"
+    return float(beyond.mean())
+
+
+
+def P_SCALE_BOUND(v):
+    """Bound on |out_kernel - out_reference| from bf16(p) rounding at two different scales (each
+    P_j carries a relative error <= 2^-9, so out = sum P v / sum p moves by <= 2^-8 max|v|), plus
+    the two output roundings."""
+    vmax = float(np.max(np.abs(emu.bf16_to_f32(v))))
+    return 2.0 ** -8 * vmax + 2 * 2.0 ** -8 * vmax
+
 
 SQRT_HEAD_DIM = np.float32(11.313708)  # attention.rs:10
 
@@ -32,7 +74,7 @@ def test_rmsnorm_softmax_small(rt, shape):
     want = emu.rmsnorm_softmax(x, g, rows, cols, 1e-6)
     out = rt.alloc(rows * cols * 2)
     rt.rmsnorm_softmax(out, rt.upload(x), rt.upload(g), rows, cols, 1e-6)
-    close(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want))
+    close_chain(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want), frac_beyond=1e-4)
 
 
 def test_rmsnorm_softmax_config(rt):
@@ -46,7 +88,7 @@ def test_rmsnorm_softmax_config(rt):
     sample = rng.choice(rows, 48, replace=False)
     xs = x.reshape(rows, cols)[sample].reshape(-1)
     want = emu.bf16_to_f32(emu.rmsnorm_softmax(xs, g, len(sample), cols, 1e-6)).reshape(len(sample), cols)
-    close(y[sample], want)
+    close_chain(y[sample], want, frac_beyond=1e-4)
 
 
 # ---- attention prefill ------------------------------------------------------------------------------
@@ -60,9 +102,13 @@ def test_attention_small(rt, shape, causal):
     q, k, v = (bf16(rng, b * h * s * d) for _ in range(3))
     sd = np.float32(np.sqrt(d)) if d != 128 else SQRT_HEAD_DIM
     want = emu.attention_prefill(q, k, v, b * h, s, d, float(sd), causal)
+    want_cm = emu.attention_prefill(q, k, v, b * h, s, d, float(sd), causal, causal_max=True)
     out = rt.alloc(b * h * s * d * 2)
     rt.attention_prefill(out, rt.upload(q), rt.upload(k), rt.upload(v), b, h, s, d, float(sd), causal)
-    close(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want))
+    got = emu.bf16_to_f32(out.read(np.uint16))
+    close_chain(got, emu.bf16_to_f32(want_cm))  # same max: 2 ulps everywhere
+    # Reference max before masking: bf16(p) rounds at another scale, |d out| <= 2^-8 max|v| + 2 ulps.
+    close_chain(got, emu.bf16_to_f32(want), frac_beyond=1e-3, hard_abs=P_SCALE_BOUND(v))
 
 
 def test_attention_config_sampled(rt):
@@ -78,9 +124,10 @@ def test_attention_config_sampled(rt):
         sl = slice(hh * s * d, (hh + 1) * s * d)
         want = emu.attention_prefill(q[sl], k[sl], v[sl], 1, s, d, float(SQRT_HEAD_DIM), True, s - 64, s)
         w = emu.bf16_to_f32(want).reshape(s, d)[s - 64:]
-        close(got[hh, s - 64:], w)
+        bound = P_SCALE_BOUND(v[sl])
+        close_chain(got[hh, s - 64:], w, frac_beyond=1e-3, hard_abs=bound)
         want0 = emu.attention_prefill(q[sl], k[sl], v[sl], 1, s, d, float(SQRT_HEAD_DIM), True, 0, 64)
-        close(got[hh, :64], emu.bf16_to_f32(want0).reshape(s, d)[:64])
+        close_chain(got[hh, :64], emu.bf16_to_f32(want0).reshape(s, d)[:64], frac_beyond=1e-3, hard_abs=bound)
 
 
 # ---- W8A8 ------------------------------------------------------------------------------------------------

@@ -50,7 +50,7 @@ def run_transpose(rt, sizes, src_t, dst_t, dtype, npdt, seed=0, **kw):
 @pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16), (I32, np.int32)], ids=["i8", "bf16", "i32"])
 def test_transpose_pairs(rt, case, dt):
     sizes, a, b = case
-    run_transpose(rt, sizes, a, b, dt[0], dt[1])
+    run_transpose(rt, sizes, a, b, dt[0], dt[1], allow_broadcast=True)
 
 
 @pytest.mark.parametrize("case", SEQ_TABLES, ids=[c[2] for c in SEQ_TABLES])
@@ -252,7 +252,7 @@ def test_reduce(rt, case, dt, opname):
     got = out.read(t)
     live = mr.liveness(do)
     n_out = mr.size(do)
-    wave_path = n_out < 16384 and len(src) // max(n_out, 1) >= 64
+    wave_path = n_out < 16384 and len(src) // max(n_out, 1) >= 64 and dt != "bf16"
     if dt == "i32" or opname == "MAX" or not wave_path:
         assert np.array_equal(got[live].view(np.uint8), want[live].view(np.uint8))
     else:
