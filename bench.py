@@ -114,6 +114,24 @@ def bench_w8a8(fh, rt, steps, warmup, rng):
     return dict(ms=ev, wall_ms=wall, tops=op / (ev * 1e-3) / 1e12, op=op, bytes=M * K + N * K + N * 4 + M * N * 2)
 
 
+def bench_relayout(fh, rt, steps, warmup, rng):
+    """BufStorage::transpose at HBM scale: an identity relayout m![R, C] -> m![R, C] (a plain copy,
+    also the known-size calibration for the FETCH_SIZE / WRITE_SIZE counters) and a transpose
+    m![R, C] -> m![C, R], both 8192 x 8192 bf16 (128 MiB each way)."""
+    R = C = 8192
+    s = dict(R=R, C=C)
+    src = rt.upload(rng.integers(0, 65535, R * C, dtype=np.uint16))
+    dst = rt.alloc(R * C * 2)
+    rc, cr = fh.m("R, C", **s), fh.m("C, R", **s)
+    out = {}
+    for name, dv in (("copy", rc), ("transpose", cr)):
+        fn = lambda dv=dv: rt.transpose(dst, src, fh.BF16, rc, dv)
+        wall, ev = timed(rt, fn, steps, warmup)
+        nbytes = 2 * R * C * 2
+        out[name] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    return out
+
+
 def bench_mlp(fh, rt, steps, warmup, rng):
     B, I, Hd, O = 64, 784, 128, 10
     x = rt.upload(f32_to_bf16(rng.uniform(0, 1, B * I).astype(np.float32)))
@@ -169,7 +187,7 @@ def main():
     only = set(filter(None, args.only.split(",")))
     res = {}
     for name, fnb in (("gemm", bench_gemm), ("norm", bench_norm), ("attention", bench_attention),
-                      ("w8a8", bench_w8a8), ("mlp", bench_mlp)):
+                      ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout)):
         if only and name not in only:
             continue
         res[name] = fnb(fh, rt, args.steps, args.warmup, rng)
@@ -192,6 +210,10 @@ def main():
     if "mlp" in res:
         r = res["mlp"]
         configs["mlp_64x784x128x10"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)
+    if "relayout" in res:
+        for k, r in res["relayout"].items():
+            configs[f"relayout_{k}_8192x8192_bf16"] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"],
+                                                           roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     if g:
         configs["mapped_gemm_4096"] = dict(value=g["tflops"], unit="TFLOP/s", ms=g["ms"],
                                            roofline_frac=g["tflops"] / PEAK_BF16_TFLOPS)

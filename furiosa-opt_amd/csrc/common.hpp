@@ -17,22 +17,25 @@ namespace fo {
 FO_HD uint32_t f32_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
 FO_HD float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 
+// Both conversions are written as selects, not branches, so per-element use compiles to
+// v_cndmask instead of divergent exec-mask regions.
 // bf16 -> f32 (bf16_to_f32): NaN -> 0x7fc00000, subnormal (and zero) -> signed zero.
 FO_HD float bf16_to_f32(uint16_t h) {
-  uint32_t e = h & 0x7f80u, m = h & 0x007fu;
-  if (e == 0x7f80u && m) return bits_f32(0x7fc00000u);
-  if (e == 0) return bits_f32((uint32_t)(h & 0x8000u) << 16);
-  return bits_f32((uint32_t)h << 16);
+  uint32_t w = (uint32_t)h << 16;
+  uint32_t e = w & 0x7f800000u;
+  w = (e == 0) ? (w & 0x80000000u) : w;
+  w = ((w & 0x7fffffffu) > 0x7f800000u) ? 0x7fc00000u : w;
+  return bits_f32(w);
 }
 
 // f32 -> bf16 (f32_to_bf16): NaN -> 0x7fc0, subnormal -> signed zero, else round to nearest even
 // (half 2.7.1 bf16::from_f32).
 FO_HD uint16_t f32_to_bf16(float f) {
   uint32_t x = f32_bits(f);
-  if ((x & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  if ((x & 0x7f800000u) == 0) return (uint16_t)((x >> 16) & 0x8000u);
-  uint32_t lsb = (x >> 16) & 1u;
-  return (uint16_t)((x + 0x7fffu + lsb) >> 16);
+  uint32_t r = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+  r = ((x & 0x7f800000u) == 0) ? ((x >> 16) & 0x8000u) : r;
+  r = ((x & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
+  return (uint16_t)r;
 }
 
 // bf16 + bf16 as `half`'s arithmetic does it: widen exactly, add in f32, round to nearest even

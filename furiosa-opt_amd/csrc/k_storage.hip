@@ -115,9 +115,48 @@ __global__ void __launch_bounds__(256) k_relayout_tiled(T* __restrict__ dst, con
   }
 }
 
+// Chunked relayout: the innermost wheel is fully live and contiguous in src (stride 1) and every
+// 16-byte chunk of dst positions maps to 16 contiguous, aligned src bytes. One thread moves one
+// chunk; only the outer wheels' liveness can drop it.
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int v4i_t;
+template <int VEC>
+__global__ void __launch_bounds__(kBlock) k_relayout_chunks(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                            int64_t dst_base_b, int64_t src_base_b, int64_t eb,
+                                                            uint32_t nchunks, Wheels<1> w) {
+  for (uint32_t c = blockIdx.x * kBlock + threadIdx.x; c < nchunks; c += gridDim.x * kBlock) {
+    uint32_t q = c * VEC;
+    int64_t off = 0;
+    bool live = true;
+    for (int i = 0; i < w.n; ++i) {
+      uint32_t nq = w.div[i].div(q);
+      uint32_t d = q - nq * w.size[i];
+      live &= d < w.live[i];
+      off += (int64_t)d * w.stride[0][i];
+      q = nq;
+    }
+    if (live)
+      *(v4i_t*)(dst + dst_base_b + (int64_t)c * 16) = *(const v4i_t*)(src + src_base_b + off * eb);
+  }
+}
+
 template <typename T>
 void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int64_t src_base, int64_t count,
                 const Wheels<1>& w) {
+  // Chunked copy when the innermost dst wheel is src-contiguous and everything is 16-byte aligned.
+  constexpr int VEC = 16 / sizeof(T);
+  if (w.n >= 1 && w.stride[0][0] == 1 && w.live[0] == w.size[0] && w.size[0] % VEC == 0 && count % VEC == 0 &&
+      dst_base % VEC == 0 && src_base % VEC == 0 && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0) {
+    bool ok = true;
+    for (int i = 1; i < w.n; ++i) ok &= (w.stride[0][i] % VEC) == 0;
+    if (ok) {
+      int64_t nchunks = count / VEC;
+      hipLaunchKernelGGL(k_relayout_chunks<VEC>, dim3(grid_for(nchunks)), dim3(kBlock), 0, s, (uint8_t*)dst,
+                         (const uint8_t*)src, dst_base * (int64_t)sizeof(T), src_base * (int64_t)sizeof(T),
+                         (int64_t)sizeof(T), (uint32_t)nchunks, w);
+      FO_HIP(hipGetLastError());
+      return;
+    }
+  }
   // Tiled transpose when the innermost dst wheel is strided in src and another wheel is the
   // contiguous src run, both big enough to fill a tile, and the positions cover whole wheels.
   int jw = -1;
