@@ -95,6 +95,15 @@ FO_HD float sqrt_rn(float x) {
   return r;
 }
 
+// Correctly rounded a / r given y = RN(1/r) (Markstein's theorem: q = RN(a y) is within an ulp,
+// the remainder a - q r is exact under FMA, and one FMA correction rounds correctly). Valid for
+// normal operands and a normal, finite quotient.
+FO_HD float div_cr(float a, float r, float y) {
+  float q = a * y;
+  float e = __builtin_fmaf(-q, r, a);
+  return __builtin_fmaf(e, y, q);
+}
+
 // float_to_fixedpoint (float/mod.rs:22-34): round half away from zero (f64::round), clamp.
 FO_HD int32_t float_to_fixedpoint(float input, uint32_t int_width) {
   if (input != input) return (f32_bits(input) >> 31) ? INT32_MIN : INT32_MAX;

@@ -11,17 +11,18 @@
 // multiply-add, both within an f32 ulp of the reference's operation.
 //
 // MFMA layout. Each wave owns 32 queries. S^T = K Q^T is computed with v_mfma_f32_32x32x16_bf16
-// (A = K rows from LDS, B = Q fragments held in registers for the whole kernel), so the
+// (A = K rows from LDS, B = Q fragments held in registers for the whole tile), so the
 // accumulator gives every lane one query (lane % 32) and 16 keys per 32-key tile. Those registers
 // are exactly the B operand of O^T = V^T P^T once the MFMA's k slots are bound to the keys the
 // lane already holds (k order inside one MFMA is free as long as A and B agree): no shuffle of P
 // through LDS. V is stored transposed in LDS with the keys of each 16-key group permuted so that
 // every A fragment of the PV product is one 16-byte read.
 //
-// Pipeline. K and V tiles are double-buffered in LDS: the global loads for block j+1 are issued
-// into registers before block j's MFMAs and written to the other LDS buffer after them, so one
-// barrier per 64-key block suffices. Blocks entirely below the diagonal skip the mask; the O
-// rescale is skipped when no query's running max moved.
+// Pipeline. K and V tiles are double-buffered in LDS with K one 64-key block ahead of V: while
+// the softmax of block j runs on the VALU, the MFMAs of S(j+1) are independent of it and issue
+// alongside; then block j's PV. Global loads for the next blocks are issued into registers
+// before a step and written to LDS after it, so one barrier per block suffices. Blocks below
+// the last two are fully visible to every query of the workgroup and run without mask code.
 #include <hip/hip_runtime.h>
 
 #include "runtime.hpp"
@@ -59,25 +60,23 @@ struct AttnCfg {
   static constexpr int KBYTES = kBN * KROW;
   static constexpr int STAGE = KBYTES + D * VROW;
   static constexpr int LDS = 2 * STAGE;
-  static constexpr int CH = D / 8;                        // 16-byte chunks per row
-  static constexpr int KL = kBN * CH / 256;               // K chunks per thread
-  static constexpr int VG = kBN / 4 * CH;                 // (4-key group, chunk) pairs per block
-  static constexpr int VL = (VG + 255) / 256;             // such pairs per thread
-  static constexpr int KS = D / 16;                       // k-steps of the QK^T contraction
-  static constexpr int DT = D / 32;                       // 32-row d tiles of O^T
+  static constexpr int CH = D / 8;             // 16-byte chunks per row
+  static constexpr int KL = kBN * CH / 256;    // K chunks per thread
+  static constexpr int VG = kBN / 4 * CH;      // (4-key group, chunk) pairs per block
+  static constexpr int VL = (VG + 255) / 256;  // such pairs per thread
+  static constexpr int KS = D / 16;            // k-steps of the QK^T contraction
+  static constexpr int DT = D / 32;            // 32-row d tiles of O^T
 };
 
 // Position of key `kk` (within a block) in a V^T row: inside each 16-key group, key 8h + 4g + i
 // sits at 8g + 4h + i, so lane group g's two 4-key runs of a PV fragment are adjacent.
 __device__ __forceinline__ int vt_pos(int kk) { return (kk & ~15) + ((kk & 4) << 1) + ((kk & 8) >> 1) + (kk & 3); }
 
-template <int D, bool MASK>
-__device__ __forceinline__ void attn_block(const uint8_t* __restrict__ sK, const uint8_t* __restrict__ sVt,
-                                           const i32x4_t (&qf)[AttnCfg<D>::KS], f32x16_t (&o)[AttnCfg<D>::DT],
-                                           float& m_run, float& l_part, int kv0, int myq, int seq, int causal,
-                                           float inv_sd, int g, int col) {
+// S^T tile pair for the 64 keys of one K buffer: keys kt*32 + 8*(r/4) + 4g + r%4 of s[kt][r].
+template <int D>
+__device__ __forceinline__ void qk(const uint8_t* __restrict__ sK, const i32x4_t (&qf)[AttnCfg<D>::KS],
+                                   f32x16_t (&s)[2], int g, int col) {
   using C = AttnCfg<D>;
-  f32x16_t s[2];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
@@ -88,30 +87,43 @@ __device__ __forceinline__ void attn_block(const uint8_t* __restrict__ sK, const
       s[kt] = mma(kf, qf[ks], s[kt]);
     }
   }
-  // Logits: scale, round to bf16 (the reference's qk_scaled narrow), mask, block max.
+}
+
+// One pipelined step: S of the next block (from sKn) is computed while the softmax of the
+// current block's S (sc) runs, then the current block's PV product; sc becomes the next S.
+template <int D, bool MASK>
+__device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const uint8_t* __restrict__ sVt,
+                                          const i32x4_t (&qf)[AttnCfg<D>::KS], f32x16_t (&o)[AttnCfg<D>::DT],
+                                          f32x16_t (&sc)[2], float& m_run, float& l_part, int kv0, int myq,
+                                          int seq, int causal, float inv_sd, int g, int col) {
+  using C = AttnCfg<D>;
+  f32x16_t sn[2];
+  qk<D>(sKn, qf, sn, g, col);
+  // Block max on the raw sums (scale and bf16 rounding are monotonic, so max commutes with
+  // them), then logits: scale, round to bf16 (the reference's qk_scaled narrow).
   float bmax = -INFINITY;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int kt = 0; kt < 2; ++kt) {
+    if (MASK) {
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) {
-      uint32_t w = pack_bf16(s[kt][r] * inv_sd, s[kt][r + 1] * inv_sd);
-      float x0 = __builtin_bit_cast(float, w << 16), x1 = __builtin_bit_cast(float, w & 0xffff0000u);
-      if (MASK) {
+      for (int r = 0; r < 16; ++r) {
         int key = kv0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        x0 = (key >= seq || (causal && key > myq)) ? -INFINITY : x0;
-        x1 = (key + 1 >= seq || (causal && key + 1 > myq)) ? -INFINITY : x1;
+        sc[kt][r] = (key >= seq || (causal && key > myq)) ? -INFINITY : sc[kt][r];
       }
-      s[kt][r] = x0;
-      s[kt][r + 1] = x1;
-      bmax = fmaxf(bmax, fmaxf(x0, x1));
     }
-  bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-  const float m_new = fmaxf(m_run, bmax);
-  const float ms = (m_new == -INFINITY) ? 0.f : m_new * kL2E;  // all-masked so far: keep p = 0, no NaN
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(sc[kt][r], sc[kt][r + 1]));
+  }
+  bmax = __builtin_fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+  bmax = __builtin_bit_cast(float, pack_bf16(bmax * inv_sd, 0.f) << 16);
+  // Online softmax step. Every query of a processed block sees key 0 of the first block, so
+  // m_new is finite from the first block on; alpha is 0 there (m_run = -inf).
+  const float m_new = __builtin_fmaxf(m_run, bmax);
+  const float ms = m_new * kL2E;
   const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kL2E, -ms));
   m_run = m_new;
   // p = exp(x - m) as f32 for the sum, bf16 pairs for the PV operand. Chunk c = (kt = c/2,
-  // h = c%2) holds s[kt][8h .. 8h+7].
+  // h = c%2) holds sc[kt][8h .. 8h+7].
   float psum = 0.f;
   i32x4_t pf[4];
 #pragma unroll
@@ -120,18 +132,19 @@ __device__ __forceinline__ void attn_block(const uint8_t* __restrict__ sK, const
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * h + 2 * e], kL2E, -ms));
-        float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][8 * h + 2 * e + 1], kL2E, -ms));
+        const int r = 8 * h + 2 * e;
+        uint32_t w = pack_bf16(sc[kt][r] * inv_sd, sc[kt][r + 1] * inv_sd);
+        float x0 = __builtin_bit_cast(float, w << 16), x1 = __builtin_bit_cast(float, w & 0xffff0000u);
+        float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, kL2E, -ms));
+        float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, kL2E, -ms));
         psum += p0 + p1;
         pf[kt * 2 + h][e] = (int)pack_bf16(p0, p1);
       }
   l_part = l_part * alpha + psum;
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {  // wave-uniform: some query's max moved
 #pragma unroll
-    for (int t = 0; t < C::DT; ++t)
+  for (int t = 0; t < C::DT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
-  }
+    for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
   // O^T += V^T P^T. Chunk c covers keys base = 32*(c/2) + 16*(c%2); lane group g binds k slots to
   // keys {base + 4g + 0..3, base + 8 + 4g + 0..3}, stored adjacently at base + 8g.
 #pragma unroll
@@ -143,6 +156,8 @@ __device__ __forceinline__ void attn_block(const uint8_t* __restrict__ sK, const
       o[t] = mma(vf, pf[c], o[t]);
     }
   }
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) sc[kt] = sn[kt];
 }
 
 template <int D>
@@ -156,7 +171,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   const int bid = blockIdx.x;
   const int qb = nqb - 1 - bid / heads_total;  // heaviest (latest) query blocks first
   const int64_t head = bid % heads_total;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave: scalar branches
   const int g = lane >> 5, col = lane & 31;
   const int q0 = qb * kBM;
   const int q0w = q0 + wave * 32;
@@ -165,48 +181,44 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   const uint16_t* Qh = q + head * (int64_t)seq * D;
   const uint16_t* Kh = k + head * (int64_t)seq * D;
   const uint16_t* Vh = v + head * (int64_t)seq * D;
-
-  // Q fragments (B operand of S^T): lane holds query myq, d in [16*ks + 8*g, +8).
-  i32x4_t qf[C::KS];
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    if (myq < seq)
-      qf[ks] = *(const i32x4_t*)(Qh + (int64_t)myq * D + ks * 16 + g * 8);
-    else
-      qf[ks] = i32x4_t{0, 0, 0, 0};
-  }
+  // Buffer loads bounded to the head's seq rows: rows past the end read as zero, so the tail
+  // block and the queries past the end need no guards.
+  const uint32_t head_bytes = (uint32_t)seq * D * 2;
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)Qh, (short)0, (int)head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)Kh, (short)0, (int)head_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)Vh, (short)0, (int)head_bytes, 0x00020000);
 
   // Tile loaders. K: chunk c -> row c / CH, 16-byte column c % CH. V: pair p -> 4-key group
   // p % 16, column p / 16 (consecutive lanes take consecutive key groups, which keeps the
   // transposed 8-byte LDS writes of one instruction on distinct banks).
+  const uint32_t koff = (uint32_t)(((tid / C::CH) * D + (tid % C::CH) * 8) * 2);
+  const uint32_t voff = (uint32_t)((((tid % (kBN / 4)) * 4) * D + (tid / (kBN / 4)) * 8) * 2);
   i32x4_t kreg[C::KL];
   i32x4_t vreg[C::VL][4];
-  auto load = [&](int kv0) {
+  auto load_k = [&](int kv0) {
 #pragma unroll
-    for (int i = 0; i < C::KL; ++i) {
-      int c = tid + i * 256, r = c / C::CH, cc = c % C::CH;
-      kreg[i] = (kv0 + r < seq) ? *(const i32x4_t*)(Kh + (int64_t)(kv0 + r) * D + cc * 8) : i32x4_t{0, 0, 0, 0};
-    }
+    for (int i = 0; i < C::KL; ++i)
+      kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff, kv0 * D * 2 + i * (256 / C::CH) * D * 2, 0);
+  };
+  auto load_v = [&](int kv0) {
 #pragma unroll
     for (int i = 0; i < C::VL; ++i) {
-      int p = tid + i * 256;
-      if (C::VG % 256 != 0 && p >= C::VG) break;
-      int kg = p % (kBN / 4), cc = p / (kBN / 4);
+      if (C::VG % 256 != 0 && tid + i * 256 >= C::VG) break;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int key = kv0 + kg * 4 + j;
-        vreg[i][j] = (key < seq) ? *(const i32x4_t*)(Vh + (int64_t)key * D + cc * 8) : i32x4_t{0, 0, 0, 0};
-      }
+      for (int j = 0; j < 4; ++j)
+        vreg[i][j] = __builtin_amdgcn_raw_buffer_load_b128(rv, voff + j * D * 2, kv0 * D * 2 + i * 256 / (kBN / 4) * 16, 0);
     }
   };
-  auto store = [&](int buf) {
+  auto store_k = [&](int buf) {
     uint8_t* sK = lds + buf * C::STAGE;
-    uint8_t* sVt = sK + C::KBYTES;
 #pragma unroll
     for (int i = 0; i < C::KL; ++i) {
       int c = tid + i * 256, r = c / C::CH, cc = c % C::CH;
       *(i32x4_t*)(sK + r * C::KROW + cc * 16) = kreg[i];
     }
+  };
+  auto store_v = [&](int buf) {
+    uint8_t* sVt = lds + buf * C::STAGE + C::KBYTES;
 #pragma unroll
     for (int i = 0; i < C::VL; ++i) {
       int p = tid + i * 256;
@@ -218,18 +230,28 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
         // d = cc*8 + e: keys 4kg .. 4kg+3 of that column, as two packed pairs.
         uint32_t a0 = (uint32_t)vreg[i][0][e >> 1], a1 = (uint32_t)vreg[i][1][e >> 1];
         uint32_t a2 = (uint32_t)vreg[i][2][e >> 1], a3 = (uint32_t)vreg[i][3][e >> 1];
-        uint32_t w0, w1;
-        if (e & 1) {
-          w0 = (a0 >> 16) | (a1 & 0xffff0000u);
-          w1 = (a2 >> 16) | (a3 & 0xffff0000u);
-        } else {
-          w0 = (a0 & 0xffffu) | (a1 << 16);
-          w1 = (a2 & 0xffffu) | (a3 << 16);
-        }
+        // v_perm_b32 byte select over {hi = a1, lo = a0}: low halves 0x05040100, high 0x07060302.
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        uint32_t w0 = __builtin_amdgcn_perm(a1, a0, sel);
+        uint32_t w1 = __builtin_amdgcn_perm(a3, a2, sel);
         *(i32x2_t*)(sVt + (cc * 8 + e) * C::VROW + pos * 2) = i32x2_t{(int)w0, (int)w1};
       }
     }
   };
+  auto sK_of = [&](int buf) { return (const uint8_t*)(lds + buf * C::STAGE); };
+  auto sVt_of = [&](int buf) { return (const uint8_t*)(lds + buf * C::STAGE + C::KBYTES); };
+
+  // Prologue: Q fragments (B operand of S^T: lane holds query myq, d in [16*ks + 8*g, +8)), K(0)
+  // and V(0) are requested together; K(1) is in flight while S(0) is computed.
+  i32x4_t qf[C::KS];
+  const uint32_t qoff = (uint32_t)(myq * D + g * 8) * 2;
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) qf[ks] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, ks * 32, 0);
+  load_k(0);
+  load_v(0);
+  store_k(0);
+  store_v(0);
+  load_k(kBN);
 
   f32x16_t o[C::DT];
 #pragma unroll
@@ -238,46 +260,62 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
   float m_run = -INFINITY, l_part = 0.f;
 
+  // Buffers: K(j) and V(j) live in buffer j % 2. Step j reads K(j+1) and V(j), then refills K
+  // buffer j % 2 with K(j+2) (K(j) was consumed by step j-1) and V buffer (j+1) % 2 with V(j+1).
+  // Loads past the head's end read zeros, so every step loads and stores unconditionally.
   const int kv_end = causal ? min(seq, q0 + kBM) : seq;
   const int nblk = (kv_end + kBN - 1) / kBN;
-  load(0);
-  store(0);
   __syncthreads();
-  for (int j = 0; j < nblk; ++j) {
+  f32x16_t sc[2];
+  qk<D>(sK_of(0), qf, sc, g, col);
+  store_k(1);
+  __syncthreads();  // K(1) visible, and every wave is done reading K buffer 0
+  const int nmain = nblk > 2 ? nblk - 2 : 0;
+  int j = 0;
+  for (; j < nmain; ++j) {
     const int kv0 = j * kBN;
-    const bool more = j + 1 < nblk;
-    if (more) load(kv0 + kBN);
-    const uint8_t* sK = lds + (j & 1) * C::STAGE;
-    const uint8_t* sVt = sK + C::KBYTES;
-    if (!(causal && kv0 > q0w + 31)) {  // wave-uniform: some of this wave's queries see these keys
-      const bool need_mask = (causal && kv0 + kBN - 1 > q0w) || kv0 + kBN > seq;
-      if (need_mask)
-        attn_block<D, true>(sK, sVt, qf, o, m_run, l_part, kv0, myq, seq, causal, inv_sd, g, col);
-      else
-        attn_block<D, false>(sK, sVt, qf, o, m_run, l_part, kv0, myq, seq, causal, inv_sd, g, col);
-    }
-    if (more) store((j + 1) & 1);
+    load_k(kv0 + 2 * kBN);
+    load_v(kv0 + kBN);
+    attn_step<D, false>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, myq, seq, causal, inv_sd,
+                        g, col);
+    store_k(j & 1);
+    store_v((j + 1) & 1);
+    __syncthreads();
+  }
+  // The last two blocks hold the causal diagonal and the sequence tail: masked, and skipped by
+  // waves whose queries all precede them.
+  for (; j < nblk; ++j) {
+    const int kv0 = j * kBN;
+    load_k(kv0 + 2 * kBN);
+    load_v(kv0 + kBN);
+    if (!(causal && kv0 > q0w + 31))  // wave-uniform
+      attn_step<D, true>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, myq, seq, causal, inv_sd,
+                         g, col);
+    store_k(j & 1);
+    store_v((j + 1) & 1);
     __syncthreads();
   }
 
-  // out[myq][d] = bf16( bf16(o) / (l + EPS) ); lane holds d = 32t + 8*(r/4) + 4g + r%4.
+  // out[myq][d] = bf16( bf16(o) / (l + EPS) ); lane holds d = 32t + 8*(r/4) + 4g + r%4. The
+  // quotient is correctly rounded (l >= 1, so it is finite and the divisor normal).
   const float l_run = l_part + __shfl_xor(l_part, 32, 64);
   if (myq < seq) {
     const float denom = l_run + kEps;
+    const float rinv = __fdiv_rn(1.0f, denom);
     uint16_t* orow = out + head * (int64_t)seq * D + (int64_t)myq * D;
 #pragma unroll
     for (int t = 0; t < C::DT; ++t)
 #pragma unroll
       for (int blk = 0; blk < 4; ++blk) {
-        i32x2_t w;
+        i32x2_t wv;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           float a = bf16_to_f32(f32_to_bf16(o[t][blk * 4 + 2 * e]));
           float b = bf16_to_f32(f32_to_bf16(o[t][blk * 4 + 2 * e + 1]));
-          uint32_t lo = f32_to_bf16(__fdiv_rn(a, denom)), hi = f32_to_bf16(__fdiv_rn(b, denom));
-          w[e] = (int)(lo | (hi << 16));
+          uint32_t lo = f32_to_bf16(div_cr(a, denom, rinv)), hi = f32_to_bf16(div_cr(b, denom, rinv));
+          wv[e] = (int)(lo | (hi << 16));
         }
-        *(i32x2_t*)(orow + t * 32 + 8 * blk + 4 * g) = w;
+        *(i32x2_t*)(orow + t * 32 + 8 * blk + 4 * g) = wv;
       }
   }
 }
@@ -302,7 +340,7 @@ void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, c
   require(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0, "attention: buffers not aligned");
   int64_t ht = batch * heads;
   int64_t nqb = (seq + kBM - 1) / kBM;
-  require(ht * nqb < (1ll << 31) && seq < (1ll << 30), "attention: shape too large");
+  require(ht * nqb < (1ll << 31) && (seq + 2 * kBN) * head_dim * 2 < (1ll << 31), "attention: shape too large");
   dim3 grid((unsigned)(ht * nqb));
   const float inv_sd = 1.0f / sqrt_d;
   if (head_dim == 128)

@@ -55,13 +55,6 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// Correctly rounded a / r given y = RN(1/r) (Markstein): valid for normal operands and results.
-__device__ __forceinline__ float div_cr(float a, float r, float y) {
-  float q = a * y;
-  float e = __builtin_fmaf(-q, r, a);
-  return __builtin_fmaf(e, y, q);
-}
-
 // The exact per-element path (reference rules at every rounding point), for rows holding a
 // non-finite value. Reads the row again from global memory.
 __device__ void row_exact(uint16_t* __restrict__ orow, const uint16_t* __restrict__ xr,
