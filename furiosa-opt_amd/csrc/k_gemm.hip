@@ -5,12 +5,17 @@
 //
 // Tiling (gfx950, wave64): a block of WM x WN waves owns a BM x BN tile; each wave owns
 // (BM/WM) x (BN/WN) as a grid of 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 /
-// v_mfma_i32_32x32x32_i8). K advances 128 bytes per stage. Stages are double-buffered in LDS with
-// the next stage's global loads in flight during the current stage's MFMAs, and the LDS fragments
-// of the next 32-byte k-step are read while the current k-step's MFMAs issue. LDS rows are padded
-// by 16 bytes: a 16-byte fragment read by 32 lanes at stride 144 B covers all 64 banks once per
-// 16 lanes. Blocks are ordered XCD-aware so the tiles that share A rows / B columns run on the same
-// XCD's L2. Row-major bf16 / i8 results are restaged through LDS and written as 16-byte rows.
+// v_mfma_i32_32x32x32_i8). K advances 128 bytes per stage; stages are double-buffered in LDS.
+//
+// Operand staging: global -> LDS by buffer_load_dwordx4 ... lds (LDS DMA: each lane's 16 bytes
+// land at the wave's LDS base + 16 * lane, no VGPR round trip and no ds_write). A wave's
+// 1 KiB DMA covers 8 rows of 128 bytes; the lane -> (row, chunk) assignment stores chunk c of row r
+// at slot c ^ ((r >> 1) & 7), so the 16 lanes of one 16-byte fragment read (16 consecutive rows,
+// one chunk) touch 16 distinct 16-byte bank groups. Rows past the operand's extent read as zero
+// (buffer range check); chunks past K are pointed outside the range for the same effect.
+//
+// Epilogue: the MFMA operands are swapped (B fragments as the A operand) so each lane holds four
+// consecutive output columns of one row, stored directly to global memory.
 //
 // Within one MFMA the hardware's k order is irrelevant: A and B fragments are loaded with the same
 // k -> (lane, element) map, and the sum over k is order-free up to f32 rounding (exact for i32).
@@ -25,9 +30,9 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16_t;
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2_t;
 
 constexpr int kBKB = 128;         // K bytes per stage
-constexpr int kRowB = kBKB + 16;  // padded LDS row stride in bytes
 
 template <bool IS_I8>
 struct MfmaT;
@@ -99,22 +104,35 @@ __device__ __forceinline__ typename OutT<OUT>::T convert_out(typename MfmaT<IS_I
   }
 }
 
+// LDS address space pointer for the DMA builtin.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Values the compiler cannot prove wave-uniform (it otherwise builds the buffer descriptor in
+// VGPRs and wraps every DMA in a readfirstlane loop); they are uniform by construction.
+__device__ __forceinline__ void* uniform_ptr(const void* p) {
+  uint64_t v = (uint64_t)p;
+  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (void*)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int uniform_i32(int64_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
+
 template <bool IS_I8, int OUT, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   using M = MfmaT<IS_I8>;
   using acc_t = typename M::acc_t;
   using out_t = typename OutT<OUT>::T;
-  constexpr int NT = 64 * WM * WN;
-  constexpr int EB = IS_I8 ? 1 : 2;  // element bytes
+  constexpr int W = WM * WN;
+  constexpr int EB = IS_I8 ? 1 : 2;            // element bytes
   constexpr int TWM = BM / WM, TWN = BN / WN;  // wave tile
   constexpr int TM = TWM / 32, TN = TWN / 32;
-  constexpr int A_LOADS = BM * kBKB / 16 / NT;  // 16-byte loads per thread per stage
-  constexpr int B_LOADS = BN * kBKB / 16 / NT;
-  static_assert(A_LOADS * NT * 16 == BM * kBKB && B_LOADS * NT * 16 == BN * kBKB, "tile/threads mismatch");
+  constexpr int A_CH = BM / 8 / W;  // 1 KiB DMA chunks (8 rows) of A per wave per stage
+  constexpr int B_CH = BN / 8 / W;
+  static_assert(A_CH * 8 * W == BM && B_CH * 8 * W == BN, "tile/waves mismatch");
+  constexpr int STAGE = (BM + BN) * kBKB;
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  auto sA = [&](int buf) { return smem + buf * (BM * kRowB); };
-  auto sB = [&](int buf) { return smem + 2 * BM * kRowB + buf * (BN * kRowB); };
+  auto sA = [&](int buf) { return smem + buf * STAGE; };
+  auto sB = [&](int buf) { return smem + buf * STAGE + BM * kBKB; };
 
   // Tile order: consecutive block ids go round-robin over the 8 XCDs; regroup so each XCD walks a
   // contiguous range of tiles, ordered in groups of 8 tile-rows so neighbours share operands in L2.
@@ -132,62 +150,51 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   const int batch = blockIdx.y;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WN, wn = wave % WN;
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t KB = g.K * EB;  // K in bytes
+  const uint32_t KB = (uint32_t)(g.K * EB);  // K in bytes
 
-  const uint8_t* A = g.a + (g.a_batch * batch) * EB;
-  const uint8_t* B = g.b + (g.b_batch * batch) * EB;
+  // Buffer resources based at the tile's first row, extent = the bytes its valid rows span.
+  const int64_t rows_a = min((int64_t)BM, g.M - m0), rows_b = min((int64_t)BN, g.N - n0);
+  const uint8_t* Abase = g.a + (g.a_batch * batch + m0 * g.lda) * EB;
+  const uint8_t* Bbase = g.b + (g.b_batch * batch + n0 * g.ldb) * EB;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Abase), (short)0, uniform_i32((rows_a - 1) * g.lda * EB + KB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Bbase), (short)0, uniform_i32((rows_b - 1) * g.ldb * EB + KB), 0x00020000);
 
-  // Global load assignment: chunk c = tid + i*NT is row c/8, byte column (c%8)*16. Interior tiles
-  // (the whole BM x BN block in range and K a whole number of stages) load without bounds checks;
-  // the test is uniform over the block, so edge tiles take the checked path without divergence.
-  const bool interior = (m0 + BM <= g.M) && (n0 + BN <= g.N) && (KB % kBKB == 0);
-  i32x4_t ra[A_LOADS], rb[B_LOADS];
-  const uint8_t* a_base[A_LOADS];
-  const uint8_t* b_base[B_LOADS];
+  // DMA source offsets: lane l of chunk q fills LDS slot l % 8 of tile row r = 8q + l / 8 with
+  // global chunk (l % 8) ^ ((r >> 1) & 7) of that row.
+  uint32_t a_off[A_CH], a_kc[A_CH], b_off[B_CH], b_kc[B_CH];
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) {
-    int c = tid + i * NT;
-    a_base[i] = A + ((m0 + (c >> 3)) * g.lda) * EB + (c & 7) * 16;
+  for (int i = 0; i < A_CH; ++i) {
+    int r = 8 * (wave * A_CH + i) + (lane >> 3);
+    int c = (lane & 7) ^ ((r >> 1) & 7);
+    a_kc[i] = (uint32_t)c * 16;
+    a_off[i] = (uint32_t)(r * g.lda * EB) + a_kc[i];
   }
 #pragma unroll
-  for (int i = 0; i < B_LOADS; ++i) {
-    int c = tid + i * NT;
-    b_base[i] = B + ((n0 + (c >> 3)) * g.ldb) * EB + (c & 7) * 16;
+  for (int i = 0; i < B_CH; ++i) {
+    int r = 8 * (wave * B_CH + i) + (lane >> 3);
+    int c = (lane & 7) ^ ((r >> 1) & 7);
+    b_kc[i] = (uint32_t)c * 16;
+    b_off[i] = (uint32_t)(r * g.ldb * EB) + b_kc[i];
   }
-  auto load_stage = [&](int64_t kb) {
-    if (interior) {
+  auto issue = [&](uint32_t kb, int buf) {
+    const bool tail = kb + kBKB > KB;  // uniform: the last, partial stage
 #pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) ra[i] = *(const i32x4_t*)(a_base[i] + kb);
-#pragma unroll
-      for (int i = 0; i < B_LOADS; ++i) rb[i] = *(const i32x4_t*)(b_base[i] + kb);
-    } else {
-#pragma unroll
-      for (int i = 0; i < A_LOADS; ++i) {
-        int c = tid + i * NT;
-        bool ok = (m0 + (c >> 3) < g.M) && (kb + (c & 7) * 16 < KB);
-        ra[i] = ok ? *(const i32x4_t*)(a_base[i] + kb) : i32x4_t{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int i = 0; i < B_LOADS; ++i) {
-        int c = tid + i * NT;
-        bool ok = (n0 + (c >> 3) < g.N) && (kb + (c & 7) * 16 < KB);
-        rb[i] = ok ? *(const i32x4_t*)(b_base[i] + kb) : i32x4_t{0, 0, 0, 0};
-      }
-    }
-  };
-  auto store_stage = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      int c = tid + i * NT;
-      *(i32x4_t*)(sA(buf) + (c >> 3) * kRowB + (c & 7) * 16) = ra[i];
+    for (int i = 0; i < A_CH; ++i) {
+      uint32_t off = a_off[i] + kb;
+      if (tail && kb + a_kc[i] >= KB) off = 0x80000000u;  // past K: out of range, reads zero
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(sA(buf) + (wave * A_CH + i) * 1024), 16, off, 0, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-      int c = tid + i * NT;
-      *(i32x4_t*)(sB(buf) + (c >> 3) * kRowB + (c & 7) * 16) = rb[i];
+    for (int i = 0; i < B_CH; ++i) {
+      uint32_t off = b_off[i] + kb;
+      if (tail && kb + b_kc[i] >= KB) off = 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(sB(buf) + (wave * B_CH + i) * 1024), 16, off, 0, 0, 0);
     }
   };
 
@@ -199,103 +206,103 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-  const int frow = lane & 31;         // fragment row within a 32-row tile
-  const int fcol = (lane >> 5) * 16;  // this lane's 16 bytes within a 32-byte k-step
-  const int arow0 = wm * TWM + frow, brow0 = wn * TWN + frow;
+  // Fragment reads: lane (frow, half) takes 16 bytes of k-step kk at chunk 2kk + half of row
+  // frow (+ 32i), found at slot (2kk + half) ^ swz; rows of a fragment tile start at multiples
+  // of 32, so swz depends on frow only.
+  const int frow = lane & 31, half = lane >> 5;
+  const int swz = (frow >> 1) & 7;
+  const int a_row = (wm * TWM + frow) * kBKB, b_row = (wn * TWN + frow) * kBKB;
+  auto slot = [&](int kk) { return ((2 * kk + half) ^ swz) * 16; };
 
-  // Pipeline: at the top of iteration s, LDS buffer (s & 1) holds stage s and the registers hold
-  // stage s + 1. The iteration reads its first fragments, writes stage s + 1 into the other buffer
-  // (last read in iteration s - 1, fenced by that iteration's barrier), issues the global loads of
-  // stage s + 2, and runs stage s's MFMAs with the next k-step's fragments read ahead.
   const int nst = (int)((KB + kBKB - 1) / kBKB);
-  load_stage(0);
-  store_stage(0);
-  if (nst > 1) load_stage(kBKB);
-  __syncthreads();
-
+  issue(0, 0);
   for (int s = 0; s < nst; ++s) {
     const int cur = s & 1;
+    // Stage s has landed (this wave's DMA), and after the barrier every wave's has; every wave is
+    // also done reading stage s - 1, whose buffer the next DMA overwrites.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (s + 1 < nst) issue((uint32_t)(s + 1) * kBKB, cur ^ 1);
     const uint8_t* a_s = sA(cur);
     const uint8_t* b_s = sB(cur);
     i32x4_t fa[2][TM], fb[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) fa[0][i] = *(const i32x4_t*)(a_s + (arow0 + i * 32) * kRowB + fcol);
+    for (int i = 0; i < TM; ++i) fa[0][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kBKB + slot(0));
 #pragma unroll
-    for (int j = 0; j < TN; ++j) fb[0][j] = *(const i32x4_t*)(b_s + (brow0 + j * 32) * kRowB + fcol);
-    if (s + 1 < nst) {
-      store_stage(cur ^ 1);
-      if (s + 2 < nst) load_stage((int64_t)(s + 2) * kBKB);
-    }
+    for (int j = 0; j < TN; ++j) fb[0][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kBKB + slot(0));
 #pragma unroll
     for (int kk = 0; kk < kBKB / 32; ++kk) {
       const int p = kk & 1;
       if (kk + 1 < kBKB / 32) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          fa[p ^ 1][i] = *(const i32x4_t*)(a_s + (arow0 + i * 32) * kRowB + (kk + 1) * 32 + fcol);
+        for (int i = 0; i < TM; ++i) fa[p ^ 1][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kBKB + slot(kk + 1));
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          fb[p ^ 1][j] = *(const i32x4_t*)(b_s + (brow0 + j * 32) * kRowB + (kk + 1) * 32 + fcol);
+        for (int j = 0; j < TN; ++j) fb[p ^ 1][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kBKB + slot(kk + 1));
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(fa[p][i], fb[p][j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(fb[p][j], fa[p][i], acc[i][j]);
     }
-    __syncthreads();
   }
 
-  // Epilogue. Accumulator layout of a 32x32 tile: lane holds column (lane % 32), rows
-  // 8*(v/4) + 4*(lane/32) + v%4 for v in [0, 16).
+  // Epilogue. With B as the MFMA's A operand, lane holds row m = 32i + (lane % 32) of the wave
+  // tile and columns n = 32j + 8*(v/4) + 4*(lane/32) + v%4: four consecutive columns per v / 4.
   const int64_t cb = g.c_batch * batch;
-  const bool full_tile = (m0 + BM <= g.M) && (n0 + BN <= g.N);
+  out_t* C = (out_t*)g.c;
   constexpr int OB = (int)sizeof(out_t);
-  constexpr int CROW = BN * OB + 16;  // padded LDS row of the staged C tile
-  if (OUT != 4 && full_tile && g.ldc_n == 1 && (g.ldc_m * OB) % 16 == 0 && (g.c_batch * OB) % 16 == 0 &&
-      BM * CROW <= 2 * (BM + BN) * kRowB && ((uintptr_t)g.c % 16) == 0) {
-    // Stage the tile in LDS, then write 16-byte rows.
-    uint8_t* sc = smem;
+  const bool vec = g.ldc_n == 1 && (g.ldc_m * OB) % (4 * OB) == 0 && (cb * OB) % (4 * OB) == 0 &&
+                   ((uintptr_t)g.c % (4 * OB)) == 0 && (OUT != 4 || ((uintptr_t)g.scale % 16) == 0);
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    const int64_t row = m0 + wm * TWM + i * 32 + frow;
+    if (row >= g.M) continue;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        int col = wn * TWN + j * 32 + (lane & 31);
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          int row = wm * TWM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          *(out_t*)(sc + row * CROW + col * OB) = convert_out<IS_I8, OUT>(acc[i][j], v, 0.f);
+      for (int vg = 0; vg < 4; ++vg) {
+        const int64_t col = n0 + wn * TWN + j * 32 + 8 * vg + 4 * half;
+        float sc[4] = {0.f, 0.f, 0.f, 0.f};
+        if (vec && col + 3 < g.N) {
+          if constexpr (OUT == 4) {
+            typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+            f32x4_t s4 = *(const f32x4_t*)(g.scale + col);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[e] = s4[e];
+          }
+          out_t o4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o4[e] = convert_out<IS_I8, OUT>(acc[i][j], vg * 4 + e, sc[e]);
+          int64_t off = cb + row * g.ldc_m + col;
+          if constexpr (OB == 1) {
+            *(uint32_t*)(C + off) = __builtin_bit_cast(uint32_t, o4);
+          } else if constexpr (OB == 2) {
+            *(i32x2_t*)(C + off) = __builtin_bit_cast(i32x2_t, o4);
+          } else {
+            *(i32x4_t*)(C + off) = __builtin_bit_cast(i32x4_t, o4);
+          }
+          if constexpr (OUT == 4) {
+            if (g.acc_out) {
+              i32x4_t a4;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) a4[e] = (int32_t)acc[i][j][vg * 4 + e];
+              *(i32x4_t*)(g.acc_out + off) = a4;
+            }
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (col + e >= g.N) continue;
+            if constexpr (OUT == 4) sc[e] = g.scale[col + e];
+            int64_t off = cb + row * g.ldc_m + (col + e) * g.ldc_n;
+            C[off] = convert_out<IS_I8, OUT>(acc[i][j], vg * 4 + e, sc[e]);
+            if constexpr (OUT == 4) {
+              if (g.acc_out) g.acc_out[off] = (int32_t)acc[i][j][vg * 4 + e];
+            }
+          }
         }
       }
-    __syncthreads();
-    constexpr int CHUNKS = BM * BN * OB / 16;
-    constexpr int ROWCH = BN * OB / 16;
-    out_t* C = (out_t*)g.c;
-    for (int c = tid; c < CHUNKS; c += NT) {
-      int row = c / ROWCH, ch = c % ROWCH;
-      i32x4_t val = *(const i32x4_t*)(sc + row * CROW + ch * 16);
-      *(i32x4_t*)((uint8_t*)(C + cb + (m0 + row) * g.ldc_m + n0) + ch * 16) = val;
-    }
-    return;
   }
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      int64_t col = n0 + wn * TWN + j * 32 + (lane & 31);
-      if (col >= g.N) continue;
-      float sc = 0.f;
-      if constexpr (OUT == 4) sc = g.scale[col];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        int64_t row = m0 + wm * TWM + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row >= g.M) continue;
-        int64_t off = cb + row * g.ldc_m + col * g.ldc_n;
-        ((out_t*)g.c)[off] = convert_out<IS_I8, OUT>(acc[i][j], v, sc);
-        if constexpr (OUT == 4) {
-          if (g.acc_out) g.acc_out[off] = (int32_t)acc[i][j][v];
-        }
-      }
-    }
 }
 
 template <bool IS_I8, int OUT, int BM, int BN, int WM, int WN>
@@ -319,7 +326,7 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   g.acc_out = acc_out;
   g.tiles_m = (int)((d.M + BM - 1) / BM);
   g.tiles_n = (int)((d.N + BN - 1) / BN);
-  size_t lds = (size_t)2 * (BM + BN) * kRowB;
+  size_t lds = (size_t)2 * (BM + BN) * kBKB;
   static bool attr_set = false;  // gfx950 LDS is 160 KiB; dynamic LDS above 64 KiB must be opted into
   if (!attr_set) {
     FO_HIP(hipFuncSetAttribute((const void*)k_gemm<IS_I8, OUT, BM, BN, WM, WN>,
