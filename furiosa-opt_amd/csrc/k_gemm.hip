@@ -5,12 +5,14 @@
 //
 // Tiling (gfx950, wave64): a block of WM x WN waves owns a BM x BN tile; each wave owns
 // (BM/WM) x (BN/WN) as a grid of 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 /
-// v_mfma_i32_32x32x32_i8). K advances 128 bytes per stage; stages are double-buffered in LDS.
+// v_mfma_i32_32x32x32_i8). K advances kRB bytes per stage; kNS stages rotate through LDS. The
+// DMA refilling a buffer is issued right after the barrier that releases it, and each stage waits
+// only for its own DMA (vmcnt counts the younger ones).
 //
 // Operand staging: global -> LDS by buffer_load_dwordx4 ... lds (LDS DMA: each lane's 16 bytes
 // land at the wave's LDS base + 16 * lane, no VGPR round trip and no ds_write). A wave's
-// 1 KiB DMA covers 8 rows of 128 bytes; the lane -> (row, chunk) assignment stores chunk c of row r
-// at slot c ^ ((r >> 1) & 7), so the 16 lanes of one 16-byte fragment read (16 consecutive rows,
+// 1 KiB DMA covers 8 rows of 128 bytes; the lane -> (row, chunk) assignment stores chunk c of row
+// r at slot c ^ ((r >> 1) & 7), so the 16 lanes of one 16-byte fragment read (16 consecutive rows,
 // one chunk) touch 16 distinct 16-byte bank groups. Rows past the operand's extent read as zero
 // (buffer range check); chunks past K are pointed outside the range for the same effect.
 //
@@ -32,7 +34,14 @@ typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16_t;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2_t;
 
-constexpr int kBKB = 128;         // K bytes per stage
+constexpr int kRB = 128;  // K bytes per row per stage (four 32-byte MFMA k-steps)
+constexpr int kNS = 2;    // LDS stages (double buffer; 64-byte stages x4 measured slower: more barriers)
+constexpr int kCPR = kRB / 16;                  // 16-byte chunks per row
+constexpr int kRPC = 1024 / kRB;                // rows per 1 KiB wave DMA
+constexpr int kSwzShift = kRB == 64 ? 2 : 1;    // rows sharing a bank-group offset: 16 / kCPR
+
+// s_waitcnt immediate (gfx9 encoding): vector memory count <= n, LDS/scalar count 0, export any.
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
 
 template <bool IS_I8>
 struct MfmaT;
@@ -125,14 +134,15 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   constexpr int EB = IS_I8 ? 1 : 2;            // element bytes
   constexpr int TWM = BM / WM, TWN = BN / WN;  // wave tile
   constexpr int TM = TWM / 32, TN = TWN / 32;
-  constexpr int A_CH = BM / 8 / W;  // 1 KiB DMA chunks (8 rows) of A per wave per stage
-  constexpr int B_CH = BN / 8 / W;
-  static_assert(A_CH * 8 * W == BM && B_CH * 8 * W == BN, "tile/waves mismatch");
-  constexpr int STAGE = (BM + BN) * kBKB;
+  constexpr int A_CH = BM / kRPC / W;  // 1 KiB DMA chunks of A per wave per stage
+  constexpr int B_CH = BN / kRPC / W;
+  static_assert(A_CH * kRPC * W == BM && B_CH * kRPC * W == BN, "tile/waves mismatch");
+  constexpr int PER = A_CH + B_CH;  // DMA instructions per wave per stage
+  constexpr int STAGE = (BM + BN) * kRB;
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   auto sA = [&](int buf) { return smem + buf * STAGE; };
-  auto sB = [&](int buf) { return smem + buf * STAGE + BM * kBKB; };
+  auto sB = [&](int buf) { return smem + buf * STAGE + BM * kRB; };
 
   // Tile order: consecutive block ids go round-robin over the 8 XCDs; regroup so each XCD walks a
   // contiguous range of tiles, ordered in groups of 8 tile-rows so neighbours share operands in L2.
@@ -165,25 +175,27 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Bbase), (short)0, uniform_i32((rows_b - 1) * g.ldb * EB + KB), 0x00020000);
 
-  // DMA source offsets: lane l of chunk q fills LDS slot l % 8 of tile row r = 8q + l / 8 with
-  // global chunk (l % 8) ^ ((r >> 1) & 7) of that row.
+  // DMA source offsets: lane l of chunk q fills LDS slot l % kCPR of tile row r = kRPC q + l / kCPR
+  // with global chunk (l % kCPR) ^ swz(r), swz(r) = (r >> kSwzShift) & (kCPR - 1).
   uint32_t a_off[A_CH], a_kc[A_CH], b_off[B_CH], b_kc[B_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
-    int r = 8 * (wave * A_CH + i) + (lane >> 3);
-    int c = (lane & 7) ^ ((r >> 1) & 7);
+    int r = kRPC * (wave * A_CH + i) + lane / kCPR;
+    int c = (lane % kCPR) ^ ((r >> kSwzShift) & (kCPR - 1));
     a_kc[i] = (uint32_t)c * 16;
     a_off[i] = (uint32_t)(r * g.lda * EB) + a_kc[i];
   }
 #pragma unroll
   for (int i = 0; i < B_CH; ++i) {
-    int r = 8 * (wave * B_CH + i) + (lane >> 3);
-    int c = (lane & 7) ^ ((r >> 1) & 7);
+    int r = kRPC * (wave * B_CH + i) + lane / kCPR;
+    int c = (lane % kCPR) ^ ((r >> kSwzShift) & (kCPR - 1));
     b_kc[i] = (uint32_t)c * 16;
     b_off[i] = (uint32_t)(r * g.ldb * EB) + b_kc[i];
   }
-  auto issue = [&](uint32_t kb, int buf) {
-    const bool tail = kb + kBKB > KB;  // uniform: the last, partial stage
+  auto issue = [&](int st) {
+    const uint32_t kb = (uint32_t)st * kRB;
+    const int buf = st % kNS;
+    const bool tail = kb + kRB > KB;  // uniform: the last, partial stage
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       uint32_t off = a_off[i] + kb;
@@ -210,39 +222,68 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   // frow (+ 32i), found at slot (2kk + half) ^ swz; rows of a fragment tile start at multiples
   // of 32, so swz depends on frow only.
   const int frow = lane & 31, half = lane >> 5;
-  const int swz = (frow >> 1) & 7;
-  const int a_row = (wm * TWM + frow) * kBKB, b_row = (wn * TWN + frow) * kBKB;
+  const int swz = (frow >> kSwzShift) & (kCPR - 1);
+  const int a_row = (wm * TWM + frow) * kRB, b_row = (wn * TWN + frow) * kRB;
   auto slot = [&](int kk) { return ((2 * kk + half) ^ swz) * 16; };
 
-  const int nst = (int)((KB + kBKB - 1) / kBKB);
-  issue(0, 0);
+  const int nst = (int)((KB + kRB - 1) / kRB);
+  constexpr int KST = kRB / 32;  // MFMA k-steps per stage
+  static_assert(KST % 2 == 0, "fragment double-buffer parity assumes an even k-step count");
+  // Stage s's DMA is complete once at most the younger stages' DMAs are outstanding; after the
+  // barrier every wave's is, and every wave has its fragments of the previous stage in registers,
+  // so that stage's buffer can be refilled. The barrier carries no memory fence (that would drain
+  // every DMA); the compiler barriers keep LDS accesses on their side of it.
+  auto stage_ready = [&](int s) {
+    // DMAs in flight younger than stage s: the prologue fills all kNS buffers; afterwards the
+    // refill of stage s - 1's buffer (stage s - 1 + kNS) is issued after this barrier.
+    const int ahead = min(nst - 1 - s, s == 0 ? kNS - 1 : kNS - 2);
+    if (ahead >= 3)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(3 * PER));
+    else if (ahead == 2)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * PER));
+    else if (ahead == 1)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(PER));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+  };
+  i32x4_t fa[2][TM], fb[2][TN];
+  auto read_frags = [&](int buf, int kk, int p) {
+    const uint8_t* a_s = sA(buf);
+    const uint8_t* b_s = sB(buf);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[p][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kRB + slot(kk));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) fb[p][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kRB + slot(kk));
+  };
+
+#pragma unroll
+  for (int st = 0; st < kNS; ++st)
+    if (st < nst) issue(st);
+  stage_ready(0);
+  read_frags(0, 0, 0);
+  // Pipeline over the flattened k-steps t = s * KST + kk: the fragments of t + 1 are read while
+  // t's MFMAs issue. Crossing into stage s + 1, its readiness barrier comes after the last
+  // fragments of stage s were read and before t's MFMAs, which then cover the latency of the
+  // first reads from stage s + 1.
   for (int s = 0; s < nst; ++s) {
-    const int cur = s & 1;
-    // Stage s has landed (this wave's DMA), and after the barrier every wave's has; every wave is
-    // also done reading stage s - 1, whose buffer the next DMA overwrites.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (s + 1 < nst) issue((uint32_t)(s + 1) * kBKB, cur ^ 1);
-    const uint8_t* a_s = sA(cur);
-    const uint8_t* b_s = sB(cur);
-    i32x4_t fa[2][TM], fb[2][TN];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) fa[0][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kBKB + slot(0));
-#pragma unroll
-    for (int j = 0; j < TN; ++j) fb[0][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kBKB + slot(0));
-#pragma unroll
-    for (int kk = 0; kk < kBKB / 32; ++kk) {
-      const int p = kk & 1;
-      if (kk + 1 < kBKB / 32) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) fa[p ^ 1][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kBKB + slot(kk + 1));
-#pragma unroll
-        for (int j = 0; j < TN; ++j) fb[p ^ 1][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kBKB + slot(kk + 1));
+    for (int kk = 0; kk < KST; ++kk) {
+      const int p = kk & 1;  // KST is even: the fragment buffer parity restarts each stage
+      if (kk + 1 < KST) {
+        read_frags(s % kNS, kk + 1, p ^ 1);
+      } else if (s + 1 < nst) {
+        stage_ready(s + 1);
+        if (s + kNS < nst) issue(s + kNS);  // into stage s's buffer, released by the barrier
+        read_frags((s + 1) % kNS, 0, p ^ 1);
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = M::mma(fb[p][j], fa[p][i], acc[i][j]);
+      __builtin_amdgcn_iglp_opt(0);  // interleave the fragment reads with the MFMAs
     }
   }
 
@@ -326,7 +367,7 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   g.acc_out = acc_out;
   g.tiles_m = (int)((d.M + BM - 1) / BM);
   g.tiles_n = (int)((d.N + BN - 1) / BN);
-  size_t lds = (size_t)2 * (BM + BN) * kBKB;
+  size_t lds = (size_t)kNS * (BM + BN) * kRB;
   static bool attr_set = false;  // gfx950 LDS is 160 KiB; dynamic LDS above 64 KiB must be opted into
   if (!attr_set) {
     FO_HIP(hipFuncSetAttribute((const void*)k_gemm<IS_I8, OUT, BM, BN, WM, WN>,
