@@ -115,6 +115,67 @@ __global__ void __launch_bounds__(256) k_relayout_tiled(T* __restrict__ dst, con
   }
 }
 
+// 16-byte variant of the tiled transpose, for whole 16-byte chunks along both wheel 0 and wheel j
+// (sizes, bases and strides multiples of V = 16 / sizeof(T) elements, both wheels fully live):
+// src rows are read and dst rows written as 16-byte vectors, the transpose happens in LDS (element
+// scatter in, 16-byte reads out).
+template <typename T>
+__global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, const T* __restrict__ src,
+                                                          int64_t dst_base, int64_t src_base, Wheels<1> w, int jw,
+                                                          uint32_t outer_count, uint32_t tiles0, uint32_t tilesj) {
+  typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
+  constexpr int V = 16 / sizeof(T);  // elements per 16-byte chunk
+  constexpr int TS = 64;             // tile edge in elements
+  constexpr int CPR = TS / V;        // chunks per tile row
+  __shared__ __attribute__((aligned(16))) T tile[TS][TS + V];  // [j][d0], rows padded by one chunk
+  uint32_t bid = blockIdx.x;
+  uint32_t t0 = bid % tiles0;
+  bid /= tiles0;
+  uint32_t tj = bid % tilesj;
+  uint32_t outer = bid / tilesj;
+  if (outer >= outer_count) return;
+  int64_t soff = 0, dpos = 0, place = 1, place_j = 0;
+  bool live_outer = true;
+  uint32_t q = outer;
+  for (int i = 0; i < w.n; ++i) {
+    if (i == 0) {
+      place *= w.size[0];
+      continue;
+    }
+    if (i == jw) {
+      place_j = place;
+      place *= w.size[i];
+      continue;
+    }
+    uint32_t nq = w.div[i].div(q);
+    uint32_t d = q - nq * w.size[i];
+    q = nq;
+    live_outer &= d < w.live[i];
+    soff += (int64_t)d * w.stride[0][i];
+    dpos += (int64_t)d * place;
+    place *= w.size[i];
+  }
+  if (!live_outer) return;  // uniform: a dead outer digit leaves the whole tile unwritten
+  const uint32_t n0 = w.size[0], nj = w.size[jw];
+  const int64_t s0 = w.stride[0][0];
+  for (int c = threadIdx.x; c < TS * CPR; c += 256) {
+    const int r = c / CPR, cc = c % CPR;  // src row d0 = r, chunk cc along j
+    const uint32_t d0 = t0 * TS + r, j0 = tj * TS + cc * V;
+    if (d0 < n0 && j0 < nj) {
+      vec_t v = *(const vec_t*)(src + src_base + soff + (int64_t)d0 * s0 + j0);
+      const T* e = (const T*)&v;
+#pragma unroll
+      for (int k = 0; k < V; ++k) tile[cc * V + k][r] = e[k];
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < TS * CPR; c += 256) {
+    const int r = c / CPR, cc = c % CPR;  // dst row j = r, chunk cc along d0
+    const uint32_t dj = tj * TS + r, d0 = t0 * TS + cc * V;
+    if (dj < nj && d0 < n0) *(vec_t*)(dst + dst_base + dpos + (int64_t)dj * place_j + d0) = *(const vec_t*)&tile[r][cc * V];
+  }
+}
+
 // Chunked relayout: the innermost wheel is fully live and contiguous in src (stride 1) and every
 // 16-byte chunk of dst positions maps to 16 contiguous, aligned src bytes. One thread moves one
 // chunk; only the outer wheels' liveness can drop it.
@@ -174,8 +235,19 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
     uint32_t outer = (uint32_t)(total / ((int64_t)w.size[0] * w.size[jw]));
     int64_t blocks = (int64_t)tiles0 * tilesj * outer;
     if (blocks < (1ll << 31)) {
-      hipLaunchKernelGGL(k_relayout_tiled<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
-                         dst_base, src_base, w, jw, outer, tiles0, tilesj);
+      // 16-byte path: whole chunks along both tile axes, every base, stride and place a multiple
+      // of a chunk, both tile wheels fully live.
+      bool v16 = sizeof(T) >= 2 && w.size[0] % VEC == 0 && w.size[jw] % VEC == 0 && w.live[0] == w.size[0] &&
+                 w.live[jw] == w.size[jw] && dst_base % VEC == 0 && src_base % VEC == 0 &&
+                 ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0;
+      for (int i = 0; i < w.n && v16; ++i)
+        if (i != jw) v16 = (w.stride[0][i] % VEC) == 0;
+      if (v16)
+        hipLaunchKernelGGL(k_relayout_tiled16<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
+                           dst_base, src_base, w, jw, outer, tiles0, tilesj);
+      else
+        hipLaunchKernelGGL(k_relayout_tiled<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
+                           dst_base, src_base, w, jw, outer, tiles0, tilesj);
       FO_HIP(hipGetLastError());
       return;
     }

@@ -77,6 +77,22 @@ def test_transpose_large_tiled(rt):
     assert np.array_equal(d.read(np.uint16), a.reshape(n, n).T.reshape(-1))
 
 
+@pytest.mark.parametrize("shape,dt,npt", [
+    ((1, 200, 136), BF16, np.uint16),  # 16-byte tiled path, partial edge tiles
+    ((3, 72, 100), I32, np.int32),     # 16-byte tiled path with an outer wheel, 4-byte elements
+    ((1, 70, 66), BF16, np.uint16),    # sizes not whole 16-byte chunks: element-wise tiled path
+    ((2, 128, 64), I8, np.int8),       # 1-byte elements: element-wise tiled path
+])
+def test_transpose_tiled_variants(rt, shape, dt, npt):
+    b, r, c = shape
+    rng = np.random.default_rng(11)
+    a = rng.integers(np.iinfo(npt).min, np.iinfo(npt).max, b * r * c, dtype=np.int64).astype(npt)
+    s, d = rt.upload(a), rt.alloc(a.nbytes)
+    sz = dict(B=b, R=r, C=c)
+    rt.transpose(d, s, dt, fh.m("B, R, C", **sz), fh.m("B, C, R", **sz))
+    assert np.array_equal(d.read(npt), a.reshape(b, r, c).transpose(0, 2, 1).reshape(-1))
+
+
 def test_transpose_partial_view_offsets(rt):
     # A tile view (mapping-expressions.md:383-398): base m![A, B], view m![A, B / 32 = 2 # 16, B % 32]
     # at offset B = 64, copied into a compact m![A, B / 32 = 2, B % 32].
