@@ -379,9 +379,10 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   FO_HIP(hipGetLastError());
 }
 
-// Tile choice: 256x256 with 8 waves (one tile per CU at 4096^2) when the problem is large,
-// 128x128 otherwise (measured best on MI355X among 128, 256/4-wave and 256/8-wave).
-// FO_GEMM_TILE overrides it for measurement: 128, 256 (4 waves of 128x128) or 2568 (8 waves).
+// Tile choice: 256x256 with 16 waves of 64x64 (one tile per CU at 4096^2, four waves per SIMD)
+// when the problem is large, 128x128 otherwise (measured best on MI355X among 128, 256 with 4, 8
+// and 16 waves). FO_GEMM_TILE overrides it for measurement: 128, 256 (4 waves of 128x128),
+// 2568 (8 waves of 128x64) or 25616 (16 waves).
 template <bool IS_I8, int OUT>
 void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b,
                  const float* scale = nullptr, int32_t* acc_out = nullptr) {
@@ -390,8 +391,9 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
     return e ? atoi(e) : 0;
   }();
   int64_t tiles256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
-  int choice = forced ? forced : (tiles256 >= 128 ? 2568 : 128);
+  int choice = forced ? forced : (tiles256 >= 128 ? 25616 : 128);
   if (choice == 2568) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
+  if (choice == 25616) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 256) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);
   return gemm_launch_cfg<IS_I8, OUT, 128, 128, 2, 2>(s, d, c, a, b, scale, acc_out);
 }
