@@ -65,14 +65,183 @@ __global__ void __launch_bounds__(256) k_mlp(int32_t* __restrict__ pred, uint16_
   }
 }
 
+// fc1 with the products taken off the critical path: waves [0, FW) fold, one thread per hidden
+// unit, in ascending k (acc = RN(acc + p_k)); the other waves compute the products
+// p_k = RN(x_k * w_hk) for the next KC-wide k chunk into LDS meanwhile (16-byte weight loads, 8
+// products per unit of work). Same roundings in the same order as the per-thread fold, so the
+// result is bit-identical; only the products run in parallel. Needs in_f % 8 == 0, 16-byte
+// aligned weights, hidden <= 256 (enough producers for kUnits per chunk) and the fc2 products
+// fitting the product buffer.
+constexpr int kKC = 64;          // k per chunk
+constexpr int kPP = kKC + 4;     // LDS row pitch in floats (16-byte rows, conflict-free b128 reads)
+constexpr int kMlpThreads = 512;
+constexpr int kUnits = 4;  // producer work units per chunk per thread (hidden * kKC / 8 <= kUnits * producers)
+constexpr int kAhead = 2;  // chunks of weights in flight ahead of the products
+// s_waitcnt immediate (gfx9 encoding): LDS/scalar count 0, vector memory and export counts left open.
+constexpr int kWaitLgkm0 = 0xF | (0x7 << 4) | (0x3 << 14);
+
+__global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__ pred, uint16_t* __restrict__ logits,
+                                                           const uint16_t* __restrict__ x,
+                                                           const uint16_t* __restrict__ w1,
+                                                           const uint16_t* __restrict__ b1,
+                                                           const uint16_t* __restrict__ w2,
+                                                           const uint16_t* __restrict__ b2, int32_t in_f,
+                                                           int32_t hidden, int32_t out_f) {
+  typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+  typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  const int hp = (hidden + 3) / 4 * 4;
+  float* xs = smem;                                  // widened inputs, in_f (padded to 4)
+  float* hs = xs + (in_f + 3) / 4 * 4;               // hidden activations
+  float* ys = hs + hp;                               // logits
+  float* pb = ys + (out_f + 3) / 4 * 4;              // 2 x hidden x kPP products
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int fw = (hidden + 63) / 64;                 // folder waves
+  const int nprod = kMlpThreads - fw * 64;           // producer threads
+  const int nchunks = (in_f + kKC - 1) / kKC;
+  constexpr int G = kKC / 8;                         // 8-product groups per row per chunk
+  for (int i = tid; i < in_f; i += kMlpThreads) xs[i] = bf16_to_f32(x[b * in_f + i]);
+  __syncthreads();
+  // Producer p owns work units p, p + nprod, ... (at most kUnits): unit u is hidden row u / G,
+  // 8-product group u % G of the chunk. Its weights are loaded kAhead chunks ahead, one register
+  // set per chunk in flight.
+  const int ptid = tid - fw * 64, units = hidden * G;
+  i32x4_t wv[kAhead][kUnits];
+  auto load = [&](int c, int set) {
+#pragma unroll
+    for (int i = 0; i < kUnits; ++i) {
+      const int u = ptid + i * nprod, h = u / G, k0 = c * kKC + (u % G) * 8;
+      if (u < units && k0 < in_f) wv[set][i] = *(const i32x4_t*)(w1 + (int64_t)h * in_f + k0);
+    }
+  };
+  auto produce = [&](int c, int buf, int set) {
+    float* P = pb + buf * hidden * kPP;
+#pragma unroll
+    for (int i = 0; i < kUnits; ++i) {
+      const int u = ptid + i * nprod, h = u / G, g = u % G, k0 = c * kKC + g * 8;
+      if (u >= units || k0 >= in_f) continue;  // in_f % 8 == 0: a group is whole or absent
+      const f32x4_t xa = *(const f32x4_t*)(xs + k0), xb = *(const f32x4_t*)(xs + k0 + 4);
+      f32x4_t p0, p1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t uw = (uint32_t)wv[set][i][e];
+        const float xl = e < 2 ? xa[2 * e] : xb[2 * e - 4], xh = e < 2 ? xa[2 * e + 1] : xb[2 * e - 3];
+        const float lo = __fmul_rn(xl, bf16_to_f32((uint16_t)(uw & 0xffffu)));
+        const float hi = __fmul_rn(xh, bf16_to_f32((uint16_t)(uw >> 16)));
+        if (e < 2) {
+          p0[2 * e] = lo;
+          p0[2 * e + 1] = hi;
+        } else {
+          p1[2 * e - 4] = lo;
+          p1[2 * e - 3] = hi;
+        }
+      }
+      *(f32x4_t*)(P + h * kPP + g * 8) = p0;
+      *(f32x4_t*)(P + h * kPP + g * 8 + 4) = p1;
+    }
+  };
+  // Barrier for LDS only: the producers' weight loads for the next chunk stay in flight across
+  // it (a fenced __syncthreads would drain them).
+  auto lds_barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+  };
+  const bool folder = tid < fw * 64;
+  float acc = 0.f;
+  if (!folder) {
+    load(0, 0);
+    if (nchunks > 1) load(1, 1);
+    produce(0, 0, 0);
+    if (nchunks > 2) load(2, 0);
+  }
+  lds_barrier();
+  for (int c = 0; c < nchunks; ++c) {
+    if (folder) {
+      if (tid < hidden) {
+        const float* P = pb + (c & 1) * hidden * kPP + tid * kPP;
+        const int kn = min(kKC, in_f - c * kKC);  // a multiple of 8
+        for (int k = 0; k < kn; k += 4) {
+          const f32x4_t p = *(const f32x4_t*)(P + k);
+          acc = __fadd_rn(acc, p[0]);
+          acc = __fadd_rn(acc, p[1]);
+          acc = __fadd_rn(acc, p[2]);
+          acc = __fadd_rn(acc, p[3]);
+        }
+      }
+    } else if (c + 1 < nchunks) {
+      // chunk c + 1's weights are in set (c + 1) % 2; that set then takes chunk c + 3
+      if ((c & 1) == 0) {
+        produce(c + 1, 1, 1);
+        if (c + 3 < nchunks) load(c + 3, 1);
+      } else {
+        produce(c + 1, 0, 0);
+        if (c + 3 < nchunks) load(c + 3, 0);
+      }
+    }
+    lds_barrier();  // chunk c folded (its buffer is free); chunk c + 1 produced
+  }
+  if (tid < hidden) {
+    float hv = bf16_to_f32(f32_to_bf16(acc));                    // contract_lane + cast
+    float z = fmaxf(__fadd_rn(hv, bf16_to_f32(b1[tid])), 0.0f);  // clip Add, clip Max 0
+    hs[tid] = bf16_to_f32(f32_to_bf16(z));
+  }
+  __syncthreads();
+  // fc2: the out_f x hidden products in parallel into the (free) product buffer, then one
+  // thread per output folds them in ascending k.
+  for (int i = tid; i < out_f * hidden; i += kMlpThreads) {
+    const int o = i / hidden, kk = i % hidden;
+    pb[o * hp + kk] = __fmul_rn(hs[kk], bf16_to_f32(w2[(int64_t)o * hidden + kk]));
+  }
+  __syncthreads();
+  for (int o = tid; o < out_f; o += kMlpThreads) {
+    float a2 = 0.f;
+    for (int kk = 0; kk < hidden; ++kk) a2 = __fadd_rn(a2, pb[o * hp + kk]);
+    float yv = bf16_to_f32(f32_to_bf16(a2));
+    uint16_t y = f32_to_bf16(__fadd_rn(yv, bf16_to_f32(b2[o])));
+    ys[o] = bf16_to_f32(y);
+    if (logits) logits[b * out_f + o] = y;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int best = 0;
+    int32_t bk = total_key(ys[0]);
+    for (int o = 1; o < out_f; ++o) {
+      int32_t kk = total_key(ys[o]);
+      if (kk >= bk) {  // max_by keeps the last of equal maxima
+        bk = kk;
+        best = o;
+      }
+    }
+    pred[b] = best;
+  }
+}
+
 }  // namespace
 
 void launch_mlp(hipStream_t s, int32_t* pred, uint16_t* logits, const uint16_t* x, const uint16_t* w1,
                 const uint16_t* b1, const uint16_t* w2, const uint16_t* b2, int64_t batch, int64_t in_f,
                 int64_t hidden, int64_t out_f) {
+  require(batch < (1ll << 31), "mlp: batch too large");
+  const size_t lds_split =
+      (size_t)(((in_f + 3) / 4 + (hidden + 3) / 4 + (out_f + 3) / 4) * 4 + 2 * hidden * kPP) * sizeof(float);
+  const int64_t producers = kMlpThreads - (hidden + 63) / 64 * 64;
+  if (in_f % 8 == 0 && hidden <= 256 && hidden * (kKC / 8) <= kUnits * producers && out_f * ((hidden + 3) / 4 * 4) <= 2 * hidden * kPP &&
+      ((uintptr_t)w1 % 16) == 0 && lds_split <= 160 * 1024) {
+    static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into
+    if (!attr_set) {
+      FO_HIP(hipFuncSetAttribute((const void*)k_mlp_split, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(k_mlp_split, dim3((unsigned)batch), dim3(kMlpThreads), lds_split, s, pred, logits, x, w1, b1, w2,
+                       b2, (int32_t)in_f, (int32_t)hidden, (int32_t)out_f);
+    FO_HIP(hipGetLastError());
+    return;
+  }
   size_t lds = (size_t)(in_f + hidden + out_f) * sizeof(float);
   require(lds <= 64 * 1024, "mlp: layer widths exceed the LDS budget");
-  require(batch < (1ll << 31), "mlp: batch too large");
   hipLaunchKernelGGL(k_mlp, dim3((unsigned)batch), dim3(256), lds, s, pred, logits, x, w1, b1, w2, b2, (int32_t)in_f,
                      (int32_t)hidden, (int32_t)out_f);
   FO_HIP(hipGetLastError());
