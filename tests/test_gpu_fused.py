@@ -183,6 +183,28 @@ def test_mapped_gemm_config_sampled(rt):
         close(got[r0:r0 + 3], want)
 
 
+@pytest.mark.parametrize("types", [(fh.BF16, fh.BF16), (fh.BF16, fh.F32)], ids=["bf16", "f32out"])
+def test_mapped_gemm_large_tiles_ragged(rt, types):
+    # Enough 256x256 tiles for the large-tile path, with a partial last tile in M and in N and a
+    # K that ends inside a 64-element stage (its DMA chunks past K must read as zero).
+    M, N, K = 2056, 4000, 200
+    in_t, out_t = types
+    s = dict(M=M, N=N, K=K)
+    rng = np.random.default_rng(38)
+    a, b = bf16(rng, M * K), bf16(rng, N * K)
+    ob = 2 if out_t == fh.BF16 else 4
+    out = rt.alloc(M * N * ob)
+    rt.contraction(out, rt.upload(a), rt.upload(b), in_t, out_t, fh.m("M / 8, M % 8, K", **s), fh.m("N, K", **s),
+                   fh.m("M / 8, M % 8, N, K", **s), fh.m("M / 8, M % 8, N", **s))
+    got = out.read(np.uint16 if out_t == fh.BF16 else np.float32).reshape(M, N)
+    for r0 in (0, 253, 2048, M - 3):
+        want = emu.gemm_rows(a, b, M, N, K, r0, r0 + 3, out_t=out_t).reshape(3, N)
+        if out_t == fh.BF16:
+            close(emu.bf16_to_f32(got[r0:r0 + 3]), emu.bf16_to_f32(want))
+        else:
+            close(got[r0:r0 + 3], want, rel=1e-3)
+
+
 # ---- MLP classifier ----------------------------------------------------------------------
 
 
