@@ -94,8 +94,8 @@ __device__ __forceinline__ void qk(const uint8_t* __restrict__ sK, const i32x4_t
 template <int D, bool MASK>
 __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const uint8_t* __restrict__ sVt,
                                           const i32x4_t (&qf)[AttnCfg<D>::KS], f32x16_t (&o)[AttnCfg<D>::DT],
-                                          f32x16_t (&sc)[2], float& m_run, float& l_part, int kv0, int myq,
-                                          int seq, int causal, float inv_sd, int g, int col) {
+                                          f32x16_t (&sc)[2], float& m_run, float& l_part, int kv0, int lim,
+                                          float inv_sd, int g, int col) {
   using C = AttnCfg<D>;
   f32x16_t sn[2];
   qk<D>(sKn, qf, sn, g, col);
@@ -105,11 +105,11 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     if (MASK) {
+      // key kv0 + kt*32 + 8(r/4) + 4g + r%4 is visible iff it is <= lim: one compare against a
+      // per-lane threshold with the register's constant key offset.
+      const int thr = lim - kv0 - kt * 32 - 4 * g;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        int key = kv0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        sc[kt][r] = (key >= seq || (causal && key > myq)) ? -INFINITY : sc[kt][r];
-      }
+      for (int r = 0; r < 16; ++r) sc[kt][r] = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : sc[kt][r];
     }
 #pragma unroll
     for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(sc[kt][r], sc[kt][r + 1]));
@@ -177,6 +177,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   const int q0 = qb * kBM;
   const int q0w = q0 + wave * 32;
   const int myq = q0w + col;
+  const int lim = causal ? min(myq, seq - 1) : seq - 1;  // last key this lane's query sees
 
   const uint16_t* Qh = q + head * (int64_t)seq * D;
   const uint16_t* Kh = k + head * (int64_t)seq * D;
@@ -276,7 +277,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     const int kv0 = j * kBN;
     load_k(kv0 + 2 * kBN);
     load_v(kv0 + kBN);
-    attn_step<D, false>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, myq, seq, causal, inv_sd,
+    attn_step<D, false>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
                         g, col);
     store_k(j & 1);
     store_v((j + 1) & 1);
@@ -289,7 +290,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     load_k(kv0 + 2 * kBN);
     load_v(kv0 + kBN);
     if (!(causal && kv0 > q0w + 31))  // wave-uniform
-      attn_step<D, true>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, myq, seq, causal, inv_sd,
+      attn_step<D, true>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
                          g, col);
     store_k(j & 1);
     store_v((j + 1) & 1);
@@ -297,7 +298,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   }
 
   // out[myq][d] = bf16( bf16(o) / (l + EPS) ); lane holds d = 32t + 8*(r/4) + 4g + r%4. The
-  // quotient is correctly rounded (l >= 1, so it is finite and the divisor normal).
+  // quotient is correctly rounded (l >= 1, so it is finite and the divisor normal); both narrows
+  // are the hardware's round-to-nearest-even (finite inputs give finite, normal-or-zero o).
   const float l_run = l_part + __shfl_xor(l_part, 32, 64);
   if (myq < seq) {
     const float denom = l_run + kEps;
@@ -310,10 +312,9 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
         i32x2_t wv;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          float a = bf16_to_f32(f32_to_bf16(o[t][blk * 4 + 2 * e]));
-          float b = bf16_to_f32(f32_to_bf16(o[t][blk * 4 + 2 * e + 1]));
-          uint32_t lo = f32_to_bf16(div_cr(a, denom, rinv)), hi = f32_to_bf16(div_cr(b, denom, rinv));
-          wv[e] = (int)(lo | (hi << 16));
+          const uint32_t ob = pack_bf16(o[t][blk * 4 + 2 * e], o[t][blk * 4 + 2 * e + 1]);
+          const float a = __builtin_bit_cast(float, ob << 16), b = __builtin_bit_cast(float, ob & 0xffff0000u);
+          wv[e] = (int)pack_bf16(div_cr(a, denom, rinv), div_cr(b, denom, rinv));
         }
         *(i32x2_t*)(orow + t * 32 + 8 * blk + 4 * g) = wv;
       }
