@@ -88,6 +88,27 @@ int64_t max_live_offset(const std::vector<fm::Wheel>& ws, int k) {
   return m;
 }
 
+// The runtime's device scratch, at least `bytes` long (grown after the stream drains).
+void* scratch(fo_runtime* rt, uint64_t bytes) {
+  if (rt->scratch_bytes < bytes) {
+    FO_HIP(hipStreamSynchronize(rt->stream));
+    if (rt->scratch) FO_HIP(hipFree(rt->scratch));
+    rt->scratch = nullptr;
+    rt->scratch_bytes = 0;
+    FO_HIP(hipMalloc(&rt->scratch, bytes));
+    rt->scratch_bytes = bytes;
+  }
+  return rt->scratch;
+}
+
+// Shared set-up of scatter / gather: the stream wheels of one side, all digits live.
+std::vector<fm::Wheel> stream_wheels(const fm::Factors& memory, const fm::Factors& outer, const fm::Factors& inner,
+                                     const char* what) {
+  fm::Joint j = fm::sequence({memory}, {outer, inner}, fm::Mode::Read);
+  for (auto& w : j.wheels) require(w.live == w.size, std::string(what) + ": padded streams are not supported");
+  return j.wheels;
+}
+
 int64_t product(const std::vector<fm::Wheel>& ws) {
   int64_t p = 1;
   for (auto& w : ws) p *= w.size;
@@ -132,6 +153,7 @@ void fo_runtime_free(fo_runtime* rt) {
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto& e : rt->events)
     if (e) (void)hipEventDestroy(e);
+  if (rt->scratch) (void)hipFree(rt->scratch);
   if (rt->stream) (void)hipStreamDestroy(rt->stream);
   delete rt;
 }
@@ -409,6 +431,92 @@ int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     set_device(rt);
     const int mem[1] = {0};
     launch_transmute(rt->stream, dst->ptr, src->ptr, eb, dn, to_desc<1>(dw, mem), to_desc<1>(sw, mem));
+  });
+}
+
+int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo_buffer* index, fo_dtype t,
+                   const char* src_map, const char* key_map, const char* dst_map, const char* idx_map,
+                   int32_t scaled) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    check_buf(index, "index");
+    fm::Factors sm = flat(src_map, "src_map"), km = flat(key_map, "key_map"), dm = flat(dst_map, "dst_map"),
+                im = flat(idx_map, "idx_map");
+    // scatter_params (backend/op_prep.rs:45-54): payload = Src / Key; the indexed dst axis is the
+    // first live axis of Dst / payload.
+    fm::Factors payload = fm::remove_padding(fm::carve(sm, km));
+    fm::Factors axis;
+    try {
+      axis = fm::first_axis(fm::carve(dm, payload));
+    } catch (const fm::Error&) {
+      throw InvalidArg("scatter: dst residue has no live target axis");
+    }
+    const int64_t eb = dtype_bytes(t), keys = fm::size(km), axis_size = fm::size(axis), np = fm::size(payload);
+    require(fm::size(im) >= keys, "scatter: the index tensor has fewer cells than the key");
+    require((int64_t)index->bytes >= keys * 4, "scatter: index buffer shorter than the key");
+    auto ws = stream_wheels(sm, payload, km, "scatter src");
+    auto wd = stream_wheels(dm, payload, axis, "scatter dst");
+    require(max_live_offset(ws, 0) < (int64_t)(src->bytes / eb), "scatter: src reads past the buffer");
+    require(max_live_offset(wd, 0) < (int64_t)(dst->bytes / eb), "scatter: dst writes past the buffer");
+    require(np * keys < (1ll << 31) && np * axis_size < (1ll << 31), "scatter: more than 2^31 positions");
+    // decode_stride (buf.rs:816-822): a scaled index is a byte offset of payload-sized blocks.
+    const int64_t div = scaled ? np * eb : 1;
+    require(div < (1ll << 31), "scatter: payload block too large");
+    if (np * keys == 0) return;
+    set_device(rt);
+    int32_t* win = (int32_t*)scratch(rt, (uint64_t)(axis_size + 1) * 4);
+    int32_t* flag = win + axis_size;
+    FO_HIP(hipMemsetAsync(win, 0xff, (size_t)axis_size * 4, rt->stream));  // -1: no key yet
+    FO_HIP(hipMemsetAsync(flag, 0, 4, rt->stream));
+    const int mem[1] = {0};
+    launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,
+                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), win, flag);
+    int32_t bad = 0;
+    FO_HIP(hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, rt->stream));
+    FO_HIP(hipStreamSynchronize(rt->stream));
+    require(bad == 0, "scatter: an index is negative or past the scatter axis");
+  });
+}
+
+int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo_buffer* index, fo_dtype t,
+                  const char* src_map, const char* dst_map, const char* idx_map, int32_t scaled) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    check_buf(index, "index");
+    fm::Factors sm = flat(src_map, "src_map"), dm = flat(dst_map, "dst_map"), im = flat(idx_map, "idx_map");
+    // gather_params (backend/op_prep.rs:78-89): payload = Dst / Idx; the indexed (table) axis is
+    // the first live axis of Src / payload; the dst slots are the index tensor's own mapping.
+    fm::Factors payload = fm::remove_padding(fm::carve(dm, im));
+    fm::Factors axis;
+    try {
+      axis = fm::first_axis(fm::carve(sm, payload));
+    } catch (const fm::Error&) {
+      throw InvalidArg("gather: src residue has no live target axis");
+    }
+    const int64_t eb = dtype_bytes(t), slots = fm::size(im), axis_size = fm::size(axis), np = fm::size(payload);
+    require((int64_t)index->bytes >= slots * 4, "gather: index buffer shorter than the index mapping");
+    auto ws = stream_wheels(sm, payload, axis, "gather src");
+    auto wd = stream_wheels(dm, payload, im, "gather dst");
+    require(max_live_offset(ws, 0) < (int64_t)(src->bytes / eb), "gather: src reads past the buffer");
+    require(max_live_offset(wd, 0) < (int64_t)(dst->bytes / eb), "gather: dst writes past the buffer");
+    require(np * slots < (1ll << 31) && np * axis_size < (1ll << 31), "gather: more than 2^31 positions");
+    const int64_t div = scaled ? np * eb : 1;
+    require(div < (1ll << 31), "gather: payload block too large");
+    if (np * slots == 0) return;
+    set_device(rt);
+    int32_t* flag = (int32_t*)scratch(rt, 4);
+    FO_HIP(hipMemsetAsync(flag, 0, 4, rt->stream));
+    const int mem[1] = {0};
+    launch_gather(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, slots, axis_size, (int32_t)div,
+                  to_desc<1>(ws, mem), to_desc<1>(wd, mem), flag);
+    int32_t bad = 0;
+    FO_HIP(hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, rt->stream));
+    FO_HIP(hipStreamSynchronize(rt->stream));
+    require(bad == 0, "gather: an index is negative or past the gathered axis");
   });
 }
 

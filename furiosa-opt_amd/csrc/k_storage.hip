@@ -293,6 +293,75 @@ __global__ void __launch_bounds__(kBlock) k_transmute(T* __restrict__ dst, const
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// scatter / gather (storage/buf.rs:485-576). Both walk a stream of (payload position, slot): the
+// src and dst offsets come from two wheel lists, and the slot's index picks the position on the
+// indexed axis. An index that is negative or past the axis is skipped and raises `flag` (the
+// reference panics there); the host reports it.
+// ---------------------------------------------------------------------------------------------
+__device__ __forceinline__ int64_t wheel_offset(const Wheels<1>& w, uint32_t q) {
+  int64_t off = 0;
+  for (int i = 0; i < w.n; ++i) {
+    uint32_t nq = w.div[i].div(q);
+    off += (int64_t)(q - nq * w.size[i]) * w.stride[0][i];
+    q = nq;
+  }
+  return off;
+}
+
+// Decoded index (decode_indices, buf.rs:801-812) or -1 when it is out of range.
+__device__ __forceinline__ int32_t decode_index(const int32_t* __restrict__ idx, uint32_t i, int32_t div,
+                                                uint32_t axis_size) {
+  int32_t raw = idx[i];
+  if (raw < 0) return -1;
+  int32_t a = raw / div;
+  return (uint32_t)a < axis_size ? a : -1;
+}
+
+// dst[off_d(p, r)] = src[off_s(p, index[r])] for every payload position p and index slot r.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) k_gather(T* __restrict__ dst, const T* __restrict__ src,
+                                                   const int32_t* __restrict__ idx, uint32_t total, FastDiv rdiv,
+                                                   uint32_t axis_size, int32_t div, Wheels<1> ws, Wheels<1> wd,
+                                                   int32_t* __restrict__ flag) {
+  for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
+    uint32_t p = rdiv.div(t), r = t - p * rdiv.d;
+    int32_t a = decode_index(idx, r, div, axis_size);
+    if (a < 0) {
+      *flag = 1;
+      continue;
+    }
+    dst[wheel_offset(wd, t)] = src[wheel_offset(ws, p * axis_size + (uint32_t)a)];
+  }
+}
+
+// win[a] = the last key slot whose index is a: the serial scatter's last write wins.
+__global__ void __launch_bounds__(kBlock) k_scatter_winners(const int32_t* __restrict__ idx, uint32_t keys,
+                                                            uint32_t axis_size, int32_t div, int32_t* __restrict__ win,
+                                                            int32_t* __restrict__ flag) {
+  for (uint32_t k = blockIdx.x * kBlock + threadIdx.x; k < keys; k += gridDim.x * kBlock) {
+    int32_t a = decode_index(idx, k, div, axis_size);
+    if (a < 0)
+      *flag = 1;
+    else
+      atomicMax(win + a, (int32_t)k);
+  }
+}
+
+// dst[off_d(p, index[k])] = src[off_s(p, k)] for the winning key slot k of each target.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) k_scatter(T* __restrict__ dst, const T* __restrict__ src,
+                                                    const int32_t* __restrict__ idx, const int32_t* __restrict__ win,
+                                                    uint32_t total, FastDiv kdiv, uint32_t axis_size, int32_t div,
+                                                    Wheels<1> ws, Wheels<1> wd) {
+  for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
+    uint32_t p = kdiv.div(t), k = t - p * kdiv.d;
+    int32_t a = decode_index(idx, k, div, axis_size);
+    if (a < 0 || win[a] != (int32_t)k) continue;
+    dst[wheel_offset(wd, p * axis_size + (uint32_t)a)] = src[wheel_offset(ws, t)];
+  }
+}
+
 }  // namespace
 
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t eb, int64_t dst_base, int64_t src_base,
@@ -850,6 +919,63 @@ void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const
   if (in_t == FO_I8 && out_t == FO_I32) return contract_t<int8_t, int32_t, int32_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_I32) return contract_t<int32_t, int32_t, int32_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   throw InvalidArg("contraction: unsupported dtype pair");
+}
+
+}  // namespace fo
+
+namespace fo {
+
+void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
+                   int64_t payload, int64_t slots, int64_t axis_size, int32_t div, const Wheels<1>& ws,
+                   const Wheels<1>& wd, int32_t* flag) {
+  const uint32_t total = (uint32_t)(payload * slots);
+  dim3 g(grid_for(total)), b(kBlock);
+  const FastDiv rdiv((uint32_t)slots);
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(k_gather<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, idx, total, rdiv,
+                         (uint32_t)axis_size, div, ws, wd, flag);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_gather<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, idx, total, rdiv,
+                         (uint32_t)axis_size, div, ws, wd, flag);
+      break;
+    case 4:
+      hipLaunchKernelGGL(k_gather<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, idx, total, rdiv,
+                         (uint32_t)axis_size, div, ws, wd, flag);
+      break;
+    default:
+      throw InvalidArg("gather: unsupported element size");
+  }
+  FO_HIP(hipGetLastError());
+}
+
+void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
+                    int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
+                    const Wheels<1>& wd, int32_t* win, int32_t* flag) {
+  hipLaunchKernelGGL(k_scatter_winners, dim3(grid_for(keys)), dim3(kBlock), 0, s, idx, (uint32_t)keys,
+                     (uint32_t)axis_size, div, win, flag);
+  FO_HIP(hipGetLastError());
+  const uint32_t total = (uint32_t)(payload * keys);
+  dim3 g(grid_for(total)), b(kBlock);
+  const FastDiv kdiv((uint32_t)keys);
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(k_scatter<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, idx, win, total, kdiv,
+                         (uint32_t)axis_size, div, ws, wd);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_scatter<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, idx, win, total, kdiv,
+                         (uint32_t)axis_size, div, ws, wd);
+      break;
+    case 4:
+      hipLaunchKernelGGL(k_scatter<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, idx, win, total, kdiv,
+                         (uint32_t)axis_size, div, ws, wd);
+      break;
+    default:
+      throw InvalidArg("scatter: unsupported element size");
+  }
+  FO_HIP(hipGetLastError());
 }
 
 }  // namespace fo

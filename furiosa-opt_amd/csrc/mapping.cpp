@@ -433,6 +433,30 @@ bool is_padding(const Factors& f) {
   return true;
 }
 
+Factors remove_padding(const Factors& f) {
+  // Mapping::remove_padding strips the Padding wrappers of the left spine: outer factors that are
+  // pure padding go, the first live factor loses its pad digits, and everything inside it stays.
+  Factors out;
+  size_t i = 0;
+  while (i < f.size() && f[i].kind == Factor::PadOnly) ++i;
+  for (; i < f.size(); ++i) {
+    Factor x = f[i];
+    if (out.empty() && x.kind == Factor::Term) x.extent = x.count;
+    out.push_back(x);
+  }
+  return out;
+}
+
+Factors first_axis(const Factors& f) {
+  for (auto& x : f)
+    if (x.kind == Factor::Term && x.count > 0) {
+      Factor a = x;
+      a.extent = a.count;  // the axis term alone: its live digits, unpadded
+      return {a};
+    }
+  throw Error("mapping has no live axis term");
+}
+
 NodeP unflatten(const Factors& fs) {
   NodeP acc = identity();
   for (auto it = fs.rbegin(); it != fs.rend(); ++it) {

@@ -19,6 +19,8 @@ struct fo_runtime {
   hipEvent_t events[16] = {};
   int cus = 0;
   std::string arch;
+  void* scratch = nullptr;  // device scratch for ops that need working memory (grown on demand)
+  uint64_t scratch_bytes = 0;
 };
 
 struct fo_buffer {
@@ -89,6 +91,15 @@ Wheels<NMEM> to_desc(const std::vector<mapping::Wheel>& ws, const int (&mem)[NME
 // Transpose: dst[dst_base + p] = src[src_base + off(p)] for live p < count.
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_base, int64_t src_base,
                      int64_t count, const Wheels<1>& w);
+// Gather: dst[off_d(p*slots + r)] = src[off_s(p*axis + index[r] / div)]; bad indices skipped, *flag = 1.
+void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
+                   int64_t payload, int64_t slots, int64_t axis_size, int32_t div, const Wheels<1>& ws,
+                   const Wheels<1>& wd, int32_t* flag);
+// Scatter: dst[off_d(p*axis + index[k] / div)] = src[off_s(p*keys + k)], the last key k winning a
+// repeated index (win: axis_size i32 set to -1 beforehand); bad indices skipped, *flag = 1.
+void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
+                    int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
+                    const Wheels<1>& wd, int32_t* win, int32_t* flag);
 // Transmute: dst live rank k <- src live rank k; dst padding zeroed.
 void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_count,
                       const Wheels<1>& dst_self, const Wheels<1>& src_self);

@@ -94,6 +94,9 @@ _sig = {
         [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p],
     ),
     "fo_transmute": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p]),
+    "fo_scatter": (C.c_int32, [_P, _P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p,
+                               C.c_int32]),
+    "fo_gather": (C.c_int32, [_P, _P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int32]),
     "fo_rmsnorm_softmax": (C.c_int32, [_P, _P, _P, _P, C.c_int64, C.c_int64, C.c_float]),
     "fo_attention_prefill": (
         C.c_int32,
@@ -237,6 +240,16 @@ class Runtime:
 
     def transmute(self, dst: "Buffer", src: "Buffer", dtype: int, src_map: str, dst_map: str):
         _check(_lib.fo_transmute(self.h, dst.h, src.h, dtype, src_map.encode(), dst_map.encode()))
+
+    def scatter(self, dst: "Buffer", src: "Buffer", index: "Buffer", dtype: int, src_map: str, key_map: str,
+                dst_map: str, idx_map: str, scaled: bool):
+        _check(_lib.fo_scatter(self.h, dst.h, src.h, index.h, dtype, src_map.encode(), key_map.encode(),
+                               dst_map.encode(), idx_map.encode(), int(scaled)))
+
+    def gather(self, dst: "Buffer", src: "Buffer", index: "Buffer", dtype: int, src_map: str, dst_map: str,
+               idx_map: str, scaled: bool):
+        _check(_lib.fo_gather(self.h, dst.h, src.h, index.h, dtype, src_map.encode(), dst_map.encode(),
+                              idx_map.encode(), int(scaled)))
 
     # -- fused chains --
     def rmsnorm_softmax(self, out: "Buffer", x: "Buffer", gain: "Buffer", rows: int, cols: int, eps: float):

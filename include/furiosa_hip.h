@@ -225,6 +225,27 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
 int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
                      const char* dst_map);
 
+/* Backend::scatter (backend/mod.rs:194-200; BufStorage::scatter, storage/buf.rs:485-521): with
+ * payload = Src / Key (carve, then remove_padding) and the indexed axis the first live axis of
+ * Dst / payload (scatter_params, backend/op_prep.rs:45-54), writes
+ *   dst[(p, index[k] / div)] = src[(p, k)]
+ * for every payload position p and key position k; div = payload size * element bytes when
+ * `scaled` (byte offsets of payload blocks), else 1. A repeated index keeps the last key's value,
+ * as the serial loop does. `index` holds i32, at least |Key| cells. An index that is negative or
+ * past the axis returns FO_ERR_INVALID (the reference panics); the valid ones are still written. */
+int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo_buffer* index, fo_dtype t,
+                   const char* src_map, const char* key_map, const char* dst_map, const char* idx_map,
+                   int32_t scaled);
+
+/* Backend::gather (backend/mod.rs:202-207; BufStorage::gather, storage/buf.rs:524-576): with
+ * payload = Dst / Idx and the indexed (table) axis the first live axis of Src / payload
+ * (gather_params, backend/op_prep.rs:78-89), writes
+ *   dst[(p, r)] = src[(p, index[r] / div)]
+ * for every payload position p and index cell r (r walks the index tensor's mapping); dst cells
+ * outside that stream keep their values. Same index decoding and errors as fo_scatter. */
+int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo_buffer* index, fo_dtype t,
+                  const char* src_map, const char* dst_map, const char* idx_map, int32_t scaled);
+
 /* ---- fused chains (each equals a sequence of the seam ops above; fused as a performance
  * contract, with the rounding points of the reference kernels) ------------------------------- */
 

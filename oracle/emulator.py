@@ -284,3 +284,48 @@ def gemm_rows(a: np.ndarray, b: np.ndarray, M: int, N: int, K: int, row_begin: i
 
 def num_threads() -> int:
     return int(lib.ref_num_threads())
+
+
+# ---- scatter / gather (storage/buf.rs:485-576, backend/op_prep.rs:45-89) ---------------------------
+
+
+def _decode(index: np.ndarray, n: int, div: int, axis_size: int) -> np.ndarray:
+    """decode_indices (buf.rs:801-812): raw / div; the reference panics on a negative raw index and
+    on a decoded one past the axis (a slice bound), which here raise IndexError."""
+    raw = np.asarray(index, np.int64)[:n]
+    if np.any(raw < 0):
+        raise IndexError("scatter/gather index must be non-negative")
+    dec = raw // div
+    if np.any(dec >= axis_size):
+        raise IndexError("scatter/gather index past the indexed axis")
+    return dec
+
+
+def scatter(dst, src, index, elem_bytes: int, src_m: dict, key_m: dict, dst_m: dict, idx_m: dict, scaled: bool):
+    """BufStorage::scatter: payload = Src / Key, the indexed dst axis the first live axis of
+    Dst / payload; dst[(p, index[k])] = src[(p, k)] in serial (payload, key) order, so the last
+    key of a repeated index wins."""
+    payload = mr.remove_padding(mr.carve(src_m, key_m))
+    axis = mr.first_axis(mr.carve(dst_m, payload))
+    ks, asz, ps = mr.size(key_m), mr.size(axis), mr.size(payload)
+    dec = _decode(index, ks, ps * elem_bytes if scaled else 1, asz)
+    src_off = mr.stream_offsets(src_m, mr.pair(payload, key_m)).reshape(ps, ks)
+    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, axis)).reshape(ps, asz)
+    out = np.array(dst, copy=True)
+    for k in range(ks):  # ascending k: a later key overwrites an earlier one with the same index
+        out[dst_off[:, dec[k]]] = np.asarray(src)[src_off[:, k]]
+    return out
+
+
+def gather(dst, src, index, elem_bytes: int, src_m: dict, dst_m: dict, idx_m: dict, scaled: bool):
+    """BufStorage::gather: payload = Dst / Idx, the indexed table axis the first live axis of
+    Src / payload; dst[(p, r)] = src[(p, index[r])]; other dst cells keep their values."""
+    payload = mr.remove_padding(mr.carve(dst_m, idx_m))
+    axis = mr.first_axis(mr.carve(src_m, payload))
+    rs, asz, ps = mr.size(idx_m), mr.size(axis), mr.size(payload)
+    dec = _decode(index, rs, ps * elem_bytes if scaled else 1, asz)
+    src_off = mr.stream_offsets(src_m, mr.pair(payload, axis)).reshape(ps, asz)
+    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, idx_m)).reshape(ps, rs)
+    out = np.array(dst, copy=True)
+    out[dst_off] = np.asarray(src)[src_off[:, dec]]
+    return out

@@ -1,4 +1,5 @@
-"""GPU parity of the Backend seam ops (transpose, map/zip/zip3, reduce, contraction, transmute)
+"""GPU parity of the Backend seam ops (transpose, map/zip/zip3, reduce, contraction, transmute,
+scatter/gather)
 against the oracle, through the C ABI. Integer, byte and layout work must match bit for bit; so
 must every f32/bf16 result the GPU folds in the emulator's order (generic contraction, thread-per-
 cell reduce, IEEE elementwise ops). Reassociated float folds use the bf16 tolerance
@@ -369,3 +370,88 @@ def test_transmute(rt, maps):
     out = rt.alloc(mr.size(do) * 4)
     rt.transmute(out, rt.upload(src), I32, fh.m(maps[0], **s), fh.m(maps[1], **s))
     assert np.array_equal(out.read(I32), want)
+
+
+# ---- scatter / gather (storage/buf.rs:485-576) -------------------------------------------------------
+
+
+def test_scatter_reference_config(rt):
+    # scatter_gather_tests.rs:17-51 at its own sizes: K = 512 keys, D = 128, C = 612 cache rows.
+    s = dict(K=512, D=128, C=612)
+    data = emu.f32_to_bf16(np.arange(1, 512 * 128 + 1, dtype=np.float32))
+    index = (np.arange(512, dtype=np.int32) * 128 * 2).astype(np.int32)
+    out = rt.upload(np.zeros(612 * 128, np.uint16))
+    rt.scatter(out, rt.upload(data), rt.upload(index), BF16, fh.m("K, D", **s), fh.m("K", **s), fh.m("C, D", **s),
+               fh.m("K", **s), scaled=True)
+    want = np.zeros(612 * 128, np.uint16)
+    want[:512 * 128] = data
+    assert np.array_equal(out.read(np.uint16), want)
+
+
+@pytest.mark.parametrize("dt,npt", [(I32, np.int32), (I8, np.int8), (BF16, np.uint16)])
+def test_scatter_repeats_last_key_wins(rt, dt, npt):
+    s = dict(K=300, D=24, C=257)
+    rng = np.random.default_rng(43)
+    data = rng.integers(-100, 100, 300 * 24).astype(npt)
+    idx = rng.integers(0, 257, 300).astype(np.int32)  # many repeats
+    init = rng.integers(-100, 100, 257 * 24).astype(npt)
+    maps = [mr.parse(t, s) for t in ("K, D", "K", "C, D", "K")]
+    want = emu.scatter(init, data, idx, np.dtype(npt).itemsize, *maps, scaled=False)
+    out = rt.upload(init)
+    rt.scatter(out, rt.upload(data), rt.upload(idx), dt, *(fh.m(t, **s) for t in ("K, D", "K", "C, D", "K")),
+               scaled=False)
+    assert np.array_equal(out.read(npt), want)
+
+
+GATHER_CASES = [
+    # gather_minimal / gather_unaligned (scatter_gather.rs:72-98): rows of a [K, D] table
+    (dict(K=512, D=128, G=512), "K, D", "G, D", "G", 512, 128 * 2),
+    (dict(K=512, D=128, U=768), "K, D", "U, D", "U", 512, 128 * 2),
+    # gather_paged_kv (:110-121): pool blocks regrouped [NBlocks, PBlock, KvHeads, HeadDim]
+    (dict(NBlocks=16, KvHeads=8, PBlock=16, HeadDim=128), "NBlocks, KvHeads, PBlock, HeadDim",
+     "NBlocks, PBlock, KvHeads, HeadDim", "NBlocks", 16, 16 * 8 * 128 * 2),
+    # gather_scaled_from_raw_index (:156-180): a 2-D index over a [Rows, Width] table
+    (dict(Rows=12, Width=8, IdxRows=16, Indices=128), "Rows, Width", "IdxRows, Indices, Width", "IdxRows, Indices",
+     12, 8 * 2),
+]
+
+
+@pytest.mark.parametrize("case", GATHER_CASES, ids=[c[2] for c in GATHER_CASES])
+def test_gather_reference_shapes(rt, case):
+    s, st, dt_, it, rows, row_bytes = case
+    sm, dm, im = (mr.parse(t, s) for t in (st, dt_, it))
+    rng = np.random.default_rng(44)
+    table = rng.integers(0, 65535, mr.size(sm)).astype(np.uint16)
+    raw = rng.integers(0, rows, mr.size(im)).astype(np.int32)
+    index = (raw * row_bytes).astype(np.int32)
+    init = rng.integers(0, 65535, mr.size(dm)).astype(np.uint16)
+    want = emu.gather(init, table, index, 2, sm, dm, im, scaled=True)
+    out = rt.upload(init)
+    rt.gather(out, rt.upload(table), rt.upload(index), BF16, fh.m(st, **s), fh.m(dt_, **s), fh.m(it, **s), scaled=True)
+    assert np.array_equal(out.read(np.uint16), want)
+
+
+def test_gather_unscaled_i32(rt):
+    s = dict(K=37, D=5, G=70)
+    rng = np.random.default_rng(45)
+    table = rng.integers(-2 ** 31, 2 ** 31 - 1, 37 * 5, dtype=np.int64).astype(np.int32)
+    idx = rng.integers(0, 37, 70).astype(np.int32)
+    out = rt.upload(np.zeros(70 * 5, np.int32))
+    rt.gather(out, rt.upload(table), rt.upload(idx), I32, fh.m("K, D", **s), fh.m("G, D", **s), fh.m("G", **s),
+              scaled=False)
+    assert np.array_equal(out.read(np.int32).reshape(70, 5), table.reshape(37, 5)[idx])
+
+
+@pytest.mark.parametrize("bad", [-1, 37])
+def test_scatter_gather_bad_index_is_an_error(rt, bad):
+    s = dict(K=37, D=5, G=4)
+    idx = rt.upload(np.array([0, 3, bad, 1], np.int32))
+    out = rt.upload(np.zeros(4 * 5, np.int32))
+    with pytest.raises(fh.FoError, match="index"):
+        rt.gather(out, rt.upload(np.zeros(37 * 5, np.int32)), idx, I32, fh.m("K, D", **s), fh.m("G, D", **s),
+                  fh.m("G", **s), scaled=False)
+    s2 = dict(G=4, D=5, K=37)
+    cache = rt.upload(np.zeros(37 * 5, np.int32))
+    with pytest.raises(fh.FoError, match="index"):
+        rt.scatter(cache, rt.upload(np.ones(4 * 5, np.int32)), idx, I32, fh.m("G, D", **s2), fh.m("G", **s2),
+                   fh.m("K, D", **s2), fh.m("G", **s2), scaled=False)

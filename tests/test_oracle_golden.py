@@ -327,3 +327,65 @@ def test_factors_match_cells(case):
     assert np.array_equal(live, st == mr.LIVE)
     for s in c:
         assert np.array_equal(coord[s][live], c[s][live])
+
+
+# ---- scatter / gather (storage/buf.rs:485-576) ----------------------------------------------------
+
+
+def test_scatter_reference_known_answer():
+    # scatter_gather_tests.rs:17-51: data[K, D] = bf16(1 .. K*D) scattered with byte-offset indices
+    # k * D * 2 into a zero cache[C, D]; the first K rows hold the data, the rest stays zero.
+    s = dict(K=512, D=128, C=612)
+    data = emu.f32_to_bf16(np.arange(1, 512 * 128 + 1, dtype=np.float32))
+    index = (np.arange(512, dtype=np.int32) * 128 * 2).astype(np.int32)
+    out = emu.scatter(np.zeros(612 * 128, np.uint16), data, index, 2, M("K, D", **s), M("K", **s), M("C, D", **s),
+                      M("K", **s), scaled=True)
+    want = np.zeros(612 * 128, np.uint16)
+    want[:512 * 128] = data
+    assert np.array_equal(out, want)
+
+
+def test_scatter_closed_form_with_repeats():
+    # index_put along dim 0 (the torch form in scatter_gather_tests.rs:3-11); a repeated index
+    # keeps the later key's row, as the serial loop writes in key order.
+    s = dict(K=40, D=6, C=50)
+    rng = np.random.default_rng(41)
+    data = rng.integers(0, 1000, 40 * 6).astype(np.int32)
+    idx = rng.integers(0, 50, 40).astype(np.int32)
+    out = emu.scatter(np.full(50 * 6, -1, np.int32), data, idx, 4, M("K, D", **s), M("K", **s), M("C, D", **s),
+                      M("K", **s), scaled=False)
+    want = np.full((50, 6), -1, np.int32)
+    for k in range(40):
+        want[idx[k]] = data.reshape(40, 6)[k]
+    assert np.array_equal(out.reshape(50, 6), want)
+
+
+def test_gather_closed_forms():
+    rng = np.random.default_rng(42)
+    # table[K, D] rows picked by a scaled index (gather_minimal, scatter_gather.rs:72-85)
+    s = dict(K=64, D=8, G=96)
+    table = rng.integers(0, 60000, 64 * 8).astype(np.uint16)
+    rows = rng.integers(0, 64, 96).astype(np.int32)
+    out = emu.gather(np.zeros(96 * 8, np.uint16), table, rows * 8 * 2, 2, M("K, D", **s), M("G, D", **s),
+                     M("G", **s), scaled=True)
+    assert np.array_equal(out.reshape(96, 8), table.reshape(64, 8)[rows])
+    # paged KV pool [NBlocks, KvHeads, PBlock, HeadDim] gathered by block into
+    # [NBlocks, PBlock, KvHeads, HeadDim] (gather_paged_kv, scatter_gather.rs:110-121)
+    s = dict(NBlocks=4, KvHeads=2, PBlock=3, HeadDim=5)
+    pool = rng.integers(0, 60000, 4 * 2 * 3 * 5).astype(np.uint16)
+    blocks = np.array([2, 0, 3, 2], np.int32)
+    out = emu.gather(np.zeros(pool.size, np.uint16), pool, blocks * (3 * 2 * 5) * 2, 2,
+                     M("NBlocks, KvHeads, PBlock, HeadDim", **s), M("NBlocks, PBlock, KvHeads, HeadDim", **s),
+                     M("NBlocks", **s), scaled=True)
+    want = pool.reshape(4, 2, 3, 5)[blocks].transpose(0, 2, 1, 3)
+    assert np.array_equal(out.reshape(4, 3, 2, 5), want)
+
+
+def test_scatter_gather_bad_index_raises():
+    s = dict(K=4, D=2, C=5)
+    with pytest.raises(IndexError):
+        emu.scatter(np.zeros(10, np.int32), np.zeros(8, np.int32), np.array([0, 1, -4, 2], np.int32), 4,
+                    M("K, D", **s), M("K", **s), M("C, D", **s), M("K", **s), scaled=False)
+    with pytest.raises(IndexError):
+        emu.gather(np.zeros(8, np.int32), np.zeros(10, np.int32), np.array([0, 5, 1, 2], np.int32), 4,
+                   M("C, D", **s), M("K, D", **s), M("K", **s), scaled=False)
