@@ -132,6 +132,34 @@ def bench_relayout(fh, rt, steps, warmup, rng):
     return out
 
 
+def bench_scatter_gather(fh, rt, steps, warmup, rng):
+    """Backend::gather / scatter at KV-cache scale (the shapes of scatter_gather.rs, enlarged):
+    a paged-KV gather of every block of a [NBlocks=2048, KvHeads=8, PBlock=16, HeadDim=128] bf16
+    pool in a permuted order (64 MiB each way), and a row scatter of [K=131072, D=128] bf16 into a
+    [C=163840, D] cache through a permuted subset of rows (32 MiB each way). Scaled indices."""
+    out = {}
+    s = dict(NBlocks=2048, KvHeads=8, PBlock=16, HeadDim=128)
+    n = 2048 * 8 * 16 * 128
+    pool = rt.upload(rng.integers(0, 65535, n, dtype=np.uint16))
+    dst = rt.alloc(n * 2)
+    blocks = rt.upload((rng.permutation(2048) * (16 * 8 * 128 * 2)).astype(np.int32))
+    maps = [fh.m(t, **s) for t in ("NBlocks, KvHeads, PBlock, HeadDim", "NBlocks, PBlock, KvHeads, HeadDim", "NBlocks")]
+    fn = lambda: rt.gather(dst, pool, blocks, fh.BF16, *maps, scaled=True)
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 2 * n * 2 + 2048 * 4
+    out["gather_paged_kv"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    s = dict(K=131072, D=128, C=163840)
+    data = rt.upload(rng.integers(0, 65535, 131072 * 128, dtype=np.uint16))
+    cache = rt.alloc(163840 * 128 * 2)
+    rows = rt.upload((rng.permutation(163840)[:131072] * (128 * 2)).astype(np.int32))
+    maps = [fh.m(t, **s) for t in ("K, D", "K", "C, D", "K")]
+    fn = lambda: rt.scatter(cache, data, rows, fh.BF16, *maps, scaled=True)
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 2 * 131072 * 128 * 2 + 131072 * 4
+    out["scatter_rows"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    return out
+
+
 def bench_mlp(fh, rt, steps, warmup, rng):
     B, I, Hd, O = 64, 784, 128, 10
     x = rt.upload(f32_to_bf16(rng.uniform(0, 1, B * I).astype(np.float32)))
@@ -187,7 +215,8 @@ def main():
     only = set(filter(None, args.only.split(",")))
     res = {}
     for name, fnb in (("gemm", bench_gemm), ("norm", bench_norm), ("attention", bench_attention),
-                      ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout)):
+                      ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout),
+                      ("scatter_gather", bench_scatter_gather)):
         if only and name not in only:
             continue
         res[name] = fnb(fh, rt, args.steps, args.warmup, rng)
@@ -210,6 +239,9 @@ def main():
     if "mlp" in res:
         r = res["mlp"]
         configs["mlp_64x784x128x10"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)
+    if "scatter_gather" in res:
+        for k, r in res["scatter_gather"].items():
+            configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     if "relayout" in res:
         for k, r in res["relayout"].items():
             configs[f"relayout_{k}_8192x8192_bf16"] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"],

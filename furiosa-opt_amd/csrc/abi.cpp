@@ -101,12 +101,41 @@ void* scratch(fo_runtime* rt, uint64_t bytes) {
   return rt->scratch;
 }
 
+// The runtime's device-visible error word (pinned host memory, written by kernels only when an
+// op's data is invalid). Returns its device address; `take_error` reads and clears it after the
+// stream has drained.
+int32_t* error_word(fo_runtime* rt) {
+  if (!rt->err_host) {
+    void* h = nullptr;
+    FO_HIP(hipHostMalloc(&h, sizeof(int32_t), hipHostMallocMapped));
+    rt->err_host = (int32_t*)h;
+    *rt->err_host = 0;
+    void* d = nullptr;
+    FO_HIP(hipHostGetDevicePointer(&d, h, 0));
+    rt->err_dev = (int32_t*)d;
+  }
+  return rt->err_dev;
+}
+int32_t take_error(fo_runtime* rt) {
+  FO_HIP(hipStreamSynchronize(rt->stream));
+  int32_t e = __atomic_load_n(rt->err_host, __ATOMIC_ACQUIRE);
+  if (e) __atomic_store_n(rt->err_host, 0, __ATOMIC_RELEASE);
+  return e;
+}
+
 // Shared set-up of scatter / gather: the stream wheels of one side, all digits live.
 std::vector<fm::Wheel> stream_wheels(const fm::Factors& memory, const fm::Factors& outer, const fm::Factors& inner,
                                      const char* what) {
   fm::Joint j = fm::sequence({memory}, {outer, inner}, fm::Mode::Read);
   for (auto& w : j.wheels) require(w.live == w.size, std::string(what) + ": padded streams are not supported");
   return j.wheels;
+}
+
+// Number of innermost wheels from the inner stream part (part 1): the outer part's follow them.
+int inner_part_wheels(const std::vector<fm::Wheel>& ws) {
+  int n = 0;
+  while (n < (int)ws.size() && ws[n].part == 1) ++n;
+  return n;
 }
 
 int64_t product(const std::vector<fm::Wheel>& ws) {
@@ -154,6 +183,7 @@ void fo_runtime_free(fo_runtime* rt) {
   for (auto& e : rt->events)
     if (e) (void)hipEventDestroy(e);
   if (rt->scratch) (void)hipFree(rt->scratch);
+  if (rt->err_host) (void)hipHostFree(rt->err_host);
   if (rt->stream) (void)hipStreamDestroy(rt->stream);
   delete rt;
 }
@@ -466,17 +496,13 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     require(div < (1ll << 31), "scatter: payload block too large");
     if (np * keys == 0) return;
     set_device(rt);
-    int32_t* win = (int32_t*)scratch(rt, (uint64_t)(axis_size + 1) * 4);
-    int32_t* flag = win + axis_size;
+    int32_t* flag = error_word(rt);
+    int32_t* win = (int32_t*)scratch(rt, (uint64_t)axis_size * 4);
     FO_HIP(hipMemsetAsync(win, 0xff, (size_t)axis_size * 4, rt->stream));  // -1: no key yet
-    FO_HIP(hipMemsetAsync(flag, 0, 4, rt->stream));
     const int mem[1] = {0};
     launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,
-                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), win, flag);
-    int32_t bad = 0;
-    FO_HIP(hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, rt->stream));
-    FO_HIP(hipStreamSynchronize(rt->stream));
-    require(bad == 0, "scatter: an index is negative or past the scatter axis");
+                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), win, flag);
+    require(take_error(rt) == 0, "scatter: an index is negative or past the scatter axis");
   });
 }
 
@@ -508,15 +534,11 @@ int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo
     require(div < (1ll << 31), "gather: payload block too large");
     if (np * slots == 0) return;
     set_device(rt);
-    int32_t* flag = (int32_t*)scratch(rt, 4);
-    FO_HIP(hipMemsetAsync(flag, 0, 4, rt->stream));
+    int32_t* flag = error_word(rt);
     const int mem[1] = {0};
     launch_gather(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, slots, axis_size, (int32_t)div,
-                  to_desc<1>(ws, mem), to_desc<1>(wd, mem), flag);
-    int32_t bad = 0;
-    FO_HIP(hipMemcpyAsync(&bad, flag, 4, hipMemcpyDeviceToHost, rt->stream));
-    FO_HIP(hipStreamSynchronize(rt->stream));
-    require(bad == 0, "gather: an index is negative or past the gathered axis");
+                  to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), flag);
+    require(take_error(rt) == 0, "gather: an index is negative or past the gathered axis");
   });
 }
 

@@ -335,6 +335,56 @@ __global__ void __launch_bounds__(kBlock) k_gather(T* __restrict__ dst, const T*
   }
 }
 
+// 16-byte form: the innermost payload wheel is contiguous in both memories and a whole number of
+// V-element chunks, so payload positions c*V .. c*V+V-1 are adjacent on both sides. Thread (r, c)
+// moves chunk c of slot r; consecutive threads take consecutive chunks of one row.
+template <int V>
+__global__ void __launch_bounds__(kBlock) k_gather_vec(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                       int64_t eb, const int32_t* __restrict__ idx, uint32_t total,
+                                                       FastDiv cdiv, uint32_t slots, uint32_t axis_size, int32_t div,
+                                                       Wheels<1> ws, Wheels<1> wd, int32_t* __restrict__ flag) {
+  typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
+  for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
+    uint32_t r = cdiv.div(t), c = t - r * cdiv.d;
+    int32_t a = decode_index(idx, r, div, axis_size);
+    if (a < 0) {
+      *flag = 1;
+      continue;
+    }
+    const uint32_t p = c * V;
+    *(vec_t*)(dst + wheel_offset(wd, p * slots + r) * eb) =
+        *(const vec_t*)(src + wheel_offset(ws, p * axis_size + (uint32_t)a) * eb);
+  }
+}
+
+template <int V>
+__global__ void __launch_bounds__(kBlock) k_scatter_vec(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                        int64_t eb, const int32_t* __restrict__ idx,
+                                                        const int32_t* __restrict__ win, uint32_t total, FastDiv cdiv,
+                                                        uint32_t keys, uint32_t axis_size, int32_t div, Wheels<1> ws,
+                                                        Wheels<1> wd) {
+  typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
+  for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
+    uint32_t k = cdiv.div(t), c = t - k * cdiv.d;
+    int32_t a = decode_index(idx, k, div, axis_size);
+    if (a < 0 || win[a] != (int32_t)k) continue;
+    const uint32_t p = c * V;
+    *(vec_t*)(dst + wheel_offset(wd, p * axis_size + (uint32_t)a) * eb) =
+        *(const vec_t*)(src + wheel_offset(ws, p * keys + k) * eb);
+  }
+}
+
+// Whether payload positions come in adjacent 16-byte runs on both sides: the innermost payload
+// wheel (part 0) has stride 1 and a multiple of V digits, every other stride is a multiple of V.
+bool payload_vec_ok(const Wheels<1>& w, int inner_slot_wheels, int V) {
+  if (inner_slot_wheels >= w.n) return false;
+  const int i0 = inner_slot_wheels;  // wheels are innermost-first: slot / axis wheels come first
+  if (w.stride[0][i0] != 1 || w.size[i0] % V != 0 || w.live[i0] != w.size[i0]) return false;
+  for (int i = 0; i < w.n; ++i)
+    if (i != i0 && w.stride[0][i] % V != 0) return false;
+  return true;
+}
+
 // win[a] = the last key slot whose index is a: the serial scatter's last write wins.
 __global__ void __launch_bounds__(kBlock) k_scatter_winners(const int32_t* __restrict__ idx, uint32_t keys,
                                                             uint32_t axis_size, int32_t div, int32_t* __restrict__ win,
@@ -927,7 +977,25 @@ namespace fo {
 
 void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                    int64_t payload, int64_t slots, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                   const Wheels<1>& wd, int32_t* flag) {
+                   const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* flag) {
+  const int V = (int)(16 / elem_bytes);
+  if (((uintptr_t)dst | (uintptr_t)src) % 16 == 0 && payload_vec_ok(ws, ws_slot_wheels, V) &&
+      payload_vec_ok(wd, wd_slot_wheels, V)) {
+    const uint32_t nch = (uint32_t)(payload / V), total = (uint32_t)(nch * slots);
+    dim3 g(grid_for(total)), b(kBlock);
+    const FastDiv cdiv(nch);
+    if (V == 8)
+      hipLaunchKernelGGL(k_gather_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, total, cdiv,
+                         (uint32_t)slots, (uint32_t)axis_size, div, ws, wd, flag);
+    else if (V == 4)
+      hipLaunchKernelGGL(k_gather_vec<4>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, total, cdiv,
+                         (uint32_t)slots, (uint32_t)axis_size, div, ws, wd, flag);
+    else
+      hipLaunchKernelGGL(k_gather_vec<16>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, total,
+                         cdiv, (uint32_t)slots, (uint32_t)axis_size, div, ws, wd, flag);
+    FO_HIP(hipGetLastError());
+    return;
+  }
   const uint32_t total = (uint32_t)(payload * slots);
   dim3 g(grid_for(total)), b(kBlock);
   const FastDiv rdiv((uint32_t)slots);
@@ -952,10 +1020,28 @@ void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx
 
 void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                     int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                    const Wheels<1>& wd, int32_t* win, int32_t* flag) {
+                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* win, int32_t* flag) {
   hipLaunchKernelGGL(k_scatter_winners, dim3(grid_for(keys)), dim3(kBlock), 0, s, idx, (uint32_t)keys,
                      (uint32_t)axis_size, div, win, flag);
   FO_HIP(hipGetLastError());
+  const int V = (int)(16 / elem_bytes);
+  if (((uintptr_t)dst | (uintptr_t)src) % 16 == 0 && payload_vec_ok(ws, ws_slot_wheels, V) &&
+      payload_vec_ok(wd, wd_slot_wheels, V)) {
+    const uint32_t nch = (uint32_t)(payload / V), total = (uint32_t)(nch * keys);
+    dim3 g(grid_for(total)), b(kBlock);
+    const FastDiv cdiv(nch);
+    if (V == 8)
+      hipLaunchKernelGGL(k_scatter_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, total,
+                         cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+    else if (V == 4)
+      hipLaunchKernelGGL(k_scatter_vec<4>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, total,
+                         cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+    else
+      hipLaunchKernelGGL(k_scatter_vec<16>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win,
+                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+    FO_HIP(hipGetLastError());
+    return;
+  }
   const uint32_t total = (uint32_t)(payload * keys);
   dim3 g(grid_for(total)), b(kBlock);
   const FastDiv kdiv((uint32_t)keys);

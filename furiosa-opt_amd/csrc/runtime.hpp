@@ -21,6 +21,8 @@ struct fo_runtime {
   std::string arch;
   void* scratch = nullptr;  // device scratch for ops that need working memory (grown on demand)
   uint64_t scratch_bytes = 0;
+  int32_t* err_host = nullptr;  // pinned, device-mapped error word: kernels set it only on failure
+  int32_t* err_dev = nullptr;   // its device address
 };
 
 struct fo_buffer {
@@ -92,14 +94,16 @@ Wheels<NMEM> to_desc(const std::vector<mapping::Wheel>& ws, const int (&mem)[NME
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_base, int64_t src_base,
                      int64_t count, const Wheels<1>& w);
 // Gather: dst[off_d(p*slots + r)] = src[off_s(p*axis + index[r] / div)]; bad indices skipped, *flag = 1.
+// `*_slot_wheels`: how many innermost wheels of each list belong to the slot / axis part (the
+// payload's wheels follow), for the 16-byte payload path.
 void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                    int64_t payload, int64_t slots, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                   const Wheels<1>& wd, int32_t* flag);
+                   const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* flag);
 // Scatter: dst[off_d(p*axis + index[k] / div)] = src[off_s(p*keys + k)], the last key k winning a
 // repeated index (win: axis_size i32 set to -1 beforehand); bad indices skipped, *flag = 1.
 void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                     int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                    const Wheels<1>& wd, int32_t* win, int32_t* flag);
+                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* win, int32_t* flag);
 // Transmute: dst live rank k <- src live rank k; dst padding zeroed.
 void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_count,
                       const Wheels<1>& dst_self, const Wheels<1>& src_self);
