@@ -30,6 +30,7 @@ sys.path.insert(0, str(ROOT / "furiosa-opt_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_I8_TOPS = 5000.0      # MI355X dense int8 MFMA
+PEAK_F8_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 
 
@@ -78,6 +79,25 @@ def bench_gemm(fh, rt, steps, warmup, rng):
     flop = 2.0 * M * N * K
     tflops = flop / (ev * 1e-3) / 1e12
     return dict(ms=ev, wall_ms=wall, tflops=tflops, flop=flop, bytes=3 * M * N * 2)
+
+
+def bench_gemm_f8(fh, rt, steps, warmup, rng):
+    """The same mapped 4096^3 contraction over f8e4m3 operands (ContractionCast: f32 accumulate),
+    with the f32 result (contract_outer's widened path) and with the one f8e4m3 narrow per cell."""
+    M = N = K = 4096
+    s = dict(M=M, N=N, K=K)
+    # f8e4m3 codes with a random sign, exponent field 4..9 (magnitudes 2^-3 .. 2^2.9) and mantissa
+    codes = lambda n: ((rng.integers(0, 2, n) << 7) | (rng.integers(4, 10, n) << 3) | rng.integers(0, 8, n)).astype(np.uint8)
+    a, b = rt.upload(codes(M * K)), rt.upload(codes(N * K))
+    maps = [fh.m(t, **s) for t in ("M / 8, M % 8, K", "N, K", "M / 8, M % 8, N, K", "M / 8, M % 8, N")]
+    out = {}
+    for name, out_t, ob in (("f32", fh.F32, 4), ("f8e4m3", fh.F8E4M3, 1)):
+        c = rt.alloc(M * N * ob)
+        fn = lambda: rt.contraction(c, a, b, fh.F8E4M3, out_t, *maps)
+        wall, ev = timed(rt, fn, steps, warmup)
+        flop = 2.0 * M * N * K
+        out[name] = dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=2 * M * K + M * N * ob)
+    return out
 
 
 def bench_norm(fh, rt, steps, warmup, rng):
@@ -214,7 +234,8 @@ def main():
     rng = np.random.default_rng(0)
     only = set(filter(None, args.only.split(",")))
     res = {}
-    for name, fnb in (("gemm", bench_gemm), ("norm", bench_norm), ("attention", bench_attention),
+    for name, fnb in (("gemm", bench_gemm), ("gemm_f8", bench_gemm_f8), ("norm", bench_norm),
+                      ("attention", bench_attention),
                       ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout),
                       ("scatter_gather", bench_scatter_gather)):
         if only and name not in only:
@@ -236,6 +257,10 @@ def main():
         r = res["w8a8"]
         configs["w8a8_2048x8192x8192"] = dict(value=r["tops"], unit="TOP/s", ms=r["ms"],
                                               roofline_frac=r["tops"] / PEAK_I8_TOPS)
+    if "gemm_f8" in res:
+        for k, r in res["gemm_f8"].items():
+            configs[f"mapped_gemm_4096_f8e4m3_to_{k}"] = dict(value=r["tflops"], unit="TFLOP/s", ms=r["ms"],
+                                                            roofline_frac=r["tflops"] / PEAK_F8_TFLOPS)
     if "mlp" in res:
         r = res["mlp"]
         configs["mlp_64x784x128x10"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)

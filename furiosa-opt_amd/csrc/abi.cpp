@@ -585,7 +585,8 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     check_buf(rhs, "rhs");
     bool ok_types = (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
                     (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32)) || (in_t == FO_F32 && out_t == FO_F32) ||
-                    (in_t == FO_I32 && out_t == FO_I32);
+                    (in_t == FO_I32 && out_t == FO_I32) ||
+                    ((in_t == FO_F8E4M3 || in_t == FO_F8E5M2) && (out_t == in_t || out_t == FO_F32));
     require(ok_types, "contraction: unsupported operand/output dtype pair");
     fm::Factors l = flat(lhs_map, "lhs_map"), r = flat(rhs_map, "rhs_map");
     fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");

@@ -5,7 +5,9 @@
 //
 // Tiling (gfx950, wave64): a block of WM x WN waves owns a BM x BN tile; each wave owns
 // (BM/WM) x (BN/WN) as a grid of 32x32 MFMA tiles (v_mfma_f32_32x32x16_bf16 /
-// v_mfma_i32_32x32x32_i8). K advances kRB bytes per stage; kNS stages rotate through LDS. The
+// v_mfma_i32_32x32x32_i8 / v_mfma_f32_32x32x64_f8f6f4 for the two 8-bit float formats, OCP E4M3
+// and E5M2, the encodings of f8e4m3 / f8e5m2). K advances kRB bytes per stage; kNS stages rotate
+// through LDS. The
 // DMA refilling a buffer is issued right after the barrier that releases it, and each stage waits
 // only for its own DMA (vmcnt counts the younger ones).
 //
@@ -33,6 +35,7 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16_t;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2_t;
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8_t;
 
 constexpr int kRB = 128;  // K bytes per row per stage (four 32-byte MFMA k-steps)
 constexpr int kNS = 2;    // LDS stages (double buffer; 64-byte stages x4 measured slower: more barriers)
@@ -43,21 +46,51 @@ constexpr int kSwzShift = kRB == 64 ? 2 : 1;    // rows sharing a bank-group off
 // s_waitcnt immediate (gfx9 encoding): vector memory count <= n, LDS/scalar count 0, export any.
 constexpr int waitcnt_vm_lgkm0(int n) { return (n & 15) | (7 << 4) | ((n >> 4) << 14); }
 
-template <bool IS_I8>
+// Operand kinds. Per MFMA, each lane supplies FRAG bytes of k (16 for bf16 / i8, 32 for the
+// 8-bit floats: k = 64 per instruction); KSTEP = 2 * FRAG bytes of k per row per MFMA.
+enum Kind { kBf16 = 0, kI8 = 1, kF8E4M3 = 2, kF8E5M2 = 3 };
+
+template <int KIND>
 struct MfmaT;
 template <>
-struct MfmaT<false> {
+struct MfmaT<kBf16> {
   using acc_t = f32x16_t;
-  static __device__ __forceinline__ acc_t mma(const i32x4_t& a, const i32x4_t& b, const acc_t& c) {
+  using frag_t = i32x4_t;
+  static constexpr int EB = 2;
+  static __device__ __forceinline__ acc_t mma(const frag_t& a, const frag_t& b, const acc_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
                                                    0, 0, 0);
   }
 };
 template <>
-struct MfmaT<true> {
+struct MfmaT<kI8> {
   using acc_t = i32x16_t;
-  static __device__ __forceinline__ acc_t mma(const i32x4_t& a, const i32x4_t& b, const acc_t& c) {
+  using frag_t = i32x4_t;
+  static constexpr int EB = 1;
+  static __device__ __forceinline__ acc_t mma(const frag_t& a, const frag_t& b, const acc_t& c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+// The f8f6f4 instruction with both operand formats set (cbsz / blgp: 0 = E4M3, 1 = E5M2) and no
+// block scale. It sums a 64-wide k block at reduced internal precision: measured on MI355X, the
+// error of one instruction is about 2e-5 of sum |a_k b_k| on average, 1.6e-4 at most (an f32
+// sequential fold: 3e-7), the products themselves being exact.
+template <>
+struct MfmaT<kF8E4M3> {
+  using acc_t = f32x16_t;
+  using frag_t = i32x8_t;
+  static constexpr int EB = 1;
+  static __device__ __forceinline__ acc_t mma(const frag_t& a, const frag_t& b, const acc_t& c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  }
+};
+template <>
+struct MfmaT<kF8E5M2> {
+  using acc_t = f32x16_t;
+  using frag_t = i32x8_t;
+  static constexpr int EB = 1;
+  static __device__ __forceinline__ acc_t mma(const frag_t& a, const frag_t& b, const acc_t& c) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 1, 1, 0, 0, 0, 0);
   }
 };
 
@@ -95,12 +128,25 @@ template <>
 struct OutT<4> {
   using T = uint16_t;
 };
+template <>
+struct OutT<5> {
+  using T = uint8_t;
+};
+template <>
+struct OutT<6> {
+  using T = uint8_t;
+};
 
 // OUT: 0 = bf16 (from f32), 1 = f32, 2 = i8 (wrap), 3 = i32,
-//      4 = W8A8 dequant: bf16(fixedpoint_to_float(acc, 31) * scale[col]) (+ optional raw i32)
-template <bool IS_I8, int OUT>
-__device__ __forceinline__ typename OutT<OUT>::T convert_out(typename MfmaT<IS_I8>::acc_t const& a, int v, float sc) {
-  if constexpr (OUT == 0) {
+//      4 = W8A8 dequant: bf16(fixedpoint_to_float(acc, 31) * scale[col]) (+ optional raw i32),
+//      5 = f8e4m3 (from f32), 6 = f8e5m2 (from f32)
+template <int KIND, int OUT>
+__device__ __forceinline__ typename OutT<OUT>::T convert_out(typename MfmaT<KIND>::acc_t const& a, int v, float sc) {
+  if constexpr (OUT == 5) {
+    return f32_to_f8e4m3(a[v]);
+  } else if constexpr (OUT == 6) {
+    return f32_to_f8e5m2(a[v]);
+  } else if constexpr (OUT == 0) {
     return f32_to_bf16(a[v]);
   } else if constexpr (OUT == 1) {
     return a[v];
@@ -125,13 +171,16 @@ __device__ __forceinline__ void* uniform_ptr(const void* p) {
 }
 __device__ __forceinline__ int uniform_i32(int64_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
 
-template <bool IS_I8, int OUT, int BM, int BN, int WM, int WN>
+template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
-  using M = MfmaT<IS_I8>;
+  using M = MfmaT<KIND>;
   using acc_t = typename M::acc_t;
+  using frag_t = typename M::frag_t;
   using out_t = typename OutT<OUT>::T;
   constexpr int W = WM * WN;
-  constexpr int EB = IS_I8 ? 1 : 2;            // element bytes
+  constexpr int EB = M::EB;                    // element bytes
+  constexpr int FRAG = (int)sizeof(frag_t);    // k bytes per lane per MFMA
+  constexpr int KSTEP = 2 * FRAG;              // k bytes per row per MFMA
   constexpr int TWM = BM / WM, TWN = BN / WN;  // wave tile
   constexpr int TM = TWM / 32, TN = TWN / 32;
   constexpr int A_CH = BM / kRPC / W;  // 1 KiB DMA chunks of A per wave per stage
@@ -218,16 +267,16 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
-  // Fragment reads: lane (frow, half) takes 16 bytes of k-step kk at chunk 2kk + half of row
-  // frow (+ 32i), found at slot (2kk + half) ^ swz; rows of a fragment tile start at multiples
-  // of 32, so swz depends on frow only.
+  // Fragment reads: lane (frow, half) takes FRAG bytes of k-step kk: the 16-byte chunks
+  // (KSTEP / 16) kk + (FRAG / 16) half + e of row frow (+ 32i), found at slot chunk ^ swz; rows of
+  // a fragment tile start at multiples of 32, so swz depends on frow only.
   const int frow = lane & 31, half = lane >> 5;
   const int swz = (frow >> kSwzShift) & (kCPR - 1);
   const int a_row = (wm * TWM + frow) * kRB, b_row = (wn * TWN + frow) * kRB;
-  auto slot = [&](int kk) { return ((2 * kk + half) ^ swz) * 16; };
+  auto slot = [&](int kk, int e) { return (((KSTEP / 16) * kk + (FRAG / 16) * half + e) ^ swz) * 16; };
 
   const int nst = (int)((KB + kRB - 1) / kRB);
-  constexpr int KST = kRB / 32;  // MFMA k-steps per stage
+  constexpr int KST = kRB / KSTEP;  // MFMA k-steps per stage
   static_assert(KST % 2 == 0, "fragment double-buffer parity assumes an even k-step count");
   // Stage s's DMA is complete once at most the younger stages' DMAs are outstanding; after the
   // barrier every wave's is, and every wave has its fragments of the previous stage in registers,
@@ -249,14 +298,30 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
     __builtin_amdgcn_s_barrier();
     __asm__ volatile("" ::: "memory");
   };
-  i32x4_t fa[2][TM], fb[2][TN];
+  frag_t fa[2][TM], fb[2][TN];
   auto read_frags = [&](int buf, int kk, int p) {
     const uint8_t* a_s = sA(buf);
     const uint8_t* b_s = sB(buf);
 #pragma unroll
-    for (int i = 0; i < TM; ++i) fa[p][i] = *(const i32x4_t*)(a_s + a_row + i * 32 * kRB + slot(kk));
+    for (int i = 0; i < TM; ++i) {
+      const uint8_t* r = a_s + a_row + i * 32 * kRB;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) fb[p][j] = *(const i32x4_t*)(b_s + b_row + j * 32 * kRB + slot(kk));
+      for (int e = 0; e < FRAG / 16; ++e) {
+        i32x4_t q = *(const i32x4_t*)(r + slot(kk, e));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) fa[p][i][4 * e + w] = q[w];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t* r = b_s + b_row + j * 32 * kRB;
+#pragma unroll
+      for (int e = 0; e < FRAG / 16; ++e) {
+        i32x4_t q = *(const i32x4_t*)(r + slot(kk, e));
+#pragma unroll
+        for (int w = 0; w < 4; ++w) fb[p][j][4 * e + w] = q[w];
+      }
+    }
   };
 
 #pragma unroll
@@ -313,7 +378,7 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
           }
           out_t o4[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o4[e] = convert_out<IS_I8, OUT>(acc[i][j], vg * 4 + e, sc[e]);
+          for (int e = 0; e < 4; ++e) o4[e] = convert_out<KIND, OUT>(acc[i][j], vg * 4 + e, sc[e]);
           int64_t off = cb + row * g.ldc_m + col;
           if constexpr (OB == 1) {
             *(uint32_t*)(C + off) = __builtin_bit_cast(uint32_t, o4);
@@ -336,7 +401,7 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
             if (col + e >= g.N) continue;
             if constexpr (OUT == 4) sc[e] = g.scale[col + e];
             int64_t off = cb + row * g.ldc_m + (col + e) * g.ldc_n;
-            C[off] = convert_out<IS_I8, OUT>(acc[i][j], vg * 4 + e, sc[e]);
+            C[off] = convert_out<KIND, OUT>(acc[i][j], vg * 4 + e, sc[e]);
             if constexpr (OUT == 4) {
               if (g.acc_out) g.acc_out[off] = (int32_t)acc[i][j][vg * 4 + e];
             }
@@ -346,7 +411,7 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   }
 }
 
-template <bool IS_I8, int OUT, int BM, int BN, int WM, int WN>
+template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b, const float* scale,
                      int32_t* acc_out) {
   GemmArgs g;
@@ -370,12 +435,12 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   size_t lds = (size_t)kNS * (BM + BN) * kRB;
   static bool attr_set = false;  // gfx950 LDS is 160 KiB; dynamic LDS above 64 KiB must be opted into
   if (!attr_set) {
-    FO_HIP(hipFuncSetAttribute((const void*)k_gemm<IS_I8, OUT, BM, BN, WM, WN>,
+    FO_HIP(hipFuncSetAttribute((const void*)k_gemm<KIND, OUT, BM, BN, WM, WN>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     attr_set = true;
   }
   dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)d.batch);
-  hipLaunchKernelGGL((k_gemm<IS_I8, OUT, BM, BN, WM, WN>), grid, dim3(64 * WM * WN), lds, s, g);
+  hipLaunchKernelGGL((k_gemm<KIND, OUT, BM, BN, WM, WN>), grid, dim3(64 * WM * WN), lds, s, g);
   FO_HIP(hipGetLastError());
 }
 
@@ -383,7 +448,7 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
 // when the problem is large, 128x128 otherwise (measured best on MI355X among 128, 256 with 4, 8
 // and 16 waves). FO_GEMM_TILE overrides it for measurement: 128, 256 (4 waves of 128x128),
 // 2568 (8 waves of 128x64) or 25616 (16 waves).
-template <bool IS_I8, int OUT>
+template <int KIND, int OUT>
 void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b,
                  const float* scale = nullptr, int32_t* acc_out = nullptr) {
   static int forced = [] {
@@ -392,16 +457,16 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
   }();
   int64_t tiles256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
   int choice = forced ? forced : (tiles256 >= 128 ? 25616 : 128);
-  if (choice == 2568) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
-  if (choice == 25616) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
-  if (choice == 256) return gemm_launch_cfg<IS_I8, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);
-  return gemm_launch_cfg<IS_I8, OUT, 128, 128, 2, 2>(s, d, c, a, b, scale, acc_out);
+  if (choice == 2568) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
+  if (choice == 25616) return gemm_launch_cfg<KIND, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
+  if (choice == 256) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);
+  return gemm_launch_cfg<KIND, OUT, 128, 128, 2, 2>(s, d, c, a, b, scale, acc_out);
 }
 
 }  // namespace
 
 bool gemm_aligned(const void* a, const void* b, fo_dtype in_t, const GemmDesc& d) {
-  int64_t eb = in_t == FO_I8 ? 1 : 2;
+  int64_t eb = dtype_bytes(in_t);
   return ((uintptr_t)a % 16) == 0 && ((uintptr_t)b % 16) == 0 && (d.lda * eb) % 16 == 0 && (d.ldb * eb) % 16 == 0 &&
          (d.K * eb) % 16 == 0 && (d.a_batch * eb) % 16 == 0 && (d.b_batch * eb) % 16 == 0 && d.M < (1ll << 31) &&
          d.N < (1ll << 31) && d.batch < 65536;
@@ -409,17 +474,22 @@ bool gemm_aligned(const void* a, const void* b, fo_dtype in_t, const GemmDesc& d
 
 bool gemm_supported(fo_dtype in_t, fo_dtype out_t) {
   return (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
-         (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32));
+         (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32)) ||
+         ((in_t == FO_F8E4M3 || in_t == FO_F8E5M2) && (out_t == in_t || out_t == FO_F32));
 }
 
 void launch_gemm(hipStream_t s, void* c, const void* a, const void* b, fo_dtype in_t, fo_dtype out_t,
                  const GemmDesc& d) {
   // 16-byte fragment loads need 16-byte aligned rows.
   require(gemm_aligned(a, b, in_t, d), "gemm: operands not 16-byte aligned or shape too large");
-  if (in_t == FO_BF16 && out_t == FO_BF16) return gemm_launch<false, 0>(s, d, c, a, b);
-  if (in_t == FO_BF16 && out_t == FO_F32) return gemm_launch<false, 1>(s, d, c, a, b);
-  if (in_t == FO_I8 && out_t == FO_I8) return gemm_launch<true, 2>(s, d, c, a, b);
-  if (in_t == FO_I8 && out_t == FO_I32) return gemm_launch<true, 3>(s, d, c, a, b);
+  if (in_t == FO_BF16 && out_t == FO_BF16) return gemm_launch<kBf16, 0>(s, d, c, a, b);
+  if (in_t == FO_BF16 && out_t == FO_F32) return gemm_launch<kBf16, 1>(s, d, c, a, b);
+  if (in_t == FO_I8 && out_t == FO_I8) return gemm_launch<kI8, 2>(s, d, c, a, b);
+  if (in_t == FO_I8 && out_t == FO_I32) return gemm_launch<kI8, 3>(s, d, c, a, b);
+  if (in_t == FO_F8E4M3 && out_t == FO_F8E4M3) return gemm_launch<kF8E4M3, 5>(s, d, c, a, b);
+  if (in_t == FO_F8E4M3 && out_t == FO_F32) return gemm_launch<kF8E4M3, 1>(s, d, c, a, b);
+  if (in_t == FO_F8E5M2 && out_t == FO_F8E5M2) return gemm_launch<kF8E5M2, 6>(s, d, c, a, b);
+  if (in_t == FO_F8E5M2 && out_t == FO_F32) return gemm_launch<kF8E5M2, 1>(s, d, c, a, b);
   throw InvalidArg("gemm: unsupported dtype pair");
 }
 
@@ -434,7 +504,7 @@ void launch_w8a8(hipStream_t s, uint16_t* out, int32_t* acc_out, const int8_t* a
   d.ldc_m = n;
   d.ldc_n = 1;
   require(gemm_aligned(a, w, FO_I8, d), "w8a8: k must be a multiple of 16 and operands 16-byte aligned");
-  gemm_launch<true, 4>(s, d, out, a, w, scale, acc_out);
+  gemm_launch<kI8, 4>(s, d, out, a, w, scale, acc_out);
 }
 
 }  // namespace fo

@@ -460,6 +460,8 @@ __device__ __forceinline__ uint32_t load_word(const void* p, fo_dtype t, uint64_
     case FO_I8:
       return (uint32_t)(int32_t)((const int8_t*)p)[i];
     case FO_U8:
+    case FO_F8E4M3:
+    case FO_F8E5M2:
       return (uint32_t)((const uint8_t*)p)[i];
     case FO_I16:
       return (uint32_t)(int32_t)((const int16_t*)p)[i];
@@ -476,6 +478,8 @@ __device__ __forceinline__ void store_word(void* p, fo_dtype t, uint64_t i, uint
   switch (t) {
     case FO_I8:
     case FO_U8:
+    case FO_F8E4M3:
+    case FO_F8E5M2:
       ((uint8_t*)p)[i] = (uint8_t)v;
       break;
     case FO_I16:
@@ -489,16 +493,24 @@ __device__ __forceinline__ void store_word(void* p, fo_dtype t, uint64_t i, uint
   }
 }
 
-// Cast (cast.rs:145-280): `w` holds the loaded source word (sign-extended ints, raw bf16 bits).
+// Cast (cast.rs:145-280): `w` holds the loaded source word (sign-extended ints, raw bf16 / f8
+// bits). Float pairs go through f32 (f8 and bf16 widen exactly); the host admits only the
+// reference's pairs: identity, bf16 <-> f32, f8 <-> f32, and any integer pair.
 __device__ __forceinline__ uint32_t cast_word(uint32_t w, fo_dtype from, fo_dtype to, bool relu) {
+  if (from == to) return w;
   float f;
-  bool is_float_src = from == FO_F32 || from == FO_BF16;
+  bool is_float_src = true;
   if (from == FO_BF16) {
     f = bf16_to_f32((uint16_t)w);
   } else if (from == FO_F32) {
     f = bits_f32(w);
+  } else if (from == FO_F8E4M3) {
+    f = f8e4m3_to_f32(w);
+  } else if (from == FO_F8E5M2) {
+    f = f8e5m2_to_f32(w);
   } else {
     f = 0.f;
+    is_float_src = false;
   }
   if (to == FO_BF16) {
     if (!is_float_src) return 0;  // not a reference cast; rejected on the host
@@ -506,8 +518,16 @@ __device__ __forceinline__ uint32_t cast_word(uint32_t w, fo_dtype from, fo_dtyp
     return f32_to_bf16(f);
   }
   if (to == FO_F32) return is_float_src ? f32_bits(f) : 0u;
+  if (to == FO_F8E4M3) return f32_to_f8e4m3(f);
+  if (to == FO_F8E5M2) return f32_to_f8e5m2(f);
   // integer targets: `as` narrowing / sign extension of the i32 word
   return w;
+}
+
+// TableLookup f8 -> bf16 (cast.rs:58-74): bf16::from_f32 of the exact f32 value. An 8-bit float's
+// f32 image has its low 16 bits zero (NaN decodes quiet), so the rounding never fires.
+__device__ __forceinline__ uint32_t table_lookup_word(uint32_t w, fo_dtype from) {
+  return f32_bits(from == FO_F8E4M3 ? f8e4m3_to_f32(w) : f8e5m2_to_f32(w)) >> 16;
 }
 
 __device__ __forceinline__ float fsel_min(float a, float b) { return fminf(a, b); }
@@ -610,6 +630,8 @@ __global__ void __launch_bounds__(kBlock) k_map(void* dst, fo_dtype dst_t, const
     uint32_t r;
     if (op.code == FO_OP_CAST || op.code == FO_OP_CAST_RELU) {
       r = cast_word(w, src_t, dst_t, op.code == FO_OP_CAST_RELU);
+    } else if (op.code == FO_OP_TABLE_LOOKUP) {
+      r = table_lookup_word(w, src_t);
     } else if (op.code < 30 || op.code == FO_OP_FXP_TO_FP || op.code == FO_OP_FP_TO_FXP) {
       r = unary_op(op.code, w, op.imm0);
     } else {
@@ -649,10 +671,18 @@ __global__ void __launch_bounds__(kBlock) k_zip3_slots(void* dst, const void* da
 
 void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t, uint64_t n,
                 const fo_op& op) {
+  auto is_f8 = [](fo_dtype t) { return t == FO_F8E4M3 || t == FO_F8E5M2; };
   if (op.code == FO_OP_CAST || op.code == FO_OP_CAST_RELU) {
-    bool fsrc = src_t == FO_F32 || src_t == FO_BF16, fdst = dst_t == FO_F32 || dst_t == FO_BF16;
+    bool fsrc = src_t == FO_F32 || src_t == FO_BF16 || is_f8(src_t);
+    bool fdst = dst_t == FO_F32 || dst_t == FO_BF16 || is_f8(dst_t);
     require(fsrc == fdst, "map: cast between a float and an integer type is not a reference cast");
+    require(src_t == dst_t || !(is_f8(src_t) || is_f8(dst_t)) || src_t == FO_F32 || dst_t == FO_F32,
+            "map: an 8-bit float casts only to and from f32 (f8 -> bf16 is FO_OP_TABLE_LOOKUP)");
     require(op.code != FO_OP_CAST_RELU || (src_t == FO_F32 && dst_t == FO_BF16), "cast_relu is f32 -> bf16");
+  } else if (op.code == FO_OP_TABLE_LOOKUP) {
+    require(is_f8(src_t) && dst_t == FO_BF16, "map: table lookup decodes an 8-bit float to bf16");
+  } else {
+    require(!is_f8(src_t) && !is_f8(dst_t), "map: 8-bit floats take casts and table lookups only");
   }
   hipLaunchKernelGGL(k_map, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, dst, dst_t, src, src_t, n, op);
   FO_HIP(hipGetLastError());
@@ -660,6 +690,8 @@ void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dt
 
 void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
                 const fo_op& op) {
+  require(in_t != FO_F8E4M3 && in_t != FO_F8E5M2 && dst_t != FO_F8E4M3 && dst_t != FO_F8E5M2,
+          "zip_with: 8-bit floats take casts and table lookups only");
   hipLaunchKernelGGL(k_zip, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, dst, dst_t, a, b, in_t, n, op);
   FO_HIP(hipGetLastError());
 }
@@ -853,8 +885,26 @@ void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_
 // ---------------------------------------------------------------------------------------------
 namespace {
 
+// The two 8-bit float operand types, distinct from each other and from uint8_t.
+struct f8e4m3_t {
+  uint8_t bits;
+};
+struct f8e5m2_t {
+  uint8_t bits;
+};
+
 template <typename In, typename Acc>
 struct MacT;
+template <>
+struct MacT<f8e4m3_t, float> {  // f8 operands, f32 accumulator (ContractionCast, cast.rs:357-363)
+  static __device__ __forceinline__ float widen(f8e4m3_t v) { return f8e4m3_to_f32(v.bits); }
+  static __device__ __forceinline__ float mac(float acc, float a, float b) { return __fadd_rn(acc, __fmul_rn(a, b)); }
+};
+template <>
+struct MacT<f8e5m2_t, float> {
+  static __device__ __forceinline__ float widen(f8e5m2_t v) { return f8e5m2_to_f32(v.bits); }
+  static __device__ __forceinline__ float mac(float acc, float a, float b) { return __fadd_rn(acc, __fmul_rn(a, b)); }
+};
 template <>
 struct MacT<uint16_t, float> {  // bf16 operands, f32 accumulator
   static __device__ __forceinline__ float widen(uint16_t v) { return bf16_to_f32(v); }
@@ -892,6 +942,22 @@ __device__ __forceinline__ float narrow<uint16_t, float, float>(float a) {
 }
 template <>
 __device__ __forceinline__ float narrow<float, float, float>(float a) {
+  return a;
+}
+template <>
+__device__ __forceinline__ f8e4m3_t narrow<f8e4m3_t, float, f8e4m3_t>(float a) {
+  return f8e4m3_t{f32_to_f8e4m3(a)};
+}
+template <>
+__device__ __forceinline__ float narrow<f8e4m3_t, float, float>(float a) {
+  return a;
+}
+template <>
+__device__ __forceinline__ f8e5m2_t narrow<f8e5m2_t, float, f8e5m2_t>(float a) {
+  return f8e5m2_t{f32_to_f8e5m2(a)};
+}
+template <>
+__device__ __forceinline__ float narrow<f8e5m2_t, float, float>(float a) {
   return a;
 }
 template <>
@@ -965,6 +1031,12 @@ void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const
   if (in_t == FO_BF16 && out_t == FO_BF16) return contract_t<uint16_t, float, uint16_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_BF16 && out_t == FO_F32) return contract_t<uint16_t, float, float>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_F32) return contract_t<float, float, float>(s, out, lhs, rhs, ll, rl, n, ow, rw);
+  if (in_t == FO_F8E4M3 && out_t == FO_F8E4M3)
+    return contract_t<f8e4m3_t, float, f8e4m3_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
+  if (in_t == FO_F8E4M3 && out_t == FO_F32) return contract_t<f8e4m3_t, float, float>(s, out, lhs, rhs, ll, rl, n, ow, rw);
+  if (in_t == FO_F8E5M2 && out_t == FO_F8E5M2)
+    return contract_t<f8e5m2_t, float, f8e5m2_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
+  if (in_t == FO_F8E5M2 && out_t == FO_F32) return contract_t<f8e5m2_t, float, float>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_I8 && out_t == FO_I8) return contract_t<int8_t, int32_t, int8_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_I8 && out_t == FO_I32) return contract_t<int8_t, int32_t, int32_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);
   if (in_t == FO_I32) return contract_t<int32_t, int32_t, int32_t>(s, out, lhs, rhs, ll, rl, n, ow, rw);

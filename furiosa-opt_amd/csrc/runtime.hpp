@@ -61,6 +61,8 @@ inline int64_t dtype_bytes(fo_dtype t) {
   switch (t) {
     case FO_I8:
     case FO_U8:
+    case FO_F8E4M3:
+    case FO_F8E5M2:
       return 1;
     case FO_I16:
     case FO_BF16:

@@ -34,8 +34,10 @@ from . import mapping_ref as mr
 HERE = Path(__file__).resolve().parent
 _SO = HERE / "libfo_cpu.so"
 
-I8, U8, I16, I32, BF16, F32 = 0, 1, 2, 3, 4, 5
-NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32}
+I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2 = 0, 1, 2, 3, 4, 5, 6, 7
+NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32, F8E4M3: np.uint8,
+      F8E5M2: np.uint8}
+OP_CAST, OP_TABLE_LOOKUP = 0, 2
 
 
 def build() -> Path:
@@ -51,6 +53,10 @@ def _load():
     sig = {
         "ref_bf16_to_f32": (F, [C.c_uint16]),
         "ref_f32_to_bf16": (C.c_uint16, [F]),
+        "ref_f8e4m3_to_f32": (F, [C.c_uint8]),
+        "ref_f32_to_f8e4m3": (C.c_uint8, [F]),
+        "ref_f8e5m2_to_f32": (F, [C.c_uint8]),
+        "ref_f32_to_f8e5m2": (C.c_uint8, [F]),
         "ref_fxp_to_fp": (F, [I32_, U32]),
         "ref_fp_to_fxp": (I32_, [F, U32]),
         "ref_contraction": (None, [P, P, C.c_int, P, C.c_int, I64, P, P, I64, P, P, I64, I64]),
@@ -186,6 +192,16 @@ def contraction(lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int, lhs_map
     return out
 
 
+def f8_to_f32(codes: np.ndarray, t: int) -> np.ndarray:
+    """Cast<f32> for f8e4m3 / f8e5m2 (cast.rs:193-219) over an array of codes."""
+    return map_(np.ascontiguousarray(codes, dtype=np.uint8), t, F32, OP_CAST)
+
+
+def f32_to_f8(x: np.ndarray, t: int) -> np.ndarray:
+    """Cast<f8e4m3> / Cast<f8e5m2> for f32 (cast.rs:200-219) over an array."""
+    return map_(np.ascontiguousarray(x, dtype=np.float32), F32, t, OP_CAST)
+
+
 def transmute(src: np.ndarray, src_map: dict, dst_map: dict) -> np.ndarray:
     sl = mr.liveness(src_map)
     dl = mr.liveness(dst_map)
@@ -266,7 +282,7 @@ def mlp(x, w1, b1, w2, b2, batch: int, in_f: int, hidden: int, out_f: int):
 
 
 def gemm_rows(a: np.ndarray, b: np.ndarray, M: int, N: int, K: int, row_begin: int, row_end: int,
-              out_t: int = BF16) -> np.ndarray:
+              out_t: int = BF16, in_t: int = BF16) -> np.ndarray:
     """contraction_in for the mapped GEMM (lhs m![M/8, M%8, K], rhs m![N, K], out m![M/8, M%8, N])
     over output rows [row_begin, row_end): its ReadPlan is affine -- base_l(o) = (o / N) * K,
     base_r(o) = (o % N) * K, delta(k) = k for both (pinned against the brute-force plan at small
@@ -277,7 +293,7 @@ def gemm_rows(a: np.ndarray, b: np.ndarray, M: int, N: int, K: int, row_begin: i
     delta = np.arange(K, dtype=np.int64)
     out = np.zeros(len(o), dtype=NP[out_t])
     A, B = np.ascontiguousarray(a), np.ascontiguousarray(b)
-    lib.ref_contraction(_p(A), _p(B), BF16, _p(out), out_t, len(o), _p(lbase), _p(rbase), K, _p(delta), _p(delta),
+    lib.ref_contraction(_p(A), _p(B), in_t, _p(out), out_t, len(o), _p(lbase), _p(rbase), K, _p(delta), _p(delta),
                         len(A), len(B))
     return out
 

@@ -299,8 +299,9 @@ CONTRACTIONS = [
 
 
 @pytest.mark.parametrize("case", CONTRACTIONS, ids=[f"{c[1]}.{c[2]}->{c[4]}" for c in CONTRACTIONS])
-@pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I8), (I8, I32), (F32, F32), (I32, I32)],
-                         ids=["bf16", "bf16w", "i8", "i8w", "f32", "i32"])
+@pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I8), (I8, I32), (F32, F32), (I32, I32),
+                                   (fh.F8E4M3, fh.F8E4M3), (fh.F8E4M3, F32), (fh.F8E5M2, fh.F8E5M2), (fh.F8E5M2, F32)],
+                         ids=["bf16", "bf16w", "i8", "i8w", "f32", "i32", "e4m3", "e4m3w", "e5m2", "e5m2w"])
 def test_contraction_generic_exact(rt, case, types):
     sizes, l_t, r_t, p_t, o_t = case
     in_t, out_t = types
@@ -313,6 +314,9 @@ def test_contraction_generic_exact(rt, case, types):
     elif in_t == F32:
         lhs = rng.standard_normal(mr.size(lo)).astype(np.float32)
         rhs = rng.standard_normal(mr.size(ro)).astype(np.float32)
+    elif in_t in (fh.F8E4M3, fh.F8E5M2):
+        lhs = emu.f32_to_f8(rng.standard_normal(mr.size(lo)).astype(np.float32), in_t)
+        rhs = emu.f32_to_f8(rng.standard_normal(mr.size(ro)).astype(np.float32), in_t)
     else:
         lhs = rng.integers(-127, 128, mr.size(lo)).astype(npin)
         rhs = rng.integers(-127, 128, mr.size(ro)).astype(npin)
