@@ -349,7 +349,7 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     check_buf(dst, "dst");
     check_buf(src, "src");
     require(op != nullptr, "op is NULL");
-    require(n * dtype_bytes(dst_t) <= dst->bytes && n * dtype_bytes(src_t) <= src->bytes, "map: n exceeds a buffer");
+    require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
     if (n == 0) return;
     set_device(rt);
     launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
@@ -586,7 +586,8 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     bool ok_types = (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
                     (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32)) || (in_t == FO_F32 && out_t == FO_F32) ||
                     (in_t == FO_I32 && out_t == FO_I32) ||
-                    ((in_t == FO_F8E4M3 || in_t == FO_F8E5M2) && (out_t == in_t || out_t == FO_F32));
+                    ((in_t == FO_F8E4M3 || in_t == FO_F8E5M2) && (out_t == in_t || out_t == FO_F32)) ||
+                    (in_t == FO_I4 && (out_t == FO_I4 || out_t == FO_I32));
     require(ok_types, "contraction: unsupported operand/output dtype pair");
     fm::Factors l = flat(lhs_map, "lhs_map"), r = flat(rhs_map, "rhs_map");
     fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");
@@ -594,65 +595,95 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     fm::Factors contracted = fm::carve(pre, o);
     fm::Joint j = fm::sequence({l, r}, {o, contracted}, fm::Mode::Read);
     auto ow = part(j, 0), rw = live_only(part(j, 1));
-    int64_t ib = dtype_bytes(in_t), ob = dtype_bytes(out_t);
     int64_t out_count = fm::size(o);
-    require(out_count * ob <= (int64_t)out->bytes, "contraction: out buffer smaller than out_map");
+    require(span_bytes(out_t, (uint64_t)out_count) <= out->bytes, "contraction: out buffer smaller than out_map");
     require(out_count < (1ll << 31), "contraction: more than 2^31 output cells");
+    require(out_t != FO_I4 || out_count % 2 == 0, "contraction: a 4-bit output stream needs an even cell count");
     if (out_count == 0) return;
-    int64_t lhs_len = (int64_t)(lhs->bytes / ib), rhs_len = (int64_t)(rhs->bytes / ib);
     set_device(rt);
 
-    // MFMA path: out wheels split into rows (lhs only) and columns (rhs only), one contiguous
-    // contracted wheel, no padding, every read in bounds.
-    if (gemm_supported(in_t, out_t)) {
-      std::vector<fm::Wheel> mw, nw, bw;
-      int64_t place = 1;
-      std::vector<int64_t> mplace, nplace, bplace;
-      bool shape_ok = true;
-      for (auto& w : ow) {
-        if (w.live != w.size) shape_ok = false;
-        bool la = w.stride[0] != 0, rb = w.stride[1] != 0;
-        if (la && !rb) {
-          mw.push_back(w);
-          mplace.push_back(place);
-        } else if (!la && rb) {
-          nw.push_back(w);
-          nplace.push_back(place);
-        } else if (la && rb) {
-          bw.push_back(w);
-          bplace.push_back(place);
-        } else {
-          mw.push_back(w);  // an output axis neither operand reads: rows that repeat
-          mplace.push_back(place);
-        }
-        place *= w.size;
+    // i4 operands (ContractionCast for i4: widen to i32, cast.rs:365-367) are unpacked to one i8 per
+    // element in scratch, exactly, and contracted as i8; an i4 result is computed as i32 and packed
+    // (one narrow per cell, Cast<i4> for i32).
+    fo_dtype ct = in_t, co = out_t;
+    const void *L = lhs->ptr, *R = rhs->ptr;
+    void* O = out->ptr;
+    int64_t lhs_len, rhs_len;
+    if (in_t == FO_I4) {
+      auto up = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
+      const uint64_t la = up(lhs->bytes * 2), ra = up(rhs->bytes * 2), oa = out_t == FO_I4 ? (uint64_t)out_count * 4 : 0;
+      uint8_t* sc = (uint8_t*)scratch(rt, la + ra + oa);
+      launch_unpack_i4(rt->stream, (int8_t*)sc, lhs->ptr, lhs->bytes);
+      launch_unpack_i4(rt->stream, (int8_t*)(sc + la), rhs->ptr, rhs->bytes);
+      L = sc;
+      R = sc + la;
+      ct = FO_I8;
+      if (out_t == FO_I4) {
+        co = FO_I32;
+        O = sc + la + ra;
       }
-      shape_ok = shape_ok && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1 && rw.size() == 1 &&
-                 rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
-      if (shape_ok) {
-        GemmDesc d;
-        d.M = mw.empty() ? 1 : mw[0].size;
-        d.N = nw.empty() ? 1 : nw[0].size;
-        d.K = rw[0].size;
-        d.batch = bw.empty() ? 1 : bw[0].size;
-        d.lda = mw.empty() ? 0 : mw[0].stride[0];
-        d.ldb = nw.empty() ? 0 : nw[0].stride[1];
-        d.ldc_m = mw.empty() ? 0 : mplace[0];
-        d.ldc_n = nw.empty() ? 0 : nplace[0];
-        d.a_batch = bw.empty() ? 0 : bw[0].stride[0];
-        d.b_batch = bw.empty() ? 0 : bw[0].stride[1];
-        d.c_batch = bw.empty() ? 0 : bplace[0];
-        int64_t amax = (d.batch - 1) * d.a_batch + (d.M - 1) * d.lda + d.K - 1;
-        int64_t bmax = (d.batch - 1) * d.b_batch + (d.N - 1) * d.ldb + d.K - 1;
-        if (amax < lhs_len && bmax < rhs_len && gemm_aligned(lhs->ptr, rhs->ptr, in_t, d)) {
-          launch_gemm(rt->stream, out->ptr, lhs->ptr, rhs->ptr, in_t, out_t, d);
-          return;
-        }
-      }
+      lhs_len = (int64_t)lhs->bytes * 2;
+      rhs_len = (int64_t)rhs->bytes * 2;
+    } else {
+      lhs_len = (int64_t)(lhs->bytes / dtype_bytes(in_t));
+      rhs_len = (int64_t)(rhs->bytes / dtype_bytes(in_t));
     }
-    const int mem[2] = {0, 1};
-    launch_contraction_generic(rt->stream, out->ptr, lhs->ptr, rhs->ptr, in_t, out_t, lhs_len, rhs_len, out_count,
-                               to_desc<2>(ow, mem), to_desc<2>(rw, mem));
+
+    auto run = [&] {
+      // MFMA path: out wheels split into rows (lhs only) and columns (rhs only), one contiguous
+      // contracted wheel, no padding, every read in bounds.
+      if (gemm_supported(ct, co)) {
+        std::vector<fm::Wheel> mw, nw, bw;
+        int64_t place = 1;
+        std::vector<int64_t> mplace, nplace, bplace;
+        bool shape_ok = true;
+        for (auto& w : ow) {
+          if (w.live != w.size) shape_ok = false;
+          bool la = w.stride[0] != 0, rb = w.stride[1] != 0;
+          if (la && !rb) {
+            mw.push_back(w);
+            mplace.push_back(place);
+          } else if (!la && rb) {
+            nw.push_back(w);
+            nplace.push_back(place);
+          } else if (la && rb) {
+            bw.push_back(w);
+            bplace.push_back(place);
+          } else {
+            mw.push_back(w);  // an output axis neither operand reads: rows that repeat
+            mplace.push_back(place);
+          }
+          place *= w.size;
+        }
+        shape_ok = shape_ok && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1 && rw.size() == 1 &&
+                   rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
+        if (shape_ok) {
+          GemmDesc d;
+          d.M = mw.empty() ? 1 : mw[0].size;
+          d.N = nw.empty() ? 1 : nw[0].size;
+          d.K = rw[0].size;
+          d.batch = bw.empty() ? 1 : bw[0].size;
+          d.lda = mw.empty() ? 0 : mw[0].stride[0];
+          d.ldb = nw.empty() ? 0 : nw[0].stride[1];
+          d.ldc_m = mw.empty() ? 0 : mplace[0];
+          d.ldc_n = nw.empty() ? 0 : nplace[0];
+          d.a_batch = bw.empty() ? 0 : bw[0].stride[0];
+          d.b_batch = bw.empty() ? 0 : bw[0].stride[1];
+          d.c_batch = bw.empty() ? 0 : bplace[0];
+          int64_t amax = (d.batch - 1) * d.a_batch + (d.M - 1) * d.lda + d.K - 1;
+          int64_t bmax = (d.batch - 1) * d.b_batch + (d.N - 1) * d.ldb + d.K - 1;
+          if (amax < lhs_len && bmax < rhs_len && gemm_aligned(L, R, ct, d)) {
+            launch_gemm(rt->stream, O, L, R, ct, co, d);
+            return;
+          }
+        }
+      }
+      const int mem[2] = {0, 1};
+      launch_contraction_generic(rt->stream, O, L, R, ct, co, lhs_len, rhs_len, out_count, to_desc<2>(ow, mem),
+                                 to_desc<2>(rw, mem));
+    };
+    run();
+    if (in_t == FO_I4 && out_t == FO_I4) launch_pack_i4(rt->stream, out->ptr, (const int32_t*)O, (uint64_t)out_count);
   });
 }
 

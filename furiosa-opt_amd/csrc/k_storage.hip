@@ -524,9 +524,21 @@ __device__ __forceinline__ uint32_t cast_word(uint32_t w, fo_dtype from, fo_dtyp
   return w;
 }
 
-// TableLookup f8 -> bf16 (cast.rs:58-74): bf16::from_f32 of the exact f32 value. An 8-bit float's
-// f32 image has its low 16 bits zero (NaN decodes quiet), so the rounding never fires.
-__device__ __forceinline__ uint32_t table_lookup_word(uint32_t w, fo_dtype from) {
+// f4e2m1 value (OCP E2M1: sign, 2-bit exponent of bias 1, 1 mantissa bit; exponent 0 holds
+// 0 and 0.5): 0, 0.5, 1, 1.5, 2, 3, 4, 6 and their negatives.
+__device__ __forceinline__ float f4e2m1_to_f32(uint32_t c) {
+  const uint32_t s = (c & 8u) << 28, e = (c >> 1) & 3u, m = c & 1u;
+  return bits_f32(s | (e == 0u ? (m ? 0x3f000000u : 0u) : (((e + 126u) << 23) | (m << 22))));
+}
+
+// Table lookups (cast.rs:47-74): f8 -> bf16 is bf16::from_f32 of the exact f32 value (an 8-bit
+// float's f32 image has its low 16 bits zero and NaN decodes quiet, so no rounding fires);
+// f4e2m1 -> f8e4m3 / f8e5m2 encode the exact e2m1 value (every one is a code of both formats).
+__device__ __forceinline__ uint32_t table_lookup_word(uint32_t w, fo_dtype from, fo_dtype to) {
+  if (from == FO_F4E2M1) {
+    const float f = f4e2m1_to_f32(w);
+    return to == FO_F8E4M3 ? f32_to_f8e4m3(f) : f32_to_f8e5m2(f);
+  }
   return f32_bits(from == FO_F8E4M3 ? f8e4m3_to_f32(w) : f8e5m2_to_f32(w)) >> 16;
 }
 
@@ -631,7 +643,7 @@ __global__ void __launch_bounds__(kBlock) k_map(void* dst, fo_dtype dst_t, const
     if (op.code == FO_OP_CAST || op.code == FO_OP_CAST_RELU) {
       r = cast_word(w, src_t, dst_t, op.code == FO_OP_CAST_RELU);
     } else if (op.code == FO_OP_TABLE_LOOKUP) {
-      r = table_lookup_word(w, src_t);
+      r = table_lookup_word(w, src_t, dst_t);
     } else if (op.code < 30 || op.code == FO_OP_FXP_TO_FP || op.code == FO_OP_FP_TO_FXP) {
       r = unary_op(op.code, w, op.imm0);
     } else {
@@ -667,10 +679,99 @@ __global__ void __launch_bounds__(kBlock) k_zip3_slots(void* dst, const void* da
   }
 }
 
+// Element i of a 4-bit stream: nibble i % 2 of byte i / 2; i4 sign-extends (i4::from_i32 of the
+// nibble, scalar.rs:663-685), f4e2m1 keeps the raw code.
+__device__ __forceinline__ uint32_t load_nibble(const uint8_t* p, fo_dtype t, uint64_t i) {
+  const uint32_t nib = (p[i >> 1] >> ((i & 1) * 4)) & 15u;
+  return t == FO_I4 ? (uint32_t)((int32_t)(nib << 28) >> 28) : nib;
+}
+
+// Maps with a 4-bit side: one thread per element pair, so each packed output byte has one writer.
+// The ops are the casts i4 <-> i32 (the i32 word narrows to its low nibble, i4::from_i32) and the
+// f4e2m1 table lookups; the host admits nothing else.
+__global__ void __launch_bounds__(kBlock) k_map_pairs(void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t,
+                                                      uint64_t pairs, fo_op op) {
+  const bool nsrc = src_t == FO_I4 || src_t == FO_F4E2M1, ndst = dst_t == FO_I4 || dst_t == FO_F4E2M1;
+  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < pairs; j += (uint64_t)gridDim.x * kBlock) {
+    uint32_t r[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint64_t i = 2 * j + e;
+      const uint32_t w = nsrc ? load_nibble((const uint8_t*)src, src_t, i) : load_word(src, src_t, i);
+      r[e] = op.code == FO_OP_TABLE_LOOKUP ? table_lookup_word(w, src_t, dst_t) : w;
+    }
+    if (ndst) {
+      ((uint8_t*)dst)[j] = (uint8_t)((r[0] & 15u) | ((r[1] & 15u) << 4));
+    } else {
+      store_word(dst, dst_t, 2 * j, r[0]);
+      store_word(dst, dst_t, 2 * j + 1, r[1]);
+    }
+  }
+}
+
+// i4 stream -> one i8 per element (exact: i4 is a subset of i8); 4 packed bytes per thread.
+__global__ void __launch_bounds__(kBlock) k_unpack_i4(int8_t* __restrict__ dst, const uint8_t* __restrict__ src,
+                                                      uint64_t nbytes) {
+  for (uint64_t q = (uint64_t)blockIdx.x * kBlock + threadIdx.x; q * 4 < nbytes; q += (uint64_t)gridDim.x * kBlock) {
+    if (q * 4 + 4 <= nbytes) {
+      const uint32_t w = ((const uint32_t*)src)[q];
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (w >> (8 * b)) & 0xffu;
+        const uint32_t pair = (uint32_t)(((int32_t)(byte << 28) >> 28) & 0xff) |
+                              ((uint32_t)(((int32_t)(byte << 24) >> 28) & 0xff) << 8);
+        if (b < 2)
+          lo |= pair << (16 * b);
+        else
+          hi |= pair << (16 * (b - 2));
+      }
+      ((uint32_t*)dst)[2 * q] = lo;
+      ((uint32_t*)dst)[2 * q + 1] = hi;
+    } else {
+      for (uint64_t i = q * 4; i < nbytes; ++i) {
+        dst[2 * i] = (int8_t)load_nibble(src, FO_I4, 2 * i);
+        dst[2 * i + 1] = (int8_t)load_nibble(src, FO_I4, 2 * i + 1);
+      }
+    }
+  }
+}
+
+// i32 accumulators -> i4 stream (each narrows to its low nibble, Cast<i4> for i32); n is even.
+__global__ void __launch_bounds__(kBlock) k_pack_i4(uint8_t* __restrict__ dst, const int32_t* __restrict__ src,
+                                                    uint64_t pairs) {
+  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < pairs; j += (uint64_t)gridDim.x * kBlock)
+    dst[j] = (uint8_t)(((uint32_t)src[2 * j] & 15u) | (((uint32_t)src[2 * j + 1] & 15u) << 4));
+}
+
 }  // namespace
+
+void launch_unpack_i4(hipStream_t s, int8_t* dst, const void* src, uint64_t nbytes) {
+  hipLaunchKernelGGL(k_unpack_i4, dim3(grid_for((int64_t)((nbytes + 3) / 4))), dim3(kBlock), 0, s, dst,
+                     (const uint8_t*)src, nbytes);
+  FO_HIP(hipGetLastError());
+}
+
+void launch_pack_i4(hipStream_t s, void* dst, const int32_t* src, uint64_t n) {
+  hipLaunchKernelGGL(k_pack_i4, dim3(grid_for((int64_t)(n / 2))), dim3(kBlock), 0, s, (uint8_t*)dst, src, n / 2);
+  FO_HIP(hipGetLastError());
+}
 
 void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t, uint64_t n,
                 const fo_op& op) {
+  if (is_nibble(src_t) || is_nibble(dst_t)) {
+    const bool cast = op.code == FO_OP_CAST &&
+                      (src_t == dst_t || (src_t == FO_I4 && dst_t == FO_I32) || (src_t == FO_I32 && dst_t == FO_I4));
+    const bool lookup =
+        op.code == FO_OP_TABLE_LOOKUP && src_t == FO_F4E2M1 && (dst_t == FO_F8E4M3 || dst_t == FO_F8E5M2);
+    require(cast || lookup,
+            "map: a 4-bit stream takes the casts i4 <-> i32 and the f4e2m1 -> f8e4m3 / f8e5m2 table lookups");
+    require(n % 2 == 0, "map: a 4-bit stream needs an even element count");
+    hipLaunchKernelGGL(k_map_pairs, dim3(grid_for((int64_t)(n / 2))), dim3(kBlock), 0, s, dst, dst_t, src, src_t,
+                       n / 2, op);
+    FO_HIP(hipGetLastError());
+    return;
+  }
   auto is_f8 = [](fo_dtype t) { return t == FO_F8E4M3 || t == FO_F8E5M2; };
   if (op.code == FO_OP_CAST || op.code == FO_OP_CAST_RELU) {
     bool fsrc = src_t == FO_F32 || src_t == FO_BF16 || is_f8(src_t);
@@ -680,7 +781,7 @@ void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dt
             "map: an 8-bit float casts only to and from f32 (f8 -> bf16 is FO_OP_TABLE_LOOKUP)");
     require(op.code != FO_OP_CAST_RELU || (src_t == FO_F32 && dst_t == FO_BF16), "cast_relu is f32 -> bf16");
   } else if (op.code == FO_OP_TABLE_LOOKUP) {
-    require(is_f8(src_t) && dst_t == FO_BF16, "map: table lookup decodes an 8-bit float to bf16");
+    require(is_f8(src_t) && dst_t == FO_BF16, "map: table lookup decodes an 8-bit float to bf16 (or f4e2m1 to f8)");
   } else {
     require(!is_f8(src_t) && !is_f8(dst_t), "map: 8-bit floats take casts and table lookups only");
   }

@@ -70,9 +70,17 @@ inline int64_t dtype_bytes(fo_dtype t) {
     case FO_I32:
     case FO_F32:
       return 4;
+    case FO_I4:
+    case FO_F4E2M1:
+      throw InvalidArg("4-bit (nibble-packed) elements are taken by map and contraction only");
   }
   throw InvalidArg("unknown dtype");
 }
+
+inline bool is_nibble(fo_dtype t) { return t == FO_I4 || t == FO_F4E2M1; }
+
+// Bytes that hold n elements (a 4-bit stream packs two per byte).
+inline uint64_t span_bytes(fo_dtype t, uint64_t n) { return is_nibble(t) ? (n + 1) / 2 : n * (uint64_t)dtype_bytes(t); }
 
 // Host-side copy of wheels into the by-value kernel descriptor.
 template <int NMEM>
@@ -111,6 +119,9 @@ void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t elem_by
                       const Wheels<1>& dst_self, const Wheels<1>& src_self);
 
 void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t, uint64_t n, const fo_op& op);
+// i4 stream of `nbytes` -> 2 * nbytes i8 elements; i32 accumulators -> i4 stream (n even)
+void launch_unpack_i4(hipStream_t s, int8_t* dst, const void* src, uint64_t nbytes);
+void launch_pack_i4(hipStream_t s, void* dst, const int32_t* src, uint64_t n);
 void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
                 const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

@@ -28,11 +28,13 @@ if not LIB_PATH.exists():
 _lib = C.CDLL(str(LIB_PATH))
 
 # ---- dtypes / ops (mirrors furiosa_hip.h) -------------------------------------------------------
-I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2 = 0, 1, 2, 3, 4, 5, 6, 7
-# bf16 and the 8-bit floats travel as their raw bit patterns
+I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2, I4, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9
+# bf16 and the 8-bit floats travel as their raw bit patterns; the 4-bit types as packed bytes
+# (element 2k in the low nibble of byte k)
 NP_DTYPE = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32,
-            F8E4M3: np.uint8, F8E5M2: np.uint8}
-NAMES = {"i8": I8, "u8": U8, "i16": I16, "i32": I32, "bf16": BF16, "f32": F32, "f8e4m3": F8E4M3, "f8e5m2": F8E5M2}
+            F8E4M3: np.uint8, F8E5M2: np.uint8, I4: np.uint8, F4E2M1: np.uint8}
+NAMES = {"i8": I8, "u8": U8, "i16": I16, "i32": I32, "bf16": BF16, "f32": F32, "f8e4m3": F8E4M3, "f8e5m2": F8E5M2,
+         "i4": I4, "f4e2m1": F4E2M1}
 
 OP = dict(
     CAST=0, CAST_RELU=1, TABLE_LOOKUP=2, EXP=10, NEG_EXP=11, SQRT=12, TANH=13, SIGMOID=14, LOG=15, SIN=16, COS=17,

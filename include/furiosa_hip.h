@@ -54,7 +54,13 @@ typedef enum fo_dtype {
   /* 8-bit floats, one byte each (scalar.rs:443-575, float/f8e4.rs, float/f8e5.rs): OCP E4M3
    * (bias 7, no inf, 0x7f/0xff NaN, max 448) and E5M2 (bias 15, IEEE-like inf/NaN). */
   FO_F8E4M3 = 6,
-  FO_F8E5M2 = 7
+  FO_F8E5M2 = 7,
+  /* 4-bit types, two per byte, element 2k in the low nibble of byte k (get_nibble / set_nibble,
+   * scalar.rs:1093-1117): i4 (two's complement, scalar.rs:585-690) and f4e2m1 (OCP E2M1,
+   * scalar.rs:925-1091). Taken by fo_map (casts, table lookup) and fo_contraction; a 4-bit
+   * stream has an even element count (pack_nibbles, scalar.rs:1119-1131). */
+  FO_I4 = 8,
+  FO_F4E2M1 = 9
 } fo_dtype;
 
 /* ---- runtime and buffers ------------------------------------------------------------------ */
@@ -115,7 +121,7 @@ typedef enum fo_op_code {
    * f32 -> f8 (cast.rs:124-125; e4m3 rounds to nearest even and saturates at +-448, e5m2 rounds
    * half away from zero and overflows to inf) are FO_OP_CAST; TableLookup f8 -> bf16 (cast.rs:58-74,
    * the only route from an 8-bit float to bf16; exact) is this code: */
-  FO_OP_TABLE_LOOKUP = 2,
+  FO_OP_TABLE_LOOKUP = 2, /* also f4e2m1 -> f8e4m3 / f8e5m2 (cast.rs:47-57; exact) */
   /* FpUnaryOp (semantics.rs:75-90), f32 -> f32 */
   FO_OP_EXP = 10,
   FO_OP_NEG_EXP = 11,

@@ -34,9 +34,10 @@ from . import mapping_ref as mr
 HERE = Path(__file__).resolve().parent
 _SO = HERE / "libfo_cpu.so"
 
-I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2 = 0, 1, 2, 3, 4, 5, 6, 7
+I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2, I4, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7, 8, 9
 NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32, F8E4M3: np.uint8,
-      F8E5M2: np.uint8}
+      F8E5M2: np.uint8, I4: np.uint8, F4E2M1: np.uint8}  # 4-bit streams: packed bytes, two elements each
+NIBBLE = (I4, F4E2M1)
 OP_CAST, OP_TABLE_LOOKUP = 0, 2
 
 
@@ -57,6 +58,7 @@ def _load():
         "ref_f32_to_f8e4m3": (C.c_uint8, [F]),
         "ref_f8e5m2_to_f32": (F, [C.c_uint8]),
         "ref_f32_to_f8e5m2": (C.c_uint8, [F]),
+        "ref_f4e2m1_to_f8e4m3": (C.c_uint8, [C.c_uint8]),
         "ref_fxp_to_fp": (F, [I32_, U32]),
         "ref_fp_to_fxp": (I32_, [F, U32]),
         "ref_contraction": (None, [P, P, C.c_int, P, C.c_int, I64, P, P, I64, P, P, I64, I64]),
@@ -185,11 +187,30 @@ def contraction(lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int, lhs_map
     lbase, ldelta = _additive(lpos, ol)
     rbase, rdelta = _additive(rpos, ol)
     n_out = mr.size(out_map)
-    out = np.zeros(n_out, dtype=NP[out_t])
+    acc_t = I32 if out_t == I4 else out_t
+    out = np.zeros(n_out, dtype=NP[acc_t])
     L, R = np.ascontiguousarray(lhs), np.ascontiguousarray(rhs)
-    lib.ref_contraction(_p(L), _p(R), in_t, _p(out), out_t, n_out, _p(lbase), _p(rbase), len(ldelta), _p(ldelta),
-                        _p(rdelta), len(L), len(R))
-    return out
+    per = 2 if in_t in NIBBLE else 1  # elements per stored byte
+    lib.ref_contraction(_p(L), _p(R), in_t, _p(out), acc_t, n_out, _p(lbase), _p(rbase), len(ldelta), _p(ldelta),
+                        _p(rdelta), len(L) * per, len(R) * per)
+    return pack_nibbles(out) if out_t == I4 else out
+
+
+def pack_nibbles(v: np.ndarray) -> np.ndarray:
+    """i32 words -> a 4-bit stream: each keeps its low nibble (Cast<i4> for i32, i4::from_i32), element
+    2k in the low half of byte k (set_nibble, scalar.rs:1106-1117); the count must be even."""
+    v = np.asarray(v).astype(np.int64)
+    if len(v) % 2:
+        raise ValueError("a 4-bit stream needs an even element count")
+    return ((v[0::2] & 15) | ((v[1::2] & 15) << 4)).astype(np.uint8)
+
+
+def unpack_i4(b: np.ndarray) -> np.ndarray:
+    """A 4-bit i4 stream -> its int32 values (get_nibble then sign extension)."""
+    b = np.asarray(b, np.uint8).astype(np.int32)
+    out = np.empty(2 * len(b), np.int32)
+    out[0::2], out[1::2] = b & 15, b >> 4
+    return np.where(out >= 8, out - 16, out).astype(np.int32)
 
 
 def f8_to_f32(codes: np.ndarray, t: int) -> np.ndarray:
@@ -214,9 +235,10 @@ def transmute(src: np.ndarray, src_map: dict, dst_map: dict) -> np.ndarray:
 
 
 def map_(src: np.ndarray, src_t: int, dst_t: int, code: int, flags: int = 0, imm0: int = 0, imm1: int = 0):
-    out = np.zeros(len(src), dtype=NP[dst_t])
     s = np.ascontiguousarray(src)
-    lib.ref_map(_p(out), dst_t, _p(s), src_t, len(s), code, flags, imm0, imm1)
+    n = len(s) * (2 if src_t in NIBBLE else 1)
+    out = np.zeros(n // 2 if dst_t in NIBBLE else n, dtype=NP[dst_t])
+    lib.ref_map(_p(out), dst_t, _p(s), src_t, n, code, flags, imm0, imm1)
     return out
 
 
@@ -293,8 +315,9 @@ def gemm_rows(a: np.ndarray, b: np.ndarray, M: int, N: int, K: int, row_begin: i
     delta = np.arange(K, dtype=np.int64)
     out = np.zeros(len(o), dtype=NP[out_t])
     A, B = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    per = 2 if in_t in NIBBLE else 1
     lib.ref_contraction(_p(A), _p(B), in_t, _p(out), out_t, len(o), _p(lbase), _p(rbase), K, _p(delta), _p(delta),
-                        len(A), len(B))
+                        len(A) * per, len(B) * per)
     return out
 
 

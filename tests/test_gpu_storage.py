@@ -300,8 +300,10 @@ CONTRACTIONS = [
 
 @pytest.mark.parametrize("case", CONTRACTIONS, ids=[f"{c[1]}.{c[2]}->{c[4]}" for c in CONTRACTIONS])
 @pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I8), (I8, I32), (F32, F32), (I32, I32),
-                                   (fh.F8E4M3, fh.F8E4M3), (fh.F8E4M3, F32), (fh.F8E5M2, fh.F8E5M2), (fh.F8E5M2, F32)],
-                         ids=["bf16", "bf16w", "i8", "i8w", "f32", "i32", "e4m3", "e4m3w", "e5m2", "e5m2w"])
+                                   (fh.F8E4M3, fh.F8E4M3), (fh.F8E4M3, F32), (fh.F8E5M2, fh.F8E5M2), (fh.F8E5M2, F32),
+                                   (fh.I4, fh.I4), (fh.I4, I32)],
+                         ids=["bf16", "bf16w", "i8", "i8w", "f32", "i32", "e4m3", "e4m3w", "e5m2", "e5m2w", "i4",
+                              "i4w"])
 def test_contraction_generic_exact(rt, case, types):
     sizes, l_t, r_t, p_t, o_t = case
     in_t, out_t = types
@@ -317,14 +319,19 @@ def test_contraction_generic_exact(rt, case, types):
     elif in_t in (fh.F8E4M3, fh.F8E5M2):
         lhs = emu.f32_to_f8(rng.standard_normal(mr.size(lo)).astype(np.float32), in_t)
         rhs = emu.f32_to_f8(rng.standard_normal(mr.size(ro)).astype(np.float32), in_t)
+    elif in_t == fh.I4:  # packed streams (an odd operand size gets one trailing pad nibble)
+        lhs = emu.pack_nibbles(rng.integers(-8, 8, mr.size(lo) + mr.size(lo) % 2))
+        rhs = emu.pack_nibbles(rng.integers(-8, 8, mr.size(ro) + mr.size(ro) % 2))
     else:
         lhs = rng.integers(-127, 128, mr.size(lo)).astype(npin)
         rhs = rng.integers(-127, 128, mr.size(ro)).astype(npin)
     want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
-    out = rt.alloc(mr.size(oo) * np.dtype(fh.NP_DTYPE[out_t]).itemsize)
+    out = rt.alloc(max(want.nbytes, 1))
     rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
     got = out.read(out_t)
     live = mr.liveness(oo)
+    if out_t == fh.I4:
+        got, want = emu.unpack_i4(got), emu.unpack_i4(want)
     assert np.array_equal(got[live].view(np.uint8), want[live].view(np.uint8))
 
 
