@@ -83,7 +83,8 @@ def bench_gemm(fh, rt, steps, warmup, rng):
 
 def bench_gemm_f8(fh, rt, steps, warmup, rng):
     """The same mapped 4096^3 contraction over f8e4m3 operands (ContractionCast: f32 accumulate),
-    with the f32 result (contract_outer's widened path) and with the one f8e4m3 narrow per cell."""
+    with the f32 result (contract_outer's widened path) and with the one f8e4m3 narrow per cell;
+    and over i4 operands with the i32 result."""
     M = N = K = 4096
     s = dict(M=M, N=N, K=K)
     # f8e4m3 codes with a random sign, exponent field 4..9 (magnitudes 2^-3 .. 2^2.9) and mantissa
@@ -97,6 +98,14 @@ def bench_gemm_f8(fh, rt, steps, warmup, rng):
         wall, ev = timed(rt, fn, steps, warmup)
         flop = 2.0 * M * N * K
         out[name] = dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=2 * M * K + M * N * ob)
+    # i4 operands (two per byte), i32 result: unpack to i8 in scratch, then the i8 MFMA GEMM
+    a4 = rt.upload(rng.integers(0, 256, M * K // 2, dtype=np.uint8))
+    b4 = rt.upload(rng.integers(0, 256, N * K // 2, dtype=np.uint8))
+    c = rt.alloc(M * N * 4)
+    fn = lambda: rt.contraction(c, a4, b4, fh.I4, fh.I32, *maps)
+    wall, ev = timed(rt, fn, steps, warmup)
+    flop = 2.0 * M * N * K
+    out["i4_i32"] = dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=M * K + M * N * 4)
     return out
 
 
@@ -259,8 +268,9 @@ def main():
                                               roofline_frac=r["tops"] / PEAK_I8_TOPS)
     if "gemm_f8" in res:
         for k, r in res["gemm_f8"].items():
-            configs[f"mapped_gemm_4096_f8e4m3_to_{k}"] = dict(value=r["tflops"], unit="TFLOP/s", ms=r["ms"],
-                                                            roofline_frac=r["tflops"] / PEAK_F8_TFLOPS)
+            name = "mapped_gemm_4096_i4_to_i32" if k == "i4_i32" else f"mapped_gemm_4096_f8e4m3_to_{k}"
+            configs[name] = dict(value=r["tflops"], unit="TOP/s" if k == "i4_i32" else "TFLOP/s", ms=r["ms"],
+                                 roofline_frac=r["tflops"] / (PEAK_I8_TOPS if k == "i4_i32" else PEAK_F8_TFLOPS))
     if "mlp" in res:
         r = res["mlp"]
         configs["mlp_64x784x128x10"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)

@@ -644,6 +644,8 @@ __global__ void __launch_bounds__(kBlock) k_map(void* dst, fo_dtype dst_t, const
       r = cast_word(w, src_t, dst_t, op.code == FO_OP_CAST_RELU);
     } else if (op.code == FO_OP_TABLE_LOOKUP) {
       r = table_lookup_word(w, src_t, dst_t);
+    } else if (op.code == FO_OP_ZERO_POINT_SUB) {
+      r = (uint32_t)((int32_t)w - (int32_t)op.imm0);
     } else if (op.code < 30 || op.code == FO_OP_FXP_TO_FP || op.code == FO_OP_FP_TO_FXP) {
       r = unary_op(op.code, w, op.imm0);
     } else {
@@ -687,8 +689,8 @@ __device__ __forceinline__ uint32_t load_nibble(const uint8_t* p, fo_dtype t, ui
 }
 
 // Maps with a 4-bit side: one thread per element pair, so each packed output byte has one writer.
-// The ops are the casts i4 <-> i32 (the i32 word narrows to its low nibble, i4::from_i32) and the
-// f4e2m1 table lookups; the host admits nothing else.
+// The ops are the casts i4 <-> i32 (the i32 word narrows to its low nibble, i4::from_i32), the
+// i4 zero-point subtraction and the f4e2m1 table lookups; the host admits nothing else.
 __global__ void __launch_bounds__(kBlock) k_map_pairs(void* dst, fo_dtype dst_t, const void* src, fo_dtype src_t,
                                                       uint64_t pairs, fo_op op) {
   const bool nsrc = src_t == FO_I4 || src_t == FO_F4E2M1, ndst = dst_t == FO_I4 || dst_t == FO_F4E2M1;
@@ -698,7 +700,9 @@ __global__ void __launch_bounds__(kBlock) k_map_pairs(void* dst, fo_dtype dst_t,
     for (int e = 0; e < 2; ++e) {
       const uint64_t i = 2 * j + e;
       const uint32_t w = nsrc ? load_nibble((const uint8_t*)src, src_t, i) : load_word(src, src_t, i);
-      r[e] = op.code == FO_OP_TABLE_LOOKUP ? table_lookup_word(w, src_t, dst_t) : w;
+      r[e] = op.code == FO_OP_TABLE_LOOKUP     ? table_lookup_word(w, src_t, dst_t)
+             : op.code == FO_OP_ZERO_POINT_SUB ? (uint32_t)((int32_t)w - (int32_t)op.imm0)
+                                               : w;
     }
     if (ndst) {
       ((uint8_t*)dst)[j] = (uint8_t)((r[0] & 15u) | ((r[1] & 15u) << 4));
@@ -764,8 +768,12 @@ void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dt
                       (src_t == dst_t || (src_t == FO_I4 && dst_t == FO_I32) || (src_t == FO_I32 && dst_t == FO_I4));
     const bool lookup =
         op.code == FO_OP_TABLE_LOOKUP && src_t == FO_F4E2M1 && (dst_t == FO_F8E4M3 || dst_t == FO_F8E5M2);
-    require(cast || lookup,
-            "map: a 4-bit stream takes the casts i4 <-> i32 and the f4e2m1 -> f8e4m3 / f8e5m2 table lookups");
+    const bool zp = op.code == FO_OP_ZERO_POINT_SUB && src_t == FO_I4 && dst_t == FO_I32;
+    require(cast || lookup || zp,
+            "map: a 4-bit stream takes the casts i4 <-> i32, the i4 zero-point subtraction and the f4e2m1 -> "
+            "f8e4m3 / f8e5m2 table lookups");
+    if (zp) require((int32_t)op.imm0 >= -8 && (int32_t)op.imm0 <= 7, "map: zero_point " +
+                    std::to_string((int32_t)op.imm0) + " is outside the source type's quantized range -8..=7");
     require(n % 2 == 0, "map: a 4-bit stream needs an even element count");
     hipLaunchKernelGGL(k_map_pairs, dim3(grid_for((int64_t)(n / 2))), dim3(kBlock), 0, s, dst, dst_t, src, src_t,
                        n / 2, op);
@@ -782,6 +790,11 @@ void launch_map(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, fo_dt
     require(op.code != FO_OP_CAST_RELU || (src_t == FO_F32 && dst_t == FO_BF16), "cast_relu is f32 -> bf16");
   } else if (op.code == FO_OP_TABLE_LOOKUP) {
     require(is_f8(src_t) && dst_t == FO_BF16, "map: table lookup decodes an 8-bit float to bf16 (or f4e2m1 to f8)");
+  } else if (op.code == FO_OP_ZERO_POINT_SUB) {
+    require(src_t == FO_I8 && dst_t == FO_I32, "map: zero-point subtraction widens i4 or i8 to i32");
+    require((int32_t)op.imm0 >= -128 && (int32_t)op.imm0 <= 127,
+            "map: zero_point " + std::to_string((int32_t)op.imm0) + " is outside the source type's quantized range "
+            "-128..=127");
   } else {
     require(!is_f8(src_t) && !is_f8(dst_t), "map: 8-bit floats take casts and table lookups only");
   }

@@ -38,7 +38,7 @@ I8, U8, I16, I32, BF16, F32, F8E4M3, F8E5M2, I4, F4E2M1 = 0, 1, 2, 3, 4, 5, 6, 7
 NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, BF16: np.uint16, F32: np.float32, F8E4M3: np.uint8,
       F8E5M2: np.uint8, I4: np.uint8, F4E2M1: np.uint8}  # 4-bit streams: packed bytes, two elements each
 NIBBLE = (I4, F4E2M1)
-OP_CAST, OP_TABLE_LOOKUP = 0, 2
+OP_CAST, OP_TABLE_LOOKUP, OP_ZERO_POINT_SUB = 0, 2, 3
 
 
 def build() -> Path:

@@ -82,3 +82,24 @@ def test_i4_gemm_large_ragged(rt):
     for r0 in (0, 255, 1031, Mm - 3):
         want = emu.gemm_rows(a, b, Mm, Nn, Kk, r0, r0 + 3, out_t=I32, in_t=I4).reshape(3, Nn)
         assert np.array_equal(got[r0:r0 + 3], want)
+
+
+def test_zero_point_sub(rt):
+    rng = np.random.default_rng(73)
+    b = rng.integers(0, 256, 4096, dtype=np.uint8)
+    for zp in (-8, 3, 7):
+        want = emu.map_(b, I4, I32, fh.OP["ZERO_POINT_SUB"], 0, zp & 0xFFFFFFFF)
+        d = rt.alloc(8192 * 4)
+        rt.map(d, I32, rt.upload(b), I4, 8192, fh.op("ZERO_POINT_SUB", 0, zp))
+        assert np.array_equal(d.read(np.int32), want)
+    a = rng.integers(-128, 128, 5000).astype(np.int8)
+    for zp in (-128, 0, 127):
+        want = emu.map_(a, fh.I8, I32, fh.OP["ZERO_POINT_SUB"], 0, zp & 0xFFFFFFFF)
+        d = rt.alloc(5000 * 4)
+        rt.map(d, I32, rt.upload(a), fh.I8, 5000, fh.op("ZERO_POINT_SUB", 0, zp))
+        assert np.array_equal(d.read(np.int32), want)
+    x, y = rt.upload(np.zeros(64, np.uint8)), rt.alloc(1024)
+    with pytest.raises(fh.FoError, match="quantized range"):
+        rt.map(y, I32, x, I4, 8, fh.op("ZERO_POINT_SUB", 0, 8))
+    with pytest.raises(fh.FoError, match="quantized range"):
+        rt.map(y, I32, x, fh.I8, 8, fh.op("ZERO_POINT_SUB", 0, -129))
