@@ -158,6 +158,42 @@ def bench_relayout(fh, rt, steps, warmup, rng):
         wall, ev = timed(rt, fn, steps, warmup)
         nbytes = 2 * R * C * 2
         out[name] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    # lazy relayout fusion: the three-step chain R,C -> R/8,C,R%8 -> C/64,R,C%64 -> C,R in one call
+    # (it collapses to the one transpose R,C -> C,R), against the same three steps materialized
+    views = [fh.m(t, **s) for t in ("R, C", "R / 8, C, R % 8", "C / 64, R, C % 64", "C, R")]
+    mids = [rt.alloc(R * C * 2) for _ in range(2)]
+    fn = lambda: rt.transpose_chain(dst, src, fh.BF16, views)
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 2 * R * C * 2
+    out["chain3_fused"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+
+    def stepwise():
+        rt.transpose(mids[0], src, fh.BF16, views[0], views[1])
+        rt.transpose(mids[1], mids[0], fh.BF16, views[1], views[2])
+        rt.transpose(dst, mids[1], fh.BF16, views[2], views[3])
+    wall, ev = timed(rt, stepwise, steps, warmup)
+    out["chain3_stepwise"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    # a chain that broadcasts X = 2 in its last step (R,C -> C,R -> C,X,R; 128 MiB in, 256 MiB out):
+    # it too collapses to one transpose
+    s2 = dict(R=R, C=C, X=2)
+    gviews = [fh.m(t, **s2) for t in ("R, C", "C, R", "C, X, R")]
+    gdst = rt.alloc(2 * R * C * 2)
+    fn = lambda: rt.transpose_chain(gdst, src, fh.BF16, gviews, [False, True])
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 3 * R * C * 2
+    out["chain_broadcast"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    del mids, gdst
+    # a switch-engine broadcast routing (engine/switch.rs:62-71 is a broadcast-allowed transpose):
+    # 256 slices [A, B] x 512 time steps x a 64-element bf16 packet, routed to [A, B / 4, X] slices
+    # with B % 4 moved into time and X = 4 replicas (16 MiB in, 64 MiB out)
+    sw = dict(A=16, B=16, C=512, K=64, X=4)
+    ssrc = rt.upload(rng.integers(0, 65535, 16 * 16 * 512 * 64, dtype=np.uint16))
+    sdst = rt.alloc(4 * 16 * 16 * 512 * 64 * 2)
+    sv, dv = fh.m("A, B, C, K", **sw), fh.m("A, B / 4, X, C, B % 4, K", **sw)
+    fn = lambda: rt.transpose(sdst, ssrc, fh.BF16, sv, dv, allow_broadcast=True)
+    wall, ev = timed(rt, fn, steps, warmup)
+    nbytes = 5 * 16 * 16 * 512 * 64 * 2
+    out["switch_broadcast"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     return out
 
 
@@ -279,8 +315,8 @@ def main():
             configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     if "relayout" in res:
         for k, r in res["relayout"].items():
-            configs[f"relayout_{k}_8192x8192_bf16"] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"],
-                                                           roofline_frac=r["gbs"] / PEAK_HBM_GBS)
+            name = "switch_broadcast_256x512x64_x4_bf16" if k == "switch_broadcast" else f"relayout_{k}_8192x8192_bf16"
+            configs[name] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     if g:
         configs["mapped_gemm_4096"] = dict(value=g["tflops"], unit="TFLOP/s", ms=g["ms"],
                                            roofline_frac=g["tflops"] / PEAK_BF16_TFLOPS)

@@ -427,6 +427,124 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
   });
 }
 
+// The live coordinates of `sym` in `f` (digit weights and counts): `bound` is the largest live
+// coordinate plus one (0 when absent); `dense` says whether they fill [0, bound) exactly once.
+struct SymCover {
+  int64_t bound = 0;
+  bool dense = true;
+};
+SymCover sym_cover(const fm::Factors& f, const std::string& sym) {
+  std::vector<const fm::Factor*> ts;
+  for (auto& x : f)
+    if (x.kind == fm::Factor::Term && x.sym == sym && x.count > 0) ts.push_back(&x);
+  SymCover c;
+  if (ts.empty()) return c;
+  std::sort(ts.begin(), ts.end(), [](const fm::Factor* a, const fm::Factor* b) { return a->weight < b->weight; });
+  int64_t expect = 1;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    if (ts[i]->weight != expect || (i + 1 < ts.size() && ts[i]->count != ts[i]->period)) c.dense = false;
+    expect = ts[i]->weight * ts[i]->period;
+    c.bound += (ts[i]->count - 1) * ts[i]->weight;
+  }
+  c.bound += 1;
+  return c;
+}
+
+int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, int32_t n_views,
+                           const char* const* views, const int32_t* allow_broadcast) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    check_buf(src, "src");
+    require(n_views >= 2 && views != nullptr, "transpose_chain: needs at least two views");
+    const int64_t eb = dtype_bytes(t);
+    std::vector<fm::Factors> v;
+    for (int i = 0; i < n_views; ++i) v.push_back(flat(views[i], "views[i]"));
+    const int steps = n_views - 1;
+    bool any_broadcast = false;
+    std::vector<ChainStep> cs(steps);
+    for (int k = 0; k < steps; ++k) {
+      const bool bc = allow_broadcast && allow_broadcast[k];
+      any_broadcast |= bc;
+      if (!bc)
+        require(fm::is_padding(fm::carve(v[k + 1], v[k])),
+                "transpose_chain: step " + std::to_string(k) + " adds axes absent from its source; allow its broadcast");
+      fm::Joint j = fm::sequence({v[k]}, {v[k + 1]}, fm::Mode::Carve);
+      const int64_t src_len = k == 0 ? (int64_t)(src->bytes / eb) : fm::size(v[k]);
+      const int64_t dst_len = k == steps - 1 ? (int64_t)(dst->bytes / eb) : fm::size(v[k + 1]);
+      const int64_t count = std::max<int64_t>(0, std::min<int64_t>({j.stream_size, fm::size(v[k + 1]), dst_len}));
+      require(max_live_offset(j.wheels, 0) < src_len || count == 0,
+              "transpose_chain: step " + std::to_string(k) + " reads past its source");
+      require(fm::size(v[k + 1]) < (1ll << 31), "transpose_chain: a view of more than 2^31 positions");
+      const int mem[1] = {0};
+      cs[k].w = to_desc<1>(j.wheels, mem);
+      cs[k].src_base = 0;
+      cs[k].count = (uint32_t)count;
+    }
+    if (cs[steps - 1].count == 0) return;
+    set_device(rt);
+
+    // Direct form: when every intermediate holds each coordinate the final view reads, exactly once
+    // and live, the chain moves each element from its source cell to its final cell untouched, so it
+    // is the one transpose first view -> last view (with that kernel's tiled and 16-byte paths). An
+    // axis the source lacks is a broadcast; an intermediate may lack it too (a transpose cannot drop
+    // an axis, so it was added by a later step), since no value depends on its coordinate.
+    bool direct = true;
+    for (auto& x : v.back())
+      if (x.kind == fm::Factor::Term && direct) {
+        const int64_t need = sym_cover(v.back(), x.sym).bound;
+        const bool in_src = sym_cover(v[0], x.sym).bound > 0;
+        for (int k = 1; k < steps && direct; ++k) {
+          const SymCover c = sym_cover(v[k], x.sym);
+          direct = c.bound == 0 ? !in_src : (c.dense && c.bound >= need);
+        }
+      }
+    if (direct) {
+      if (!any_broadcast) require(fm::is_padding(fm::carve(v.back(), v[0])), "transpose_chain: broadcast mismatch");
+      fm::Joint j = fm::sequence({v[0]}, {v.back()}, fm::Mode::Carve);
+      const int64_t count = std::min<int64_t>({j.stream_size, fm::size(v.back()), (int64_t)(dst->bytes / eb)});
+      require(max_live_offset(j.wheels, 0) < (int64_t)(src->bytes / eb), "transpose_chain: reads past the source");
+      const int mem[1] = {0};
+      launch_relayout(rt->stream, dst->ptr, src->ptr, eb, 0, 0, count, to_desc<1>(j.wheels, mem));
+      return;
+    }
+
+    // General form: groups of up to kMaxChain steps, each a back-walking gather; a group that ends
+    // on an intermediate materializes it (whole, zero where unwritten) in scratch.
+    const void* in = src->ptr;
+    int k0 = 0;
+    uint8_t* sc = nullptr;
+    uint64_t half = 0;
+    int flip = 0;
+    while (k0 < steps) {
+      const int k1 = std::min(steps, k0 + kMaxChain);
+      Chain c;
+      c.n = k1 - k0;
+      for (int k = k0; k < k1; ++k) c.step[k - k0] = cs[k];
+      void* out;
+      if (k1 == steps) {
+        c.total = cs[steps - 1].count;
+        c.zero_unwritten = 0;
+        out = dst->ptr;
+      } else {
+        if (!sc) {
+          int64_t most = 0;
+          for (int k = 1; k < steps; ++k) most = std::max(most, fm::size(v[k]));
+          half = ((uint64_t)most * eb + 255) & ~(uint64_t)255;
+          sc = (uint8_t*)scratch(rt, 2 * half);
+        }
+        c.total = (uint32_t)fm::size(v[k1]);
+        c.zero_unwritten = 1;
+        out = sc + (flip ? half : 0);
+        flip ^= 1;
+      }
+      launch_relayout_chain(rt->stream, out, in, eb, c);
+      in = out;
+      k0 = k1;
+    }
+  });
+}
+
 int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,
                      const char* dst_map) {
   return guard([&] {

@@ -259,6 +259,46 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
 }
 
 // ---------------------------------------------------------------------------------------------
+// Relayout chain (lazy relayout fusion): each final position walks back through the steps. A
+// position a step did not write reads as the zero of its fresh storage (Tensor::transpose zeroes
+// its destination, tensor/mod.rs:302-306); one the last step does not write is left alone.
+// ---------------------------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kBlock) k_relayout_chain(T* __restrict__ dst, const T* __restrict__ src, Chain c) {
+  const int unwritten = c.zero_unwritten ? 1 : 2;
+  for (uint32_t p = blockIdx.x * kBlock + threadIdx.x; p < c.total; p += gridDim.x * kBlock) {
+    int64_t pos = p;
+    int state = 0;  // 0: read src at pos, 1: zero, 2: not written
+    for (int k = c.n - 1; k >= 0; --k) {
+      const ChainStep& st = c.step[k];
+      if (pos >= (int64_t)st.count) {
+        state = k == c.n - 1 ? unwritten : 1;
+        break;
+      }
+      uint32_t q = (uint32_t)pos;
+      int64_t off = 0;
+      bool live = true;
+      for (int i = 0; i < st.w.n; ++i) {
+        const uint32_t nq = st.w.div[i].div(q);
+        const uint32_t d = q - nq * st.w.size[i];
+        live &= d < st.w.live[i];
+        off += (int64_t)d * st.w.stride[0][i];
+        q = nq;
+      }
+      if (!live) {
+        state = k == c.n - 1 ? unwritten : 1;
+        break;
+      }
+      pos = st.src_base + off;
+    }
+    if (state == 0)
+      dst[p] = src[pos];
+    else if (state == 1)
+      dst[p] = T(0);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // transmute: dst live rank k <- src live rank k (place_live_elems, storage/buf.rs:785-797).
 // `ds` walks dst wire positions (size = extent, live = count); `ss` maps a live rank to a src
 // wire position (size = live count, stride = wire place).
@@ -413,6 +453,21 @@ __global__ void __launch_bounds__(kBlock) k_scatter(T* __restrict__ dst, const T
 }
 
 }  // namespace
+
+void launch_relayout_chain(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, const Chain& c) {
+  dim3 g(grid_for((int64_t)c.total)), b(kBlock);
+  switch (elem_bytes) {
+    case 1:
+      hipLaunchKernelGGL(k_relayout_chain<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, c);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_relayout_chain<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, c);
+      break;
+    default:
+      hipLaunchKernelGGL(k_relayout_chain<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, c);
+  }
+  FO_HIP(hipGetLastError());
+}
 
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t eb, int64_t dst_base, int64_t src_base,
                      int64_t count, const Wheels<1>& w) {

@@ -103,6 +103,23 @@ Wheels<NMEM> to_desc(const std::vector<mapping::Wheel>& ws, const int (&mem)[NME
 // Transpose: dst[dst_base + p] = src[src_base + off(p)] for live p < count.
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_base, int64_t src_base,
                      int64_t count, const Wheels<1>& w);
+// A chain of full-view transposes as one gather. Step k writes its positions p < count (a live
+// digit walk of its wheels) into a fresh zeroed storage from src_base + off(p) of the previous one.
+// The kernel covers positions [0, total) of the last storage; those the last step does not write
+// are zeroed when `zero_unwritten` (the last storage is itself a fresh intermediate), else kept.
+constexpr int kMaxChain = 6;
+struct ChainStep {
+  Wheels<1> w;
+  int64_t src_base;
+  uint32_t count;
+};
+struct Chain {
+  int32_t n = 0;
+  int32_t zero_unwritten = 0;
+  uint32_t total = 0;
+  ChainStep step[kMaxChain];
+};
+void launch_relayout_chain(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, const Chain& c);
 // Gather: dst[off_d(p*slots + r)] = src[off_s(p*axis + index[r] / div)]; bad indices skipped, *flag = 1.
 // `*_slot_wheels`: how many innermost wheels of each list belong to the slot / axis part (the
 // payload's wheels follow), for the 16-byte payload path.

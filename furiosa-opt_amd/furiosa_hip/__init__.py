@@ -93,6 +93,8 @@ _sig = {
         C.c_int32,
         [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p, C.c_int32],
     ),
+    "fo_transpose_chain": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, C.POINTER(C.c_char_p),
+                                       C.POINTER(C.c_int32)]),
     "fo_reduce": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_int32, C.c_uint32, C.c_int32]),
     "fo_contraction": (
         C.c_int32,
@@ -222,6 +224,15 @@ class Runtime:
         _check(_lib.fo_transpose(self.h, dst.h, src.h, dtype, src_view.encode(), dst_view.encode(), _b(src_map),
                                  _b(dst_map), _b(json.dumps(src_offset) if src_offset else None),
                                  _b(json.dumps(dst_offset) if dst_offset else None), int(allow_broadcast)))
+
+    def transpose_chain(self, dst: "Buffer", src: "Buffer", dtype: int, views: Sequence[str],
+                        allow_broadcast: Optional[Sequence[bool]] = None):
+        """The full-view transposes views[0] -> views[1] -> ... as one pass; only the last is written."""
+        arr = (C.c_char_p * len(views))(*[v.encode() for v in views])
+        bc = None
+        if allow_broadcast is not None:
+            bc = (C.c_int32 * (len(views) - 1))(*[int(b) for b in allow_broadcast])
+        _check(_lib.fo_transpose_chain(self.h, dst.h, src.h, dtype, len(views), arr, bc))
 
     def map(self, dst: "Buffer", dst_t: int, src: "Buffer", src_t: int, n: int, op: FoOp):
         _check(_lib.fo_map(self.h, dst.h, dst_t, src.h, src_t, n, C.byref(op)))

@@ -240,6 +240,16 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
                        fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
                        const char* out_map);
 
+/* Lazy relayout fusion: the chain src -> views[1] -> ... -> views[n_views-1] of full-view
+ * transposes as Tensor::transpose runs them (tensor/mod.rs:302-306: each intermediate a fresh zeroed
+ * storage; BufStorage::transpose, storage/buf.rs:257-313), with only the last materialized, in dst.
+ * views[0] is src's mapping; step k (views[k] -> views[k+1]) may broadcast when allow_broadcast[k]
+ * (NULL: none may). The engine's fetch -> switch -> collect -> commit sequence of relayouts is such a
+ * chain. One HBM pass: a single transpose first -> last when every intermediate holds each
+ * coordinate the last view reads, else a gather walking each final cell back through the steps. */
+int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, int32_t n_views,
+                           const char* const* views, const int32_t* allow_broadcast);
+
 /* Backend::transmute (backend/mod.rs:228-232; BufStorage::transmute, storage/buf.rs:592-601):
  * compacts src's live cells (wire order) into dst's live cells (wire order); dst padding is 0. */
 int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_map,

@@ -12,6 +12,7 @@ images:
 
 Functions and their reference anchors:
   transpose        BufStorage::transpose        storage/buf.rs:257-313 (+ window_base :760-781)
+  transpose_chain  Tensor::transpose repeated    tensor/mod.rs:302-306 (pinned through transpose)
   reduce           BufStorage::reduce           storage/buf.rs:331-376
   contraction      BufStorage::contraction_in   storage/buf.rs:401-447 (ReadPlan :680-753)
   transmute        BufStorage::transmute        storage/buf.rs:592-601
@@ -156,6 +157,17 @@ def _additive(pos: np.ndarray, out_live: np.ndarray):
     if not np.array_equal(pos[good], base[good][:, None] + delta[None, :]):
         raise AssertionError("read plan is not additive in (out, residue)")
     return base, delta.astype(np.int64)
+
+
+def transpose_chain(dst: np.ndarray, src: np.ndarray, views: list) -> np.ndarray:
+    """Consecutive full-view transposes as Tensor::transpose runs them (tensor/mod.rs:302-306): each
+    intermediate a fresh zeroed storage of its view, the last written into `dst`."""
+    cur = src
+    for k in range(len(views) - 1):
+        last = k == len(views) - 2
+        nxt = dst if last else np.zeros(mr.size(views[k + 1]), dtype=src.dtype)
+        cur = transpose(nxt, cur, views[k], views[k + 1])
+    return cur
 
 
 def reduce(src: np.ndarray, dtype: int, src_map: dict, dst_map: dict, op: int, identity_bits: int) -> np.ndarray:

@@ -54,6 +54,80 @@ def test_transpose_pairs(rt, case, dt):
     run_transpose(rt, sizes, a, b, dt[0], dt[1], allow_broadcast=True)
 
 
+# The switch engine's data path is a broadcast-allowed transpose of the TuTensor layout
+# [Slice, Time, Packet] (engine/switch.rs:62-71, `self.inner.transpose(true)`). The slice / time
+# pairs below are the accepted routings of the reference's switch tests (engine/switch.rs:128-272,
+# with their axis sizes); a packet axis K is appended. Output axes absent from the input (X, Y, Z,
+# S) are broadcasts: every replica holds the same element.
+SWITCH_AXES = dict(A=16, B=16, C=8, D=2, E=2, P=4, Q=8, R=8, S=256, X=4, Y=2, Z=2, K=8)
+SWITCH_CASES = [
+    ("S", "C", "S", "C"),
+    ("A, B", "C", "B % 4, B / 4, A % 4, A / 4", "C"),
+    ("A, B", "C", "A, B % 4, B / 4", "C"),
+    ("R, Q, P", "C", "R, P, Q", "C"),
+    ("R # 16, Q # 16", "C", "Q # 16, R # 16", "C"),
+    ("R # 16, Q # 16", "C", "Q # 32, R # 8", "C"),
+    ("R # 16, Q # 16", "C", "R # 16, Q # 16 % 4, Q # 16 / 4", "C"),
+    ("A, B", "C", "A, B / 4, X", "C, B % 4"),
+    ("A, B", "C", "A / 2, Y, B / 2, Z", "C, A % 2, B % 2"),
+    ("A, B", "C", "A % 4, A / 4, B / 4, X", "C, B % 4"),
+    ("R, Q, P", "C", "R, P / 2, Q, Y", "C, P % 2"),
+    ("R, Q, P", "C", "R / 2, Y, Q, P / 2, Z", "C, R % 2, P % 2"),
+    ("A, B", "C", "S", "C, A, B"),
+    ("A, B", "C # 32", "A, B / 4, X", "C # 32, B % 4"),
+    ("P # 8, Q # 32", "C", "P # 8, Q # 32 / 4, X", "C, Q # 32 % 4"),
+    ("P # 16, Q # 16", "C", "P # 16, Q # 16 / 4, X", "C, Q # 16 % 4"),
+    ("P # 8, Q # 32", "C # 16", "P # 8, Q # 32 / 4, X", "C # 16, Q # 32 % 4"),
+]
+
+
+@pytest.mark.parametrize("case", SWITCH_CASES, ids=[f"{c[0]}|{c[1]} -> {c[2]}|{c[3]}" for c in SWITCH_CASES])
+@pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16)], ids=["i8", "bf16"])
+def test_switch_broadcast_routings(rt, case, dt):
+    ins, int_, outs, outt = case
+    run_transpose(rt, SWITCH_AXES, f"{ins}, {int_}, K", f"{outs}, {outt}, K", dt[0], dt[1], allow_broadcast=True)
+
+
+# Lazy relayout fusion: a chain of full-view transposes (fresh zeroed intermediates, as
+# Tensor::transpose makes them) in one call. The first four take the direct form (every
+# intermediate holds each final coordinate once, or lacks an axis that is broadcast later); the
+# others walk back through the steps: an intermediate whose Q % 4 digit is resized (not dense), and
+# nine views through such an intermediate (two gather passes through scratch).
+CHAIN_AXES = dict(R=64, C=96, A=20, B=12, X=4, K=8, Q=16)
+CHAINS = [
+    (["R, C", "C, R", "R / 8, C, R % 8", "C / 32, R, C % 32", "R, C"], None),
+    (["A, B, K", "A, B / 4, X, K, B % 4", "X, A, B, K"], [True, False]),
+    (["A, B", "A # 24, B", "B, A # 32", "A, B"], None),
+    (["A, B", "B, A", "B, X, A"], [False, True]),
+    (["Q, B", "Q / 4, B, Q % 4 = 2", "B, Q / 4, Q % 4 = 2"], None),
+    (["A, B", "B, A", "B, X, A", "X, A, B", "A, X, B", "B, A, X", "X, B, A", "A, B, X", "B, X, A"],
+     [False, True] + [False] * 6),
+    (["Q, B", "Q / 4, B, Q % 4 = 2", "B, Q / 4, Q % 4 = 2", "Q / 4, Q % 4 = 2, B", "B, Q / 4, Q % 4 = 2",
+      "Q / 4, X, B, Q % 4 = 2", "X, Q / 4, Q % 4 = 2, B", "B, Q / 4, Q % 4 = 2, X", "Q % 4 = 2, B, Q / 4, X"],
+     [False] * 4 + [True] + [False] * 3),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CHAINS)), ids=[" -> ".join(c[0]) for c in CHAINS])
+@pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16), (I32, np.int32)], ids=["i8", "bf16", "i32"])
+def test_transpose_chain(rt, case, dt):
+    views, bc = CHAINS[case]
+    rng = np.random.default_rng(20 + case)
+    parsed = [mr.parse(v, CHAIN_AXES) for v in views]
+    src = rand_words(rng, mr.size(parsed[0]), dt[1])
+    init = rand_words(rng, mr.size(parsed[-1]), dt[1])
+    want = emu.transpose_chain(init, src, parsed)
+    d = rt.upload(init)
+    rt.transpose_chain(d, rt.upload(src), dt[0], [fh.m(v, **CHAIN_AXES) for v in views], bc)
+    assert np.array_equal(d.read(dt[1]), want)
+
+
+def test_transpose_chain_requires_broadcast_flag(rt):
+    views = [fh.m(v, **CHAIN_AXES) for v in ("A, B", "B, A", "B, X, A")]
+    with pytest.raises(fh.FoError, match="allow its broadcast"):
+        rt.transpose_chain(rt.alloc(4 * 20 * 12 * 4), rt.alloc(20 * 12 * 4), I32, views)
+
+
 @pytest.mark.parametrize("case", SEQ_TABLES, ids=[c[2] for c in SEQ_TABLES])
 def test_transpose_doc_tables(rt, case):
     sizes, mem, stream, _ = case
