@@ -158,6 +158,17 @@ def bench_relayout(fh, rt, steps, warmup, rng):
         wall, ev = timed(rt, fn, steps, warmup)
         nbytes = 2 * R * C * 2
         out[name] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    return out
+
+
+def bench_chain(fh, rt, steps, warmup, rng):
+    """Relayout chains and the switch engine's broadcast routing (kept apart from bench_relayout so
+    that the copy kernel's counters calibrate on the copy alone)."""
+    R = C = 8192
+    s = dict(R=R, C=C)
+    src = rt.upload(rng.integers(0, 65535, R * C, dtype=np.uint16))
+    dst = rt.alloc(R * C * 2)
+    out = {}
     # lazy relayout fusion: the three-step chain R,C -> R/8,C,R%8 -> C/64,R,C%64 -> C,R in one call
     # (it collapses to the one transpose R,C -> C,R), against the same three steps materialized
     views = [fh.m(t, **s) for t in ("R, C", "R / 8, C, R % 8", "C / 64, R, C % 64", "C, R")]
@@ -280,7 +291,7 @@ def main():
     only = set(filter(None, args.only.split(",")))
     res = {}
     for name, fnb in (("gemm", bench_gemm), ("gemm_f8", bench_gemm_f8), ("norm", bench_norm),
-                      ("attention", bench_attention),
+                      ("attention", bench_attention), ("chain", bench_chain),
                       ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout),
                       ("scatter_gather", bench_scatter_gather)):
         if only and name not in only:
@@ -313,8 +324,8 @@ def main():
     if "scatter_gather" in res:
         for k, r in res["scatter_gather"].items():
             configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
-    if "relayout" in res:
-        for k, r in res["relayout"].items():
+    for group in ("relayout", "chain"):
+        for k, r in res.get(group, {}).items():
             name = "switch_broadcast_256x512x64_x4_bf16" if k == "switch_broadcast" else f"relayout_{k}_8192x8192_bf16"
             configs[name] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     if g:
