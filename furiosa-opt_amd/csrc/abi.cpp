@@ -1,7 +1,9 @@
 // The C ABI (include/furiosa_hip.h): handle management, error translation, and the host-side
 // planning that turns each Backend seam call's mappings into kernel descriptors.
 #include <algorithm>
+#include <cstdio>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -61,6 +63,45 @@ void check_buf(const fo_buffer* b, const char* what) {
 }
 
 void set_device(fo_runtime* rt) { FO_HIP(hipSetDevice(rt->device)); }
+
+// One op's trace span: events recorded on the runtime's stream before and after its launches.
+struct TraceScope {
+  fo_runtime* rt;
+  const char* name;
+  hipEvent_t begin = nullptr;
+  TraceScope(fo_runtime* r, const char* n) : rt(r), name(n) {
+    if (!rt->trace_sink) return;
+    FO_HIP(hipEventCreate(&begin));
+    FO_HIP(hipEventRecord(begin, rt->stream));
+  }
+  ~TraceScope() {
+    if (!begin) return;
+    hipEvent_t end = nullptr;
+    if (hipEventCreate(&end) == hipSuccess && hipEventRecord(end, rt->stream) == hipSuccess) {
+      rt->spans.push_back({name, begin, end});
+    } else {
+      (void)hipEventDestroy(begin);
+      if (end) (void)hipEventDestroy(end);
+    }
+  }
+};
+
+// Hands the recorded spans to the sink (the stream has drained), then releases their events.
+void flush_trace(fo_runtime* rt) {
+  if (rt->spans.empty()) return;
+  std::vector<fo_runtime::Span> spans;
+  spans.swap(rt->spans);
+  for (auto& sp : spans) {
+    float b = 0.f, e = 0.f;
+    if (rt->trace_sink && rt->trace_base && hipEventElapsedTime(&b, rt->trace_base, sp.begin) == hipSuccess &&
+        hipEventElapsedTime(&e, rt->trace_base, sp.end) == hipSuccess)
+      rt->trace_sink(rt->trace_ctx, sp.name, std::strlen(sp.name), (uint64_t)((double)b * 1e6),
+                     (uint64_t)((double)e * 1e6));
+    (void)hipEventDestroy(sp.begin);
+    (void)hipEventDestroy(sp.end);
+  }
+  if (rt->trace_done) rt->trace_done(rt->trace_ctx);
+}
 
 // The live-digit sub-odometer of a wheel list (digits >= live are padding and never folded).
 std::vector<fm::Wheel> live_only(const std::vector<fm::Wheel>& ws) {
@@ -144,6 +185,81 @@ int64_t product(const std::vector<fm::Wheel>& ws) {
   return p;
 }
 
+// ---- safetensors -----------------------------------------------------------------------------
+// safetensors host loading at the boundary: HostTensor::from_safetensors (furiosa-opt-std/src/
+// tensor/memory.rs:190-223) for a file on disk, so weights reach HBM without a host-side copy of
+// the whole file in another format.
+//
+// File layout (the safetensors format): an 8-byte little-endian header length N, N bytes of JSON
+// mapping each tensor name to {"dtype", "shape", "data_offsets": [begin, end]} (offsets relative to
+// the byte after the header; an optional "__metadata__" entry), then the data. The reference
+// checks the view's shape against the pair-flattened sizes of the element mapping and its byte
+// length against the mapping's size; the bytes are then the packed device image as they are.
+
+struct TensorInfo {
+  std::string dtype;
+  std::vector<int64_t> shape;
+  uint64_t begin = 0, end = 0;  // absolute file offsets of the data
+};
+
+struct File {
+  FILE* f = nullptr;
+  explicit File(const char* path) : f(std::fopen(path, "rb")) {}
+  ~File() {
+    if (f) std::fclose(f);
+  }
+};
+
+TensorInfo find_tensor(File& file, const char* path, const char* name) {
+  require(file.f != nullptr, std::string("safetensors: cannot open '") + path + "'");
+  unsigned char len8[8];
+  require(std::fread(len8, 1, 8, file.f) == 8, "safetensors: file shorter than its header length");
+  uint64_t n = 0;
+  for (int i = 7; i >= 0; --i) n = (n << 8) | len8[i];
+  require(n > 0 && n < (1ull << 30), "safetensors: implausible header length");
+  std::string header(n, '\0');
+  require(std::fread(&header[0], 1, n, file.f) == n, "safetensors: truncated header");
+  std::fseek(file.f, 0, SEEK_END);
+  const uint64_t file_size = (uint64_t)std::ftell(file.f);
+  fo::json::Value h = fo::json::parse(header);
+  require(h.kind == fo::json::Value::Object, "safetensors: the header is not a JSON object");
+  const fo::json::Value* t = h.get(name);
+  require(t != nullptr && std::string(name) != "__metadata__", std::string("safetensors: no tensor '") + name + "'");
+  TensorInfo info;
+  info.dtype = t->at("dtype").as_str();
+  for (auto& d : t->at("shape").arr) info.shape.push_back(d.as_int());
+  const fo::json::Value& off = t->at("data_offsets");
+  require(off.kind == fo::json::Value::Array && off.arr.size() == 2, "safetensors: data_offsets is not a pair");
+  const int64_t b = off.arr[0].as_int(), e = off.arr[1].as_int();
+  require(b >= 0 && e >= b, "safetensors: bad data_offsets");
+  info.begin = 8 + n + (uint64_t)b;
+  info.end = 8 + n + (uint64_t)e;
+  require(info.end <= file_size, "safetensors: data_offsets past the end of the file");
+  return info;
+}
+
+// flat_shape (memory.rs:204-212): a Pair contributes its two sides, anything else its size.
+void flat_shape(const fm::NodeP& m, std::vector<int64_t>& out) {
+  if (m->kind == fm::Node::Pair) {
+    flat_shape(m->a, out);
+    flat_shape(m->b, out);
+  } else {
+    out.push_back(fm::size(m));
+  }
+}
+
+int32_t dtype_code(const std::string& s) {
+  if (s == "I8") return FO_I8;
+  if (s == "U8") return FO_U8;
+  if (s == "I16") return FO_I16;
+  if (s == "I32") return FO_I32;
+  if (s == "BF16") return FO_BF16;
+  if (s == "F32") return FO_F32;
+  if (s == "F8_E4M3") return FO_F8E4M3;
+  if (s == "F8_E5M2") return FO_F8E5M2;
+  return -1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -182,6 +298,11 @@ void fo_runtime_free(fo_runtime* rt) {
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto& e : rt->events)
     if (e) (void)hipEventDestroy(e);
+  for (auto& sp : rt->spans) {
+    (void)hipEventDestroy(sp.begin);
+    (void)hipEventDestroy(sp.end);
+  }
+  if (rt->trace_base) (void)hipEventDestroy(rt->trace_base);
   if (rt->scratch) (void)hipFree(rt->scratch);
   if (rt->err_host) (void)hipHostFree(rt->err_host);
   if (rt->stream) (void)hipStreamDestroy(rt->stream);
@@ -192,6 +313,27 @@ int32_t fo_runtime_synchronize(fo_runtime* rt) {
   return guard([&] {
     check_rt(rt);
     FO_HIP(hipStreamSynchronize(rt->stream));
+    flush_trace(rt);
+  });
+}
+
+int32_t fo_runtime_set_trace(fo_runtime* rt, fo_trace_sink sink, fo_trace_done done, void* ctx) {
+  return guard([&] {
+    check_rt(rt);
+    set_device(rt);
+    FO_HIP(hipStreamSynchronize(rt->stream));
+    flush_trace(rt);  // spans of the previous sink go to it
+    if (rt->trace_base) {
+      (void)hipEventDestroy(rt->trace_base);
+      rt->trace_base = nullptr;
+    }
+    rt->trace_sink = sink;
+    rt->trace_done = done;
+    rt->trace_ctx = ctx;
+    if (sink) {
+      FO_HIP(hipEventCreate(&rt->trace_base));
+      FO_HIP(hipEventRecord(rt->trace_base, rt->stream));
+    }
   });
 }
 
@@ -255,6 +397,7 @@ int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* ds
     require(host != nullptr || bytes == 0, "host pointer is NULL");
     require(bytes <= dst->bytes, "write of " + std::to_string(bytes) + " bytes exceeds the buffer");
     set_device(rt);
+    TraceScope trace_span(rt, "write");
     FO_HIP(hipMemcpyAsync(dst->ptr, host, bytes, hipMemcpyHostToDevice, rt->stream));
     FO_HIP(hipStreamSynchronize(rt->stream));
   });
@@ -267,6 +410,7 @@ int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes
     require(host != nullptr || bytes == 0, "host pointer is NULL");
     require(bytes <= src->bytes, "read of " + std::to_string(bytes) + " bytes exceeds the buffer");
     set_device(rt);
+    TraceScope trace_span(rt, "read");
     FO_HIP(hipMemcpyAsync(host, src->ptr, bytes, hipMemcpyDeviceToHost, rt->stream));
     FO_HIP(hipStreamSynchronize(rt->stream));
   });
@@ -352,6 +496,7 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
     if (n == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "map");
     launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
   });
 }
@@ -369,6 +514,7 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
             "zip_with: n exceeds a buffer");
     if (n == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "zip_with");
     launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
   });
 }
@@ -391,6 +537,7 @@ int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, con
     }
     if (n == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "zip3_slots");
     launch_zip3_slots(rt->stream, dst->ptr, data->ptr, slots->has_port ? port->ptr : nullptr,
                       (const uint8_t*)tag_u8->ptr, t, n, *slots);
   });
@@ -422,6 +569,7 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     require(src_base + max_live_offset(j.wheels, 0) < src_len, "transpose: the src window reads past the buffer");
     require(count < (1ll << 31), "transpose: more than 2^31 positions");
     set_device(rt);
+    TraceScope trace_span(rt, "transpose");
     const int mem[1] = {0};
     launch_relayout(rt->stream, dst->ptr, src->ptr, eb, dst_base, src_base, count, to_desc<1>(j.wheels, mem));
   });
@@ -483,6 +631,7 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
     }
     if (cs[steps - 1].count == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "transpose_chain");
 
     // Direct form: when every intermediate holds each coordinate the final view reads, exactly once
     // and live, the chain moves each element from its source cell to its final cell untouched, so it
@@ -577,6 +726,7 @@ int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     if (dn == 0) return;
     require(dn < (1ll << 31), "transmute: more than 2^31 positions");
     set_device(rt);
+    TraceScope trace_span(rt, "transmute");
     const int mem[1] = {0};
     launch_transmute(rt->stream, dst->ptr, src->ptr, eb, dn, to_desc<1>(dw, mem), to_desc<1>(sw, mem));
   });
@@ -614,6 +764,7 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     require(div < (1ll << 31), "scatter: payload block too large");
     if (np * keys == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "scatter");
     int32_t* flag = error_word(rt);
     int32_t* win = (int32_t*)scratch(rt, (uint64_t)axis_size * 4);
     FO_HIP(hipMemsetAsync(win, 0xff, (size_t)axis_size * 4, rt->stream));  // -1: no key yet
@@ -652,6 +803,7 @@ int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo
     require(div < (1ll << 31), "gather: payload block too large");
     if (np * slots == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "gather");
     int32_t* flag = error_word(rt);
     const int mem[1] = {0};
     launch_gather(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, slots, axis_size, (int32_t)div,
@@ -687,6 +839,7 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     require(out_count < (1ll << 31), "reduce: more than 2^31 output cells");
     if (out_count == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "reduce");
     const int mem[1] = {0};
     launch_reduce(rt->stream, dst->ptr, src->ptr, t, (int64_t)(src->bytes / eb), out_count, to_desc<1>(ow, mem),
                   to_desc<1>(rw, mem), op, identity);
@@ -719,6 +872,7 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     require(out_t != FO_I4 || out_count % 2 == 0, "contraction: a 4-bit output stream needs an even cell count");
     if (out_count == 0) return;
     set_device(rt);
+    TraceScope trace_span(rt, "contraction");
 
     // i4 operands (ContractionCast for i4: widen to i32, cast.rs:365-367) are unpacked to one i8 per
     // element in scratch, exactly, and contracted as i8; an i4 result is computed as i32 and packed
@@ -819,6 +973,7 @@ int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, c
                 (uint64_t)(cols * 2) <= gain->bytes,
             "rmsnorm_softmax: shape exceeds a buffer");
     set_device(rt);
+    TraceScope trace_span(rt, "rmsnorm_softmax");
     launch_rmsnorm_softmax(rt->stream, (uint16_t*)out->ptr, (const uint16_t*)x->ptr, (const uint16_t*)gain->ptr, rows,
                            cols, eps);
   });
@@ -839,6 +994,7 @@ int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q,
     require(bytes <= q->bytes && bytes <= k->bytes && bytes <= v->bytes && bytes <= out->bytes,
             "attention: shape exceeds a buffer");
     set_device(rt);
+    TraceScope trace_span(rt, "attention_prefill");
     launch_attention_prefill(rt->stream, (uint16_t*)out->ptr, (const uint16_t*)q->ptr, (const uint16_t*)k->ptr,
                              (const uint16_t*)v->ptr, batch, heads, seq, head_dim, sqrt_d, causal);
   });
@@ -861,6 +1017,7 @@ int32_t fo_gemm_w8a8_dequant(fo_runtime* rt, fo_buffer* out, fo_buffer* acc_out,
       require((uint64_t)(m * n * 4) <= acc_out->bytes, "w8a8: shape exceeds acc_out");
     }
     set_device(rt);
+    TraceScope trace_span(rt, "gemm_w8a8_dequant");
     launch_w8a8(rt->stream, (uint16_t*)out->ptr, acc_out ? (int32_t*)acc_out->ptr : nullptr, (const int8_t*)a->ptr,
                 (const int8_t*)w->ptr, (const float*)scale->ptr, m, n, k);
   });
@@ -888,9 +1045,60 @@ int32_t fo_mlp(fo_runtime* rt, fo_buffer* pred_i32, fo_buffer* logits, const fo_
       require((uint64_t)(batch * out_features * 2) <= logits->bytes, "mlp: shape exceeds logits");
     }
     set_device(rt);
+    TraceScope trace_span(rt, "mlp");
     launch_mlp(rt->stream, (int32_t*)pred_i32->ptr, logits ? (uint16_t*)logits->ptr : nullptr,
                (const uint16_t*)x->ptr, (const uint16_t*)w1->ptr, (const uint16_t*)b1->ptr, (const uint16_t*)w2->ptr,
                (const uint16_t*)b2->ptr, batch, in_features, hidden, out_features);
+  });
+}
+
+// ---- safetensors ----------------------------------------------------------------------------------
+
+int32_t fo_safetensors_info(const char* path, const char* name, int32_t* dtype, int64_t* shape, int32_t cap,
+                            int32_t* rank, uint64_t* data_begin, uint64_t* data_end) {
+  return guard([&] {
+    require(path != nullptr && name != nullptr, "safetensors: path or name is NULL");
+    File file(path);
+    TensorInfo info = find_tensor(file, path, name);
+    if (dtype) *dtype = dtype_code(info.dtype);
+    if (rank) *rank = (int32_t)info.shape.size();
+    for (int32_t i = 0; shape && i < cap && i < (int32_t)info.shape.size(); ++i) shape[i] = info.shape[i];
+    if (data_begin) *data_begin = info.begin;
+    if (data_end) *data_end = info.end;
+  });
+}
+
+int32_t fo_safetensors_load(fo_runtime* rt, fo_buffer* dst, const char* path, const char* name, fo_dtype t,
+                            const char* element_map) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(dst, "dst");
+    require(path != nullptr && name != nullptr && element_map != nullptr, "safetensors: NULL argument");
+    fm::NodeP m = fm::parse_json(element_map);
+    File file(path);
+    TensorInfo info = find_tensor(file, path, name);
+    std::vector<int64_t> want;
+    flat_shape(m, want);
+    // TensorInvalidInfo (memory.rs:213-220): the shape and the byte length must match the mapping.
+    require(info.shape == want, "safetensors: the tensor's shape is not the element mapping's pair-flattened sizes");
+    const uint64_t bytes = span_bytes(t, (uint64_t)fm::size(m));
+    require(info.end - info.begin == bytes, "safetensors: the tensor's byte length does not match the mapping");
+    require(bytes <= dst->bytes, "safetensors: dst buffer smaller than the tensor");
+    set_device(rt);
+    TraceScope trace_span(rt, "safetensors_load");
+    // Stream through a pinned staging buffer in 64 MiB pieces.
+    const uint64_t piece = std::min<uint64_t>(bytes, 64ull << 20);
+    if (bytes == 0) return;
+    void* stage = nullptr;
+    FO_HIP(hipHostMalloc(&stage, piece, hipHostMallocDefault));
+    std::unique_ptr<void, void (*)(void*)> guard_stage(stage, [](void* p) { (void)hipHostFree(p); });
+    std::fseek(file.f, (long)info.begin, SEEK_SET);
+    for (uint64_t done = 0; done < bytes; done += piece) {
+      const uint64_t len = std::min(piece, bytes - done);
+      require(std::fread(stage, 1, len, file.f) == len, "safetensors: short read");
+      FO_HIP(hipMemcpyAsync((uint8_t*)dst->ptr + done, stage, len, hipMemcpyHostToDevice, rt->stream));
+      FO_HIP(hipStreamSynchronize(rt->stream));
+    }
   });
 }
 

@@ -6,8 +6,10 @@
 //
 // Layout: one wave64 per row; lane l holds the 16-byte chunks c*64 + l (8 bf16 each), so every wave
 // load or store is 1 KiB contiguous. The row stays packed as bf16 in registers (x, then y); the
-// waves are persistent (a grid-stride loop over rows) and prefetch the next row's x while the
-// current one is computed, so the load stream never drains. The gain is staged once per block in
+// waves are persistent (a grid-stride loop over rows) and keep the next two rows' x in flight while
+// the current one is computed, so the load stream never drains. exp(y - max) is evaluated twice
+// (for the sum, then for the output) rather than held, which frees the registers the second
+// prefetched row needs at two waves per SIMD. The gain is staged once per block in
 // LDS as f32.
 //
 // Numerics. This file is compiled with f32 denormals flushed (inputs and results, sign kept),
@@ -86,7 +88,7 @@ __device__ void row_exact(uint16_t* __restrict__ orow, const uint16_t* __restric
 
 // NCH 16-byte chunks per lane: cols = NCH * 512.
 template <int NCH>
-__global__ void __launch_bounds__(256) k_rmsnorm_softmax(uint16_t* __restrict__ out, const uint16_t* __restrict__ x,
+__global__ void __launch_bounds__(256, 2) k_rmsnorm_softmax(uint16_t* __restrict__ out, const uint16_t* __restrict__ x,
                                                          const uint16_t* __restrict__ gain, int64_t rows, float cols_f,
                                                          float eps) {
   constexpr int cols = NCH * 512;
@@ -114,16 +116,21 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax(uint16_t* __restrict__ 
   int64_t row = wave;
   if (row >= rows) return;
 
-  i32x4_t cur[NCH], nxt[NCH];
+  i32x4_t cur[NCH], nxt[NCH], nx2[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) cur[c] = __builtin_nontemporal_load((const i32x4_t*)(x + row * cols + (c * 64 + lane) * 8));
+  if (row + nwaves < rows) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      nxt[c] = __builtin_nontemporal_load((const i32x4_t*)(x + (row + nwaves) * cols + (c * 64 + lane) * 8));
+  }
 
   for (; row < rows; row += nwaves) {
-    const int64_t nrow = row + nwaves;
-    if (nrow < rows) {
+    const int64_t nrow = row + nwaves, n2row = row + 2 * nwaves;
+    if (n2row < rows) {
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        nxt[c] = __builtin_nontemporal_load((const i32x4_t*)(x + nrow * cols + (c * 64 + lane) * 8));
+        nx2[c] = __builtin_nontemporal_load((const i32x4_t*)(x + n2row * cols + (c * 64 + lane) * 8));
     }
     // sum of squares: each square rounded, then added (MulF with the stash, then the Add reduce)
     float ss = 0.f;
@@ -167,16 +174,13 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax(uint16_t* __restrict__ 
       const float L2E = 1.4426950408889634f;
       const float mxl = mx * L2E;
       float s = 0.f;
-      f32x2_t pe[NCH][4];
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           uint32_t w = (uint32_t)cur[c][e];
-          pe[c][e][0] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(w), L2E, -mxl));
-          pe[c][e][1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(w), L2E, -mxl));
-          s += pe[c][e][0];
-          s += pe[c][e][1];
+          s += __builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(w), L2E, -mxl));
+          s += __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(w), L2E, -mxl));
         }
       s = wave_sum(s);
       const float sinv = __builtin_amdgcn_rcpf(s);
@@ -184,13 +188,20 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax(uint16_t* __restrict__ 
       for (int c = 0; c < NCH; ++c) {
         i32x4_t o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = (int)pack_bf16(pe[c][e][0] * sinv, pe[c][e][1] * sinv);
+        for (int e = 0; e < 4; ++e) {
+          uint32_t w = (uint32_t)cur[c][e];
+          o[e] = (int)pack_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(w), L2E, -mxl)) * sinv,
+                                __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(w), L2E, -mxl)) * sinv);
+        }
         __builtin_nontemporal_store(o, (i32x4_t*)(orow + (c * 64 + lane) * 8));
       }
     }
     if (nrow < rows) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) cur[c] = nxt[c];
+      for (int c = 0; c < NCH; ++c) {
+        cur[c] = nxt[c];
+        nxt[c] = nx2[c];
+      }
     }
   }
 }

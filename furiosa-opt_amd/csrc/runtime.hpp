@@ -23,6 +23,17 @@ struct fo_runtime {
   uint64_t scratch_bytes = 0;
   int32_t* err_host = nullptr;  // pinned, device-mapped error word: kernels set it only on failure
   int32_t* err_dev = nullptr;   // its device address
+  // Trace spans (fo_runtime_set_trace): while a sink is set, every op brackets its launches with a
+  // pair of events; the spans are read back and handed to the sink at the next synchronize.
+  fo_trace_sink trace_sink = nullptr;
+  fo_trace_done trace_done = nullptr;
+  void* trace_ctx = nullptr;
+  hipEvent_t trace_base = nullptr;
+  struct Span {
+    const char* name;
+    hipEvent_t begin, end;
+  };
+  std::vector<Span> spans;
 };
 
 struct fo_buffer {

@@ -65,11 +65,14 @@ class FoSlots(C.Structure):
 
 
 _P = C.c_void_p
+TRACE_SINK = C.CFUNCTYPE(None, C.c_void_p, C.POINTER(C.c_char), C.c_uint64, C.c_uint64, C.c_uint64)
+TRACE_DONE = C.CFUNCTYPE(None, C.c_void_p)
 _sig = {
     "fo_last_error": (C.c_char_p, []),
     "fo_runtime_init": (C.c_int32, [C.c_int32, C.POINTER(_P)]),
     "fo_runtime_free": (None, [_P]),
     "fo_runtime_synchronize": (C.c_int32, [_P]),
+    "fo_runtime_set_trace": (C.c_int32, [_P, TRACE_SINK, TRACE_DONE, _P]),
     "fo_runtime_device_info": (C.c_int32, [_P, C.POINTER(C.c_int32), C.c_char_p, C.c_uint64]),
     "fo_buffer_alloc": (C.c_int32, [_P, C.c_uint64, C.POINTER(_P)]),
     "fo_buffer_free": (None, [_P]),
@@ -95,6 +98,9 @@ _sig = {
     ),
     "fo_transpose_chain": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_int32, C.POINTER(C.c_char_p),
                                        C.POINTER(C.c_int32)]),
+    "fo_safetensors_load": (C.c_int32, [_P, _P, C.c_char_p, C.c_char_p, C.c_int32, C.c_char_p]),
+    "fo_safetensors_info": (C.c_int32, [C.c_char_p, C.c_char_p, C.POINTER(C.c_int32), C.POINTER(C.c_int64), C.c_int32,
+                                        C.POINTER(C.c_int32), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     "fo_reduce": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_int32, C.c_uint32, C.c_int32]),
     "fo_contraction": (
         C.c_int32,
@@ -234,6 +240,20 @@ class Runtime:
             bc = (C.c_int32 * (len(views) - 1))(*[int(b) for b in allow_broadcast])
         _check(_lib.fo_transpose_chain(self.h, dst.h, src.h, dtype, len(views), arr, bc))
 
+    def set_trace(self, on_span=None, on_done=None):
+        """on_span(name, begin_ns, end_ns) per executed op, delivered at sync(); None turns tracing off."""
+        if on_span is None:
+            self._trace = None
+            _check(_lib.fo_runtime_set_trace(self.h, TRACE_SINK(), TRACE_DONE(), None))
+            return
+        sink = TRACE_SINK(lambda ctx, name, n, b, e: on_span(C.string_at(name, n).decode(), b, e))
+        done = TRACE_DONE(lambda ctx: on_done() if on_done else None)
+        self._trace = (sink, done)  # the callbacks live as long as the runtime uses them
+        _check(_lib.fo_runtime_set_trace(self.h, sink, done, None))
+
+    def load_safetensors(self, dst: "Buffer", path: str, name: str, dtype: int, element_map: str):
+        _check(_lib.fo_safetensors_load(self.h, dst.h, str(path).encode(), name.encode(), dtype, element_map.encode()))
+
     def map(self, dst: "Buffer", dst_t: int, src: "Buffer", src_t: int, n: int, op: FoOp):
         _check(_lib.fo_map(self.h, dst.h, dst_t, src.h, src_t, n, C.byref(op)))
 
@@ -313,6 +333,16 @@ class Buffer:
         out = np.empty(n, dtype=dt)
         _check(_lib.fo_read(self.rt.h, self.h, out.ctypes.data, out.nbytes))
         return out
+
+
+def safetensors_info(path: str, name: str):
+    """(dtype code or -1, shape, (data_begin, data_end)) of one tensor of a safetensors file; host only."""
+    dt, rank = C.c_int32(), C.c_int32()
+    shape = (C.c_int64 * 16)()
+    b, e = C.c_uint64(), C.c_uint64()
+    _check(_lib.fo_safetensors_info(str(path).encode(), name.encode(), C.byref(dt), shape, 16, C.byref(rank),
+                                    C.byref(b), C.byref(e)))
+    return dt.value, [shape[i] for i in range(min(rank.value, 16))], (b.value, e.value)
 
 
 def op(code: str, flags: int = 0, imm0=0, imm1=0) -> FoOp:

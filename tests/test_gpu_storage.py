@@ -540,3 +540,50 @@ def test_scatter_gather_bad_index_is_an_error(rt, bad):
     with pytest.raises(fh.FoError, match="index"):
         rt.scatter(cache, rt.upload(np.ones(4 * 5, np.int32)), idx, I32, fh.m("G, D", **s2), fh.m("G", **s2),
                    fh.m("K, D", **s2), fh.m("G", **s2), scaled=False)
+
+
+# ---- safetensors loading (tensor/memory.rs:190-223) ------------------------------------------------
+
+
+def test_safetensors_load(rt, tmp_path):
+    from test_safetensors import write_raw
+    rng = np.random.default_rng(90)
+    w1 = emu.f32_to_bf16(rng.standard_normal(128 * 784).astype(np.float32))  # the MNIST fc1 layout
+    b8 = rng.integers(-128, 128, 40).astype(np.int8)
+    p = tmp_path / "m.safetensors"
+    write_raw(p, [("fc1.weight", "BF16", (128, 784), w1.tobytes()), ("q", "I8", (5, 8), b8.tobytes())])
+    d = rt.alloc(w1.nbytes)
+    rt.load_safetensors(d, p, "fc1.weight", BF16, fh.m("H, X", H=128, X=784))
+    assert np.array_equal(d.read(np.uint16), w1)
+    d8 = rt.alloc(64)
+    rt.load_safetensors(d8, p, "q", I8, fh.m("A / 8, A % 8", A=40))  # pair-flattened [5, 8]
+    assert np.array_equal(d8.read(np.int8)[:40], b8)
+    with pytest.raises(fh.FoError, match="pair-flattened"):
+        rt.load_safetensors(d, p, "fc1.weight", BF16, fh.m("X, H", H=128, X=784))
+    with pytest.raises(fh.FoError, match="byte length"):
+        rt.load_safetensors(d, p, "fc1.weight", F32, fh.m("H, X", H=128, X=784))
+
+
+# ---- trace spans (backend/npu/ffi.rs:13-66) --------------------------------------------------------
+
+
+def test_trace_spans(rt):
+    spans, dones = [], []
+    rt.set_trace(lambda n, b, e: spans.append((n, b, e)), lambda: dones.append(1))
+    try:
+        s = dict(R=512, C=256)
+        x = rt.upload(np.arange(512 * 256, dtype=np.int32))
+        y = rt.alloc(512 * 256 * 4)
+        rt.transpose(y, x, I32, fh.m("R, C", **s), fh.m("C, R", **s))
+        rt.map(x, I32, y, I32, 512 * 256, fh.op("ADD_FXP", fh.RHS_IMM, 1))
+        rt.sync()
+        assert [n for n, _, _ in spans] == ["write", "transpose", "map"] and dones == [1]  # upload = fo_write
+        assert all(b <= e for _, b, e in spans)
+        assert all(spans[i][2] <= spans[i + 1][1] for i in range(2))  # one stream: in order
+        rt.sync()
+        assert len(spans) == 3 and dones == [1]  # nothing new to report
+    finally:
+        rt.set_trace(None)
+    rt.map(x, I32, y, I32, 16, fh.op("ADD_FXP", fh.RHS_IMM, 1))
+    rt.sync()
+    assert len(spans) == 3
