@@ -277,6 +277,9 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     const int kv0 = j * kBN;
     load_k(kv0 + 2 * kBN);
     load_v(kv0 + kBN);
+    // Keep the loads here: left to itself the scheduler sinks them next to their LDS stores at the
+    // end of the step (to save registers), exposing the whole global latency every step.
+    __builtin_amdgcn_sched_barrier(0);
     attn_step<D, false>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
                         g, col);
     store_k(j & 1);
@@ -289,6 +292,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     const int kv0 = j * kBN;
     load_k(kv0 + 2 * kBN);
     load_v(kv0 + kBN);
+    __builtin_amdgcn_sched_barrier(0);
     if (!(causal && kv0 > q0w + 31))  // wave-uniform
       attn_step<D, true>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
                          g, col);
