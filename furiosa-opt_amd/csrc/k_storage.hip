@@ -119,15 +119,17 @@ __global__ void __launch_bounds__(256) k_relayout_tiled(T* __restrict__ dst, con
 // (sizes, bases and strides multiples of V = 16 / sizeof(T) elements, both wheels fully live):
 // src rows are read and dst rows written as 16-byte vectors, the transpose happens in LDS (element
 // scatter in, 16-byte reads out).
-template <typename T>
+// TS0 x TSJ tiles (elements along wheel 0 x wheel jw): 64 x 64, or one chunk wide on the side
+// whose run is one chunk long, with as many elements as a 64 x 64 tile.
+template <typename T, int TS0, int TSJ>
 __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, const T* __restrict__ src,
                                                           int64_t dst_base, int64_t src_base, Wheels<1> w, int jw,
                                                           uint32_t outer_count, uint32_t tiles0, uint32_t tilesj) {
   typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
   constexpr int V = 16 / sizeof(T);  // elements per 16-byte chunk
-  constexpr int TS = 64;             // tile edge in elements
-  constexpr int CPR = TS / V;        // chunks per tile row
-  __shared__ __attribute__((aligned(16))) T tile[TS][TS + V];  // [j][d0], rows padded by one chunk
+  constexpr int CPR = TSJ / V;       // chunks per tile row on the read side (along j)
+  constexpr int CPW = TS0 / V;       // chunks per tile row on the write side (along d0)
+  __shared__ __attribute__((aligned(16))) T tile[TSJ][TS0 + V];  // [j][d0], rows padded by one chunk
   uint32_t bid = blockIdx.x;
   uint32_t t0 = bid % tiles0;
   bid /= tiles0;
@@ -158,9 +160,9 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
   if (!live_outer) return;  // uniform: a dead outer digit leaves the whole tile unwritten
   const uint32_t n0 = w.size[0], nj = w.size[jw];
   const int64_t s0 = w.stride[0][0];
-  for (int c = threadIdx.x; c < TS * CPR; c += 256) {
+  for (int c = threadIdx.x; c < TS0 * CPR; c += 256) {
     const int r = c / CPR, cc = c % CPR;  // src row d0 = r, chunk cc along j
-    const uint32_t d0 = t0 * TS + r, j0 = tj * TS + cc * V;
+    const uint32_t d0 = t0 * TS0 + r, j0 = tj * TSJ + cc * V;
     if (d0 < n0 && j0 < nj) {
       vec_t v = *(const vec_t*)(src + src_base + soff + (int64_t)d0 * s0 + j0);
       const T* e = (const T*)&v;
@@ -169,9 +171,9 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
     }
   }
   __syncthreads();
-  for (int c = threadIdx.x; c < TS * CPR; c += 256) {
-    const int r = c / CPR, cc = c % CPR;  // dst row j = r, chunk cc along d0
-    const uint32_t dj = tj * TS + r, d0 = t0 * TS + cc * V;
+  for (int c = threadIdx.x; c < TSJ * CPW; c += 256) {
+    const int r = c / CPW, cc = c % CPW;  // dst row j = r, chunk cc along d0
+    const uint32_t dj = tj * TSJ + r, d0 = t0 * TS0 + cc * V;
     if (dj < nj && d0 < n0) *(vec_t*)(dst + dst_base + dpos + (int64_t)dj * place_j + d0) = *(const vec_t*)&tile[r][cc * V];
   }
 }
@@ -220,18 +222,27 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
   }
   // Tiled transpose when the innermost dst wheel is strided in src and another wheel is the
   // contiguous src run, both big enough to fill a tile, and the positions cover whole wheels.
+  // A contiguous src run, or a contiguous dst run, of one 16-byte chunk (e.g. an 8-element packet
+  // of bf16) also qualifies, for the 16-byte path only: its tiles are one chunk wide on that side,
+  // still coalesced on both.
   int jw = -1;
-  if (w.n >= 2 && w.stride[0][0] != 1 && w.size[0] >= 16) {
-    for (int i = 1; i < w.n; ++i)
-      if (w.stride[0][i] == 1 && w.size[i] >= 16) {
+  bool chunk_run = w.n >= 1 && w.size[0] < 16;  // a one-chunk dst run: the 16-byte path only
+  if (w.n >= 2 && w.stride[0][0] != 1 && w.size[0] >= (chunk_run ? VEC : 16) && w.size[0] % (chunk_run ? VEC : 1) == 0) {
+    for (int i = 1; i < w.n && jw < 0; ++i)
+      if (w.stride[0][i] == 1 && w.size[i] >= 16) jw = i;
+    for (int i = 1; i < w.n && jw < 0; ++i)
+      if (w.stride[0][i] == 1 && w.size[i] >= VEC && w.size[i] % VEC == 0) {
         jw = i;
-        break;
+        chunk_run = true;
       }
   }
   int64_t total = 1;
   for (int i = 0; i < w.n; ++i) total *= w.size[i];
+  // tile shape: one chunk wide on a one-chunk side (TS0 x TSJ = 4096 elements), else 64 x 64
+  const int ts0 = chunk_run && w.n >= 1 && w.size[0] < 16 ? VEC : chunk_run ? 4096 / VEC : 64;
+  const int tsj = chunk_run && w.n >= 1 && w.size[0] < 16 ? 4096 / VEC : chunk_run ? VEC : 64;
   if (jw > 0 && total == count) {
-    uint32_t tiles0 = (w.size[0] + 63) / 64, tilesj = (w.size[jw] + 63) / 64;
+    uint32_t tiles0 = (w.size[0] + ts0 - 1) / ts0, tilesj = (w.size[jw] + tsj - 1) / tsj;
     uint32_t outer = (uint32_t)(total / ((int64_t)w.size[0] * w.size[jw]));
     int64_t blocks = (int64_t)tiles0 * tilesj * outer;
     if (blocks < (1ll << 31)) {
@@ -242,14 +253,22 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
                  ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0;
       for (int i = 0; i < w.n && v16; ++i)
         if (i != jw) v16 = (w.stride[0][i] % VEC) == 0;
-      if (v16)
-        hipLaunchKernelGGL(k_relayout_tiled16<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
-                           dst_base, src_base, w, jw, outer, tiles0, tilesj);
-      else
-        hipLaunchKernelGGL(k_relayout_tiled<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
-                           dst_base, src_base, w, jw, outer, tiles0, tilesj);
-      FO_HIP(hipGetLastError());
-      return;
+      if (v16 || !chunk_run) {
+        if (v16 && ts0 == VEC)
+          hipLaunchKernelGGL((k_relayout_tiled16<T, VEC, 4096 / VEC>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
+                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+        else if (v16 && tsj == VEC)
+          hipLaunchKernelGGL((k_relayout_tiled16<T, 4096 / VEC, VEC>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
+                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+        else if (v16)
+          hipLaunchKernelGGL((k_relayout_tiled16<T, 64, 64>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
+                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+        else
+          hipLaunchKernelGGL(k_relayout_tiled<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
+                             dst_base, src_base, w, jw, outer, tiles0, tilesj);
+        FO_HIP(hipGetLastError());
+        return;
+      }
     }
   }
   constexpr int RUN = 8;

@@ -128,6 +128,17 @@ def test_transpose_chain_requires_broadcast_flag(rt):
         rt.transpose_chain(rt.alloc(4 * 20 * 12 * 4), rt.alloc(20 * 12 * 4), I32, views)
 
 
+@pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16), (I32, np.int32)], ids=["i8", "bf16", "i32"])
+@pytest.mark.parametrize("shape", [
+    (dict(R=64, C=128), "R / 8, C, R % 8", "C / 64, R, C % 64"),    # src runs of 8 (packets of 8)
+    (dict(R=48, C=200), "R / 8, C, R % 8", "C, R"),
+    (dict(R=32, C=64, X=3), "R / 16, C, R % 16", "C / 8, X, R, C % 8"),
+])
+def test_transpose_short_src_runs(rt, dt, shape):
+    sizes, a, b = shape
+    run_transpose(rt, sizes, a, b, dt[0], dt[1], allow_broadcast=True)
+
+
 @pytest.mark.parametrize("case", SEQ_TABLES, ids=[c[2] for c in SEQ_TABLES])
 def test_transpose_doc_tables(rt, case):
     sizes, mem, stream, _ = case
