@@ -182,6 +182,73 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
 // 16-byte chunk of dst positions maps to 16 contiguous, aligned src bytes. One thread moves one
 // chunk; only the outer wheels' liveness can drop it.
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int v4i_t;
+
+// Register-tiled relayout for short runs: one thread moves a V x V block (V = elements per
+// 16-byte chunk) between wheel 0 (contiguous in dst) and wheel jw (contiguous in src). It reads V
+// chunks along jw (one per wheel-0 index), transposes them in registers, and writes V chunks
+// along wheel 0 (one per jw index). Consecutive threads take consecutive wheel-0 blocks, then
+// jw blocks, so both sides move whole chunks in runs.
+template <typename T>
+__device__ __forceinline__ void transpose_block(const v4i_t (&in)[16 / sizeof(T)], v4i_t (&out)[16 / sizeof(T)]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out[m][k] = in[k][m];
+  } else {
+    // 16-bit elements: output chunk m word q = (in[2q] element m, in[2q + 1] element m); element m
+    // is the low (m even) or high (m odd) half of word m / 2. v_perm_b32 picks the two halves.
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t a = (uint32_t)in[2 * q][m >> 1], b = (uint32_t)in[2 * q + 1][m >> 1];
+        out[m][q] = (int)__builtin_amdgcn_perm(b, a, (m & 1) ? 0x07060302u : 0x05040100u);
+      }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) k_relayout_rt(T* __restrict__ dst, const T* __restrict__ src, int64_t dst_base,
+                                                     int64_t src_base, Wheels<1> w, int jw, uint32_t nb0, uint32_t nbj,
+                                                     uint32_t outer_count) {
+  constexpr int V = 16 / sizeof(T);
+  const uint32_t total = nb0 * nbj * outer_count;
+  for (uint32_t idx = blockIdx.x * 256 + threadIdx.x; idx < total; idx += gridDim.x * 256) {
+    const uint32_t b0 = idx % nb0, t = idx / nb0, bj = t % nbj, outer = t / nbj;
+    int64_t soff = 0, dpos = 0, place = 1, place_j = 0;
+    bool live = true;
+    uint32_t q = outer;
+    for (int i = 0; i < w.n; ++i) {
+      if (i == 0) {
+        place *= w.size[0];
+        continue;
+      }
+      if (i == jw) {
+        place_j = place;
+        place *= w.size[i];
+        continue;
+      }
+      const uint32_t nq = w.div[i].div(q);
+      const uint32_t d = q - nq * w.size[i];
+      q = nq;
+      live &= d < w.live[i];
+      soff += (int64_t)d * w.stride[0][i];
+      dpos += (int64_t)d * place;
+      place *= w.size[i];
+    }
+    if (!live) continue;
+    v4i_t in[V], out[V];
+    const T* sp = src + src_base + soff + (int64_t)(V * b0) * w.stride[0][0] + V * bj;
+#pragma unroll
+    for (int k = 0; k < V; ++k) in[k] = *(const v4i_t*)(sp + (int64_t)k * w.stride[0][0]);
+    transpose_block<T>(in, out);
+    T* dp = dst + dst_base + dpos + (int64_t)(V * bj) * place_j + V * b0;
+#pragma unroll
+    for (int m = 0; m < V; ++m) *(v4i_t*)(dp + (int64_t)m * place_j) = out[m];
+  }
+}
+
 template <int VEC>
 __global__ void __launch_bounds__(kBlock) k_relayout_chunks(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
                                                             int64_t dst_base_b, int64_t src_base_b, int64_t eb,
@@ -241,6 +308,22 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
   // tile shape: one chunk wide on a one-chunk side (TS0 x TSJ = 4096 elements), else 64 x 64
   const int ts0 = chunk_run && w.n >= 1 && w.size[0] < 16 ? VEC : chunk_run ? 4096 / VEC : 64;
   const int tsj = chunk_run && w.n >= 1 && w.size[0] < 16 ? 4096 / VEC : chunk_run ? VEC : 64;
+  if (jw > 0 && total == count && chunk_run && (sizeof(T) == 2 || sizeof(T) == 4)) {
+    // Short runs on one side: register-tiled V x V blocks, when every chunk is aligned.
+    bool rt = w.size[0] % VEC == 0 && w.size[jw] % VEC == 0 && w.live[0] == w.size[0] &&
+              w.live[jw] == w.size[jw] && dst_base % VEC == 0 && src_base % VEC == 0 &&
+              ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0;
+    for (int i = 0; i < w.n && rt; ++i)
+      if (i != jw) rt = (w.stride[0][i] % VEC) == 0;
+    const uint32_t nb0 = w.size[0] / VEC, nbj = w.size[jw] / VEC;
+    const uint32_t outer = (uint32_t)(total / ((int64_t)w.size[0] * w.size[jw]));
+    if (rt && (int64_t)nb0 * nbj * outer < (1ll << 31)) {
+      hipLaunchKernelGGL(k_relayout_rt<T>, dim3(grid_for((int64_t)nb0 * nbj * outer)), dim3(256), 0, s, (T*)dst,
+                         (const T*)src, dst_base, src_base, w, jw, nb0, nbj, outer);
+      FO_HIP(hipGetLastError());
+      return;
+    }
+  }
   if (jw > 0 && total == count) {
     uint32_t tiles0 = (w.size[0] + ts0 - 1) / ts0, tilesj = (w.size[jw] + tsj - 1) / tsj;
     uint32_t outer = (uint32_t)(total / ((int64_t)w.size[0] * w.size[jw]));
