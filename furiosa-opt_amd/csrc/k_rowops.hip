@@ -4,13 +4,14 @@
 // slice reduce; fp_div by the column count; clip Add eps; Sqrt; (x * g) / r in f32; cast to bf16 at
 // commit. The softmax re-fetches the committed bf16 values: max, exp(y - max), sum, divide, cast.
 //
-// Layout: one wave64 per row; lane l holds the 16-byte chunks c*64 + l (8 bf16 each), so every wave
-// load or store is 1 KiB contiguous. The row stays packed as bf16 in registers (x, then y); the
-// waves are persistent (a grid-stride loop over rows) and keep the next two rows' x in flight while
-// the current one is computed, so the load stream never drains. exp(y - max) is evaluated twice
-// (for the sum, then for the output) rather than held, which frees the registers the second
-// prefetched row needs at two waves per SIMD. The gain is staged once per block in
-// LDS as f32.
+// Layout: lane l of a wave holds the 16-byte chunks c*64 + l of its part of the row (8 bf16 each), so
+// every wave load or store is 1 KiB contiguous. The row stays packed as bf16 in registers (x, then
+// y); exp(y - max) is held in f32 registers from the sum to the output, so each element is read,
+// exponentiated and written once. The gain is staged once per block in LDS as f32. Two kernels:
+//   * k_rmsnorm_softmax_dma (512 to 4096 columns): one wave per row, persistent waves, the next row
+//     fetched into LDS by DMA while the current one is computed;
+//   * k_rmsnorm_softmax_split (8192 columns): a row spread over four waves, whose reductions combine
+//     through LDS, so that a wave's registers still hold its share of the row and its exponentials.
 //
 // Numerics. This file is compiled with f32 denormals flushed (inputs and results, sign kept),
 // which is the reference's own numeric model: its bf16 widen and narrow flush every subnormal to a
@@ -36,15 +37,48 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_t;
 
+// Wave64 reductions to a uniform value: four DPP steps combine the 16 lanes of each row (swap
+// neighbours, swap pairs, mirror within 8, mirror within 16; after each step the lanes of a group
+// hold equal values), then the four row results are read out with v_readlane. DPP moves data
+// between lanes inside the VALU, without the LDS round trip of ds_bpermute. All 64 lanes must be
+// active.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xb1;         // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4e;         // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppMirror = 0x140;      // row_mirror
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
-  return v;
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-  return v;
+  v = fmaxf(v, dpp<kDppXor1>(v));
+  v = fmaxf(v, dpp<kDppXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+
+// A pointer the compiler cannot prove wave-uniform but is by construction (so a buffer descriptor
+// built from it stays in SGPRs).
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  uint64_t v = (uint64_t)p;
+  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(((uint64_t)hi << 32) | lo);
+}
+
+// a.lo * b.lo + a.hi * b.hi + c on packed bf16 pairs (v_dot2_f32_bf16).
+__device__ __forceinline__ float dot2_bf16(int a, int b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
 // Plain widen of the low / high bf16 of a packed word (subnormals read as zero in flush mode).
@@ -86,64 +120,86 @@ __device__ void row_exact(uint16_t* __restrict__ orow, const uint16_t* __restric
   }
 }
 
-// NCH 16-byte chunks per lane: cols = NCH * 512.
+// Rows of up to 4096 columns: one wave per row, persistent waves, the next row fetched into LDS
+// by DMA (buffer_load ... lds) while the current one is computed. A register prefetch would not
+// stay in flight: with this row's stores also outstanding the compiler waits for every access
+// before touching the prefetched registers. Here the only wait on vector memory is explicit and
+// sits just before the row's stores, when the DMA issued at the start of the row and the previous
+// row's stores are a whole row's compute old. exp(y - max) is kept in registers from the sum to
+// the output, so each element is exponentiated once.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+#endif
+}
+constexpr int waitcnt_vm0 = (0 & 15) | (7 << 4) | (15 << 8);  // vmcnt(0); lgkmcnt, expcnt left alone
+constexpr int waitcnt_lgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);  // lgkmcnt(0); vmcnt left alone
+
+constexpr int kDmaWaves = 8;  // waves per block (they share the staged gain)
 template <int NCH>
-__global__ void __launch_bounds__(256, 2) k_rmsnorm_softmax(uint16_t* __restrict__ out, const uint16_t* __restrict__ x,
-                                                         const uint16_t* __restrict__ gain, int64_t rows, float cols_f,
-                                                         float eps) {
+__global__ void __launch_bounds__(64 * kDmaWaves) k_rmsnorm_softmax_dma(uint16_t* __restrict__ out, const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ gain, int64_t rows,
+                                                             float cols_f, float eps) {
   constexpr int cols = NCH * 512;
   const int lane = threadIdx.x & 63;
-  const int64_t wave = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t nwaves = (int64_t)gridDim.x * 4;
-  // The gain row is shared by every row: widen it once per block into LDS (reference widen rule),
-  // and note whether it holds a non-finite value.
+  const int wv = threadIdx.x >> 6;
+  const int64_t wave = (int64_t)blockIdx.x * kDmaWaves + wv;
+  const int64_t nwaves = (int64_t)gridDim.x * kDmaWaves;
   __shared__ __attribute__((aligned(16))) float sg[cols];
-  __shared__ int g_bad;
-  if (threadIdx.x == 0) g_bad = 0;
+  __shared__ __attribute__((aligned(16))) i32x4_t sx[kDmaWaves][NCH * 64];  // the wave's next row: chunk c at [c * 64 + lane]
+  // Chunk c of a row (1 KiB) lands at sx[wv][c * 64]: lane l's 16 bytes at + 16 l, where lane l reads
+  // them back (conflict-free b128 reads).
+  auto fetch = [&](int64_t r) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(uniform_ptr(x + r * cols)), (short)0, cols * 2, 0x00020000);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) dma16(rs, &sx[wv][c * 64], (uint32_t)(c * 1024 + lane * 16));
+  };
+  int64_t row = __builtin_amdgcn_readfirstlane((int)wave);
+  if (row < rows) fetch(row);  // overlaps the gain staging below
+  // The gain row is shared by every row: widen it once per block into LDS (reference widen rule),
+  // and note whether it holds a non-finite value or a magnitude of 2^120 or more (below that no y
+  // can overflow once the row's sum of squares is finite: |x_i| <= sqrt(ss) and r >= sqrt(ss / cols)
+  // give |y_i| <= sqrt(cols) * max|g| < 2^7 * 2^120).
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) sg[i] = bf16_to_f32(gain[i]);
   __syncthreads();
-  // A gain at or above 2^120 in magnitude also takes the exact path: below it no y can overflow
-  // once the row's sum of squares is finite, because |x_i| <= sqrt(ss) and r >= sqrt(ss / cols)
-  // give |y_i| <= sqrt(cols) * max|g| < 2^7 * 2^120.
-  int bad_local = 0;
-  for (int i = threadIdx.x; i < cols; i += blockDim.x) {
-    float gv = bf16_to_f32(gain[i]);
-    sg[i] = gv;
-    bad_local |= !(__builtin_fabsf(gv) < 0x1p120f);
+  int bad_local = 0;  // each wave scans the staged row itself (no block-wide flag in LDS)
+  for (int i = lane * 4; i < cols; i += 256) {
+    f32x4_t gv = *(const f32x4_t*)(sg + i);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) bad_local |= !(__builtin_fabsf(gv[k]) < 0x1p120f);
   }
-  if (bad_local) g_bad = 1;
-  __syncthreads();
-  const bool gain_bad = g_bad != 0;
-  int64_t row = wave;
+  const bool gain_bad = __any(bad_local);
   if (row >= rows) return;
-
-  i32x4_t cur[NCH], nxt[NCH], nx2[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) cur[c] = __builtin_nontemporal_load((const i32x4_t*)(x + row * cols + (c * 64 + lane) * 8));
-  if (row + nwaves < rows) {
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      nxt[c] = __builtin_nontemporal_load((const i32x4_t*)(x + (row + nwaves) * cols + (c * 64 + lane) * 8));
-  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm0);
 
   for (; row < rows; row += nwaves) {
-    const int64_t nrow = row + nwaves, n2row = row + 2 * nwaves;
-    if (n2row < rows) {
+    i32x4_t v[NCH];
+    __asm__ volatile("" ::: "memory");
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
-        nx2[c] = __builtin_nontemporal_load((const i32x4_t*)(x + n2row * cols + (c * 64 + lane) * 8));
+    for (int c = 0; c < NCH; ++c) v[c] = sx[wv][c * 64 + lane];
+    __builtin_amdgcn_s_waitcnt(waitcnt_lgkm0);  // the row is in registers before its buffer is refilled
+    __asm__ volatile("" ::: "memory");
+    if (row + nwaves < rows) fetch(row + nwaves);
+    // Sum of squares by v_dot2_f32_bf16 on the packed pairs (two chains). The reference rounds each
+    // square and then each partial sum; the squares of bf16 values are exact in f32, and its
+    // reduction order is not this one anyway, so the sums agree to f32 rounding.
+    float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      ss0 = dot2_bf16(v[c][0], v[c][0], ss0);
+      ss1 = dot2_bf16(v[c][1], v[c][1], ss1);
+      ss0 = dot2_bf16(v[c][2], v[c][2], ss0);
+      ss1 = dot2_bf16(v[c][3], v[c][3], ss1);
     }
-    // sum of squares: each square rounded, then added (MulF with the stash, then the Add reduce)
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint32_t w = (uint32_t)cur[c][e];
-        float a = lo_raw(w), b = hi_raw(w);
-        ss += a * a;
-        ss += b * b;
-      }
-    ss = wave_sum(ss);
+    const float ss = wave_sum(ss0 + ss1);
+    uint16_t* orow = out + row * cols;
+    if (!__builtin_isfinite(ss) || gain_bad) {
+      row_exact(orow, x + row * cols, gain, cols, eps, lane);
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm0);
+      continue;
+    }
     const float ms = __fadd_rn(__fdiv_rn(ss, cols_f), eps);  // fp_div, then clip Add eps
     const float r = sqrt_rn(ms);                              // FpUnaryOp::Sqrt
     const float rinv = __fdiv_rn(1.0f, r);
@@ -155,55 +211,198 @@ __global__ void __launch_bounds__(256, 2) k_rmsnorm_softmax(uint16_t* __restrict
       f32x4_t g1 = *(const f32x4_t*)(sg + (c * 64 + lane) * 8 + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        uint32_t w = (uint32_t)cur[c][e];
+        uint32_t u = (uint32_t)v[c][e];
         float glo = e < 2 ? g0[2 * e] : g1[2 * e - 4];
         float ghi = e < 2 ? g0[2 * e + 1] : g1[2 * e - 3];
-        float ylo = div_cr(lo_raw(w) * glo, r, rinv);
-        float yhi = div_cr(hi_raw(w) * ghi, r, rinv);
+        float ylo = div_cr(lo_raw(u) * glo, r, rinv);
+        float yhi = div_cr(hi_raw(u) * ghi, r, rinv);
         mx = fmaxf(mx, fmaxf(ylo, yhi));
-        cur[c][e] = (int)pack_bf16(ylo, yhi);
+        v[c][e] = (int)pack_bf16(ylo, yhi);
       }
     }
     mx = wave_max(mx);
-    uint16_t* orow = out + row * cols;
-    if (!__builtin_isfinite(ss) || gain_bad) {
-      row_exact(orow, x + row * cols, gain, cols, eps, lane);
-    } else {
-      mx = bits_f32(pack_bf16(mx, mx) << 16);  // the max of the committed bf16 values
-      // softmax: e = exp(y - max) kept in f32, s = sum(e), out = bf16(e / s)
-      const float L2E = 1.4426950408889634f;
-      const float mxl = mx * L2E;
-      float s = 0.f;
+    mx = bits_f32(pack_bf16(mx, mx) << 16);  // the max of the committed bf16 values
+    // softmax: e = exp(y - max) kept in f32, s = sum(e), out = bf16(e / s)
+    const float L2E = 1.4426950408889634f;
+    const float mxl = mx * L2E;
+    float ex[NCH][8];
+    float s = 0.f;
 #pragma unroll
-      for (int c = 0; c < NCH; ++c)
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint32_t w = (uint32_t)cur[c][e];
-          s += __builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(w), L2E, -mxl));
-          s += __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(w), L2E, -mxl));
-        }
-      s = wave_sum(s);
-      const float sinv = __builtin_amdgcn_rcpf(s);
-#pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        i32x4_t o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          uint32_t w = (uint32_t)cur[c][e];
-          o[e] = (int)pack_bf16(__builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(w), L2E, -mxl)) * sinv,
-                                __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(w), L2E, -mxl)) * sinv);
-        }
-        __builtin_nontemporal_store(o, (i32x4_t*)(orow + (c * 64 + lane) * 8));
+      for (int e = 0; e < 4; ++e) {
+        uint32_t u = (uint32_t)v[c][e];
+        ex[c][2 * e] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(u), L2E, -mxl));
+        ex[c][2 * e + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(u), L2E, -mxl));
+        s += ex[c][2 * e];
+        s += ex[c][2 * e + 1];
       }
-    }
-    if (nrow < rows) {
+    s = wave_sum(s);
+    const float sinv = __builtin_amdgcn_rcpf(s);
+    // The next row's DMA and the previous row's stores are complete before these stores go out, so
+    // no vector memory access is pending at the next row's LDS reads.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm0);
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        cur[c] = nxt[c];
-        nxt[c] = nx2[c];
-      }
+    for (int c = 0; c < NCH; ++c) {
+      i32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (int)pack_bf16(ex[c][2 * e] * sinv, ex[c][2 * e + 1] * sinv);
+      __builtin_nontemporal_store(o, (i32x4_t*)(orow + (c * 64 + lane) * 8));
     }
   }
+}
+
+template <int NCH>
+void rs_dma_launch(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* g, int64_t rows, float eps) {
+  static int64_t resident_blocks = [] {
+    int dev = 0, per_cu = 1, cus = 1;
+    (void)hipGetDevice(&dev);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_rmsnorm_softmax_dma<NCH>, 64 * kDmaWaves, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    return (int64_t)per_cu * cus;
+  }();
+  int64_t blocks = (rows + kDmaWaves - 1) / kDmaWaves;
+  if (blocks > resident_blocks) blocks = resident_blocks;
+  hipLaunchKernelGGL(k_rmsnorm_softmax_dma<NCH>, dim3((unsigned)blocks), dim3(64 * kDmaWaves), 0, s, out, x, g, rows,
+                     (float)(NCH * 512), eps);
+}
+
+// Split rows (8192 columns): a block of kSplit waves normalises one row at a time, each wave holding
+// CPW 16-byte chunks per lane (cols = kSplit * CPW * 512); the three row reductions combine the
+// waves' partials through LDS. Blocks are persistent and loop over rows; latency is hidden by the
+// other blocks on the CU (four waves per SIMD at CPW = 4) rather than by a prefetch.
+constexpr int kSplit = 4;
+template <int CPW>
+__global__ void __launch_bounds__(64 * kSplit) k_rmsnorm_softmax_split(uint16_t* __restrict__ out,
+                                                                      const uint16_t* __restrict__ x,
+                                                                      const uint16_t* __restrict__ gain, int64_t rows,
+                                                                      float cols_f, float eps) {
+  constexpr int cols = kSplit * CPW * 512;
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  __shared__ __attribute__((aligned(16))) float sg[cols];
+  __shared__ float red[3][kSplit];
+  __shared__ int g_bad;
+  if (threadIdx.x == 0) g_bad = 0;
+  __syncthreads();
+  // Gain staged once per block, widened by the reference rule; at or above 2^120 in magnitude it
+  // takes the exact path, as in k_rmsnorm_softmax.
+  int bad_local = 0;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+    float gv = bf16_to_f32(gain[i]);
+    sg[i] = gv;
+    bad_local |= !(__builtin_fabsf(gv) < 0x1p120f);
+  }
+  if (bad_local) g_bad = 1;
+  __syncthreads();
+  const bool gain_bad = g_bad != 0;
+  // The block's combine of the per-wave partials, in a fixed order so every wave gets the same
+  // value. A slot is rewritten only after the next barrier, which every reader has passed after
+  // its read.
+  auto block_sum = [&](int k, float v) {
+    if (lane == 0) red[k][w] = v;
+    __syncthreads();
+    float s = red[k][0];
+#pragma unroll
+    for (int i = 1; i < kSplit; ++i) s += red[k][i];
+    return s;
+  };
+  auto block_max = [&](int k, float v) {
+    if (lane == 0) red[k][w] = v;
+    __syncthreads();
+    float m = red[k][0];
+#pragma unroll
+    for (int i = 1; i < kSplit; ++i) m = fmaxf(m, red[k][i]);
+    return m;
+  };
+  const int e0 = ((w * CPW) * 64 + lane) * 8;  // first element of this lane's chunk 0; chunk c adds c * 512
+
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const uint16_t* xr = x + row * cols;
+    i32x4_t v[CPW];
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) v[c] = __builtin_nontemporal_load((const i32x4_t*)(xr + e0 + c * 512));
+    // Sum of squares by v_dot2_f32_bf16 on the packed pairs. The reference rounds each square and
+    // then each partial sum; the squares of bf16 values are exact in f32, and its reduction order
+    // is not this one anyway, so the sums agree to f32 rounding.
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = dot2_bf16(v[c][e], v[c][e], ss);
+    ss = block_sum(0, wave_sum(ss));
+    uint16_t* orow = out + row * cols;
+    if (!__builtin_isfinite(ss) || gain_bad) {  // block-uniform
+      if (w == 0) row_exact(orow, xr, gain, cols, eps, lane);
+      __syncthreads();  // every wave has read red[0] before the next row rewrites it
+      continue;
+    }
+    const float ms = __fadd_rn(__fdiv_rn(ss, cols_f), eps);  // fp_div, then clip Add eps
+    const float r = sqrt_rn(ms);                              // FpUnaryOp::Sqrt
+    const float rinv = __fdiv_rn(1.0f, r);
+    // y = bf16((x * g) / r), kept packed; row max on the f32 values
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      f32x4_t g0 = *(const f32x4_t*)(sg + e0 + c * 512);
+      f32x4_t g1 = *(const f32x4_t*)(sg + e0 + c * 512 + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t u = (uint32_t)v[c][e];
+        float glo = e < 2 ? g0[2 * e] : g1[2 * e - 4];
+        float ghi = e < 2 ? g0[2 * e + 1] : g1[2 * e - 3];
+        float ylo = div_cr(lo_raw(u) * glo, r, rinv);
+        float yhi = div_cr(hi_raw(u) * ghi, r, rinv);
+        mx = fmaxf(mx, fmaxf(ylo, yhi));
+        v[c][e] = (int)pack_bf16(ylo, yhi);
+      }
+    }
+    mx = block_max(1, wave_max(mx));
+    mx = bits_f32(pack_bf16(mx, mx) << 16);  // the max of the committed bf16 values
+    // softmax: e = exp(y - max) kept in f32, s = sum(e), out = bf16(e / s)
+    const float L2E = 1.4426950408889634f;
+    const float mxl = mx * L2E;
+    float ex[CPW][8];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPW; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t u = (uint32_t)v[c][e];
+        ex[c][2 * e] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo_raw(u), L2E, -mxl));
+        ex[c][2 * e + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi_raw(u), L2E, -mxl));
+        s += ex[c][2 * e];
+        s += ex[c][2 * e + 1];
+      }
+    s = block_sum(2, wave_sum(s));
+    const float sinv = __builtin_amdgcn_rcpf(s);
+#pragma unroll
+    for (int c = 0; c < CPW; ++c) {
+      i32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (int)pack_bf16(ex[c][2 * e] * sinv, ex[c][2 * e + 1] * sinv);
+      __builtin_nontemporal_store(o, (i32x4_t*)(orow + e0 + c * 512));
+    }
+  }
+}
+
+template <int CPW>
+void rs_split_launch(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* g, int64_t rows, float eps) {
+  static int64_t resident_blocks = [] {
+    int dev = 0, per_cu = 1, cus = 1;
+    (void)hipGetDevice(&dev);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_rmsnorm_softmax_split<CPW>, 64 * kSplit, 0) !=
+            hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    return (int64_t)per_cu * cus;
+  }();
+  int64_t blocks = rows < resident_blocks ? rows : resident_blocks;
+  hipLaunchKernelGGL(k_rmsnorm_softmax_split<CPW>, dim3((unsigned)blocks), dim3(64 * kSplit), 0, s, out, x, g, rows,
+                     (float)(kSplit * CPW * 512), eps);
 }
 
 // Any column count: the exact per-element path, one wave per row.
@@ -216,25 +415,6 @@ __global__ void __launch_bounds__(256) k_rmsnorm_softmax_any(uint16_t* __restric
   row_exact(out + row * cols, x + row * cols, gain, (int)cols, eps, lane);
 }
 
-template <int NCH>
-void rs_launch(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* g, int64_t rows, float eps) {
-  // Persistent waves: exactly as many blocks as can be resident at once (occupancy x CUs), so every
-  // wave starts immediately and loops over rows; never more waves than rows.
-  static int64_t resident_blocks = [] {
-    int dev = 0, per_cu = 1, cus = 1;
-    (void)hipGetDevice(&dev);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_rmsnorm_softmax<NCH>, 256, 0) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-    return (int64_t)per_cu * cus;
-  }();
-  int64_t blocks = (rows + 3) / 4;
-  if (blocks > resident_blocks) blocks = resident_blocks;
-  hipLaunchKernelGGL(k_rmsnorm_softmax<NCH>, dim3((unsigned)blocks), dim3(256), 0, s, out, x, g, rows,
-                     (float)(NCH * 512), eps);
-}
-
 }  // namespace
 
 void launch_rmsnorm_softmax(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* gain, int64_t rows,
@@ -244,11 +424,11 @@ void launch_rmsnorm_softmax(hipStream_t s, uint16_t* out, const uint16_t* x, con
   bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)out % 16 == 0) && ((uintptr_t)gain % 16 == 0);
   if (aligned && cols % 512 == 0 && cols <= 8192) {
     switch (cols / 512) {
-      case 1: rs_launch<1>(s, out, x, gain, rows, eps); break;
-      case 2: rs_launch<2>(s, out, x, gain, rows, eps); break;
-      case 4: rs_launch<4>(s, out, x, gain, rows, eps); break;
-      case 8: rs_launch<8>(s, out, x, gain, rows, eps); break;
-      case 16: rs_launch<16>(s, out, x, gain, rows, eps); break;
+      case 1: rs_dma_launch<1>(s, out, x, gain, rows, eps); break;
+      case 2: rs_dma_launch<2>(s, out, x, gain, rows, eps); break;
+      case 4: rs_dma_launch<4>(s, out, x, gain, rows, eps); break;
+      case 8: rs_dma_launch<8>(s, out, x, gain, rows, eps); break;
+      case 16: rs_split_launch<4>(s, out, x, gain, rows, eps); break;
       default:
         hipLaunchKernelGGL(k_rmsnorm_softmax_any, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, out, x, gain, rows,
                            cols, eps);

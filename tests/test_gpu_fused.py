@@ -77,6 +77,32 @@ def test_rmsnorm_softmax_small(rt, shape):
     close_chain(emu.bf16_to_f32(out.read(np.uint16)), emu.bf16_to_f32(want), frac_beyond=1e-4)
 
 
+@pytest.mark.parametrize("cols", [1024, 2048, 4096, 8192])
+@pytest.mark.parametrize("gain_case", ["finite", "inf", "huge"])
+def test_rmsnorm_softmax_nonfinite(rt, cols, gain_case):
+    """Rows holding +-inf, NaN or a value whose square overflows take the per-element reference path
+    (a NaN row stays NaN, an overflowed sum of squares gives the uniform row); so does every row when
+    the gain holds inf or a magnitude of 2^121. Rows next to them keep the fast path."""
+    rows = 8
+    rng = np.random.default_rng(33)
+    x = bf16(rng, rows * cols).reshape(rows, cols)
+    g = emu.f32_to_bf16(rng.uniform(0.1, 1.0, cols).astype(np.float32))
+    special = emu.f32_to_bf16(np.array([np.inf, np.nan, 1e20, -np.inf, 2.0 ** 121], np.float32))
+    x[1, 5], x[2, 7], x[3, 0], x[4, 9] = special[:4]
+    if gain_case == "inf":
+        g[3] = special[0]
+    elif gain_case == "huge":
+        g[3] = special[4]
+    want = emu.bf16_to_f32(emu.rmsnorm_softmax(x.ravel(), g, rows, cols, 1e-6)).reshape(rows, cols)
+    out = rt.alloc(rows * cols * 2)
+    rt.rmsnorm_softmax(out, rt.upload(x.ravel()), rt.upload(g), rows, cols, 1e-6)
+    got = emu.bf16_to_f32(out.read(np.uint16)).reshape(rows, cols)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.isnan(want[[1, 2, 4]]).all() and fin[[0, 3, 5, 6, 7]].any()
+    close_chain(got[fin], want[fin], frac_beyond=1e-4)
+
+
 def test_rmsnorm_softmax_config(rt):
     rows, cols = 8192, 4096  # BASELINE.json configs[2]
     rng = np.random.default_rng(31)
