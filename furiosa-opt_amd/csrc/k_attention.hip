@@ -18,11 +18,13 @@
 // through LDS. V is stored transposed in LDS with the keys of each 16-key group permuted so that
 // every A fragment of the PV product is one 16-byte read.
 //
-// Pipeline. K and V tiles are double-buffered in LDS with K one 64-key block ahead of V: while
-// the softmax of block j runs on the VALU, the MFMAs of S(j+1) are independent of it and issue
-// alongside; then block j's PV. Global loads for the next blocks are issued into registers
-// before a step and written to LDS after it, so one barrier per block suffices. Blocks below
-// the last two are fully visible to every query of the workgroup and run without mask code.
+// Pipeline. K and V tiles are double-buffered in LDS. A step computes S of its block, the
+// softmax, then the PV product; the two waves that share a SIMD overlap one's MFMAs with the
+// other's softmax. (Computing the next block's S during this block's softmax, in the same wave,
+// measured 7% slower: the second S tile's 32 registers leave none for LDS reads in flight.)
+// Global loads for the next block are issued into registers before a step and written to LDS
+// after it, so one barrier per block suffices. Blocks below the last two are fully visible to
+// every query of the workgroup and run without mask code.
 #include <hip/hip_runtime.h>
 
 #include "runtime.hpp"
@@ -41,6 +43,7 @@ constexpr int kBM = 128;  // queries per workgroup (4 waves x 32)
 constexpr int kBN = 64;   // keys per block
 constexpr float kEps = 6.25e-8f;  // attention.rs:13
 constexpr float kL2E = 1.4426950408889634f;
+constexpr float kTau = 5.545177444479562f;  // 8 ln 2: p = exp(s - m_run) <= 2^8 between rescales
 
 __device__ __forceinline__ f32x16_t mma(const i32x4_t& a, const i32x4_t& b, const f32x16_t& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c, 0,
@@ -89,39 +92,52 @@ __device__ __forceinline__ void qk(const uint8_t* __restrict__ sK, const i32x4_t
   }
 }
 
-// One pipelined step: S of the next block (from sKn) is computed while the softmax of the
-// current block's S (sc) runs, then the current block's PV product; sc becomes the next S.
+// One step: S of the block (K from sK), its softmax, then its PV product (V^T from sVt).
 template <int D, bool MASK>
-__device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const uint8_t* __restrict__ sVt,
+__device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const uint8_t* __restrict__ sVt,
                                           const i32x4_t (&qf)[AttnCfg<D>::KS], f32x16_t (&o)[AttnCfg<D>::DT],
-                                          f32x16_t (&sc)[2], float& m_run, float& l_part, int kv0, int lim,
-                                          float inv_sd, int g, int col) {
+                                          float& m_run, float& l_part,
+                                          int kv0, int lim, float inv_sd, int g, int col) {
   using C = AttnCfg<D>;
-  f32x16_t sn[2];
-  qk<D>(sKn, qf, sn, g, col);
-  // Block max on the raw sums (scale and bf16 rounding are monotonic, so max commutes with
-  // them), then logits: scale, round to bf16 (the reference's qk_scaled narrow).
+  f32x16_t sc[2];
+  qk<D>(sK, qf, sc, g, col);
+  // Scaled sums first, then the block max over them (the max of products is the product of the
+  // max, and bf16 rounding is monotonic, so the max commutes with both). Taking it on product
+  // results also spares the quieting of each operand that a max of raw MFMA outputs needs.
   float bmax = -INFINITY;
+  float xs[2][16];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) xs[kt][r] = sc[kt][r] * inv_sd;
     if (MASK) {
       // key kv0 + kt*32 + 8(r/4) + 4g + r%4 is visible iff it is <= lim: one compare against a
       // per-lane threshold with the register's constant key offset.
       const int thr = lim - kv0 - kt * 32 - 4 * g;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sc[kt][r] = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : sc[kt][r];
+      for (int r = 0; r < 16; ++r) xs[kt][r] = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : xs[kt][r];
     }
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(sc[kt][r], sc[kt][r + 1]));
+    for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(xs[kt][r], xs[kt][r + 1]));
   }
   bmax = __builtin_fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-  bmax = __builtin_bit_cast(float, pack_bf16(bmax * inv_sd, 0.f) << 16);
-  // Online softmax step. Every query of a processed block sees key 0 of the first block, so
-  // m_new is finite from the first block on; alpha is 0 there (m_run = -inf).
-  const float m_new = __builtin_fmaxf(m_run, bmax);
-  const float ms = m_new * kL2E;
-  const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kL2E, -ms));
-  m_run = m_new;
+  bmax = __builtin_bit_cast(float, pack_bf16(bmax, 0.f) << 16);
+  // Online softmax step with a lazy reference max: O and the sum are rescaled only when some
+  // lane's block max exceeds its reference max by more than kTau, so p = exp(s - m_run) stays
+  // <= e^kTau = 256 and most blocks skip the rescale of the 64 O registers. The ratio O / sum
+  // does not depend on the reference (every p of a row shares it). Every query of a processed
+  // block sees key 0 of the first block, so the first block always rescales (alpha = 0 there,
+  // m_run = -inf) and m_run is finite from then on.
+  if (bmax > m_run + kTau) {  // per lane: skipped as a whole when no lane of the wave needs it
+    const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kL2E, -bmax * kL2E));
+    m_run = bmax;
+    l_part *= alpha;
+#pragma unroll
+    for (int t = 0; t < C::DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+  }
+  const float ms = m_run * kL2E;
   // p = exp(x - m) as f32 for the sum, bf16 pairs for the PV operand. Chunk c = (kt = c/2,
   // h = c%2) holds sc[kt][8h .. 8h+7].
   float psum = 0.f;
@@ -133,18 +149,14 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 8 * h + 2 * e;
-        uint32_t w = pack_bf16(sc[kt][r] * inv_sd, sc[kt][r + 1] * inv_sd);
+        uint32_t w = pack_bf16(xs[kt][r], xs[kt][r + 1]);
         float x0 = __builtin_bit_cast(float, w << 16), x1 = __builtin_bit_cast(float, w & 0xffff0000u);
         float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, kL2E, -ms));
         float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, kL2E, -ms));
         psum += p0 + p1;
         pf[kt * 2 + h][e] = (int)pack_bf16(p0, p1);
       }
-  l_part = l_part * alpha + psum;
-#pragma unroll
-  for (int t = 0; t < C::DT; ++t)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
+  l_part += psum;
   // O^T += V^T P^T. Chunk c covers keys base = 32*(c/2) + 16*(c%2); lane group g binds k slots to
   // keys {base + 4g + 0..3, base + 8 + 4g + 0..3}, stored adjacently at base + 8g.
 #pragma unroll
@@ -156,8 +168,6 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sKn, const
       o[t] = mma(vf, pf[c], o[t]);
     }
   }
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt) sc[kt] = sn[kt];
 }
 
 template <int D>
@@ -243,7 +253,7 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   auto sVt_of = [&](int buf) { return (const uint8_t*)(lds + buf * C::STAGE + C::KBYTES); };
 
   // Prologue: Q fragments (B operand of S^T: lane holds query myq, d in [16*ks + 8*g, +8)), K(0)
-  // and V(0) are requested together; K(1) is in flight while S(0) is computed.
+  // and V(0) are requested together.
   i32x4_t qf[C::KS];
   const uint32_t qoff = (uint32_t)(myq * D + g * 8) * 2;
 #pragma unroll
@@ -252,7 +262,6 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   load_v(0);
   store_k(0);
   store_v(0);
-  load_k(kBN);
 
   f32x16_t o[C::DT];
 #pragma unroll
@@ -261,42 +270,33 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
   float m_run = -INFINITY, l_part = 0.f;
 
-  // Buffers: K(j) and V(j) live in buffer j % 2. Step j reads K(j+1) and V(j), then refills K
-  // buffer j % 2 with K(j+2) (K(j) was consumed by step j-1) and V buffer (j+1) % 2 with V(j+1).
-  // Loads past the head's end read zeros, so every step loads and stores unconditionally.
+  // Buffers: K(j) and V(j) live in buffer j % 2. Step j reads them, and after it writes K(j+1)
+  // and V(j+1) (loaded during the step) into buffer (j+1) % 2, last read by step j-1 before the
+  // previous barrier. Loads past the head's end read zeros, so every step loads and stores
+  // unconditionally.
   const int kv_end = causal ? min(seq, q0 + kBM) : seq;
   const int nblk = (kv_end + kBN - 1) / kBN;
-  __syncthreads();
-  f32x16_t sc[2];
-  qk<D>(sK_of(0), qf, sc, g, col);
-  store_k(1);
-  __syncthreads();  // K(1) visible, and every wave is done reading K buffer 0
   const int nmain = nblk > 2 ? nblk - 2 : 0;
+  __syncthreads();
   int j = 0;
   for (; j < nmain; ++j) {
     const int kv0 = j * kBN;
-    load_k(kv0 + 2 * kBN);
+    load_k(kv0 + kBN);
     load_v(kv0 + kBN);
-    // Keep the loads here: left to itself the scheduler sinks them next to their LDS stores at the
-    // end of the step (to save registers), exposing the whole global latency every step.
     __builtin_amdgcn_sched_barrier(0);
-    attn_step<D, false>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
-                        g, col);
-    store_k(j & 1);
+    attn_step<D, false>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
+    store_k((j + 1) & 1);
     store_v((j + 1) & 1);
     __syncthreads();
   }
-  // The last two blocks hold the causal diagonal and the sequence tail: masked, and skipped by
-  // waves whose queries all precede them.
   for (; j < nblk; ++j) {
     const int kv0 = j * kBN;
-    load_k(kv0 + 2 * kBN);
+    load_k(kv0 + kBN);
     load_v(kv0 + kBN);
     __builtin_amdgcn_sched_barrier(0);
     if (!(causal && kv0 > q0w + 31))  // wave-uniform
-      attn_step<D, true>(sK_of((j + 1) & 1), sVt_of(j & 1), qf, o, sc, m_run, l_part, kv0, lim, inv_sd,
-                         g, col);
-    store_k(j & 1);
+      attn_step<D, true>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
+    store_k((j + 1) & 1);
     store_v((j + 1) & 1);
     __syncthreads();
   }
