@@ -273,8 +273,10 @@ def cpu_baseline_gemm(target_s: float = 12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # Defaults long enough for the steady state: over the first tens of back-to-back launches the
+    # GEMM's per-launch time still falls (135 us at 20 launches, 127 at 200, 123 at 1000).
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--only", default="")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
