@@ -143,8 +143,7 @@ void* scratch(fo_runtime* rt, uint64_t bytes) {
 }
 
 // The runtime's device-visible error word (pinned host memory, written by kernels only when an
-// op's data is invalid). Returns its device address; `take_error` reads and clears it after the
-// stream has drained.
+// op's data is invalid). Returns its device address.
 int32_t* error_word(fo_runtime* rt) {
   if (!rt->err_host) {
     void* h = nullptr;
@@ -157,11 +156,18 @@ int32_t* error_word(fo_runtime* rt) {
   }
   return rt->err_dev;
 }
-int32_t take_error(fo_runtime* rt) {
-  FO_HIP(hipStreamSynchronize(rt->stream));
-  int32_t e = __atomic_load_n(rt->err_host, __ATOMIC_ACQUIRE);
-  if (e) __atomic_store_n(rt->err_host, 0, __ATOMIC_RELEASE);
-  return e;
+// Index errors of gather / scatter are found on the device. The op itself returns as soon as it is
+// enqueued, like every other op; the next call that waits for the stream (fo_runtime_synchronize,
+// fo_read) reports the error and clears the word. Call after the stream has drained.
+void raise_device_errors(fo_runtime* rt) {
+  if (!rt->err_ops) return;
+  const uint32_t ops = rt->err_ops;
+  rt->err_ops = 0;
+  if (__atomic_load_n(rt->err_host, __ATOMIC_ACQUIRE) == 0) return;
+  __atomic_store_n(rt->err_host, 0, __ATOMIC_RELEASE);
+  throw InvalidArg(std::string(ops == 1 ? "gather" : ops == 2 ? "scatter" : "gather or scatter") +
+                   ": an index is negative or past the indexed axis (in an op issued since the last "
+                   "synchronization; the valid indices were applied)");
 }
 
 // Shared set-up of scatter / gather: the stream wheels of one side, all digits live.
@@ -314,6 +320,7 @@ int32_t fo_runtime_synchronize(fo_runtime* rt) {
     check_rt(rt);
     FO_HIP(hipStreamSynchronize(rt->stream));
     flush_trace(rt);
+    raise_device_errors(rt);
   });
 }
 
@@ -413,6 +420,7 @@ int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes
     TraceScope trace_span(rt, "read");
     FO_HIP(hipMemcpyAsync(host, src->ptr, bytes, hipMemcpyDeviceToHost, rt->stream));
     FO_HIP(hipStreamSynchronize(rt->stream));
+    raise_device_errors(rt);
   });
 }
 
@@ -771,7 +779,7 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     const int mem[1] = {0};
     launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,
                    to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), win, flag);
-    require(take_error(rt) == 0, "scatter: an index is negative or past the scatter axis");
+    rt->err_ops |= 2;
   });
 }
 
@@ -808,7 +816,7 @@ int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo
     const int mem[1] = {0};
     launch_gather(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, slots, axis_size, (int32_t)div,
                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), flag);
-    require(take_error(rt) == 0, "gather: an index is negative or past the gathered axis");
+    rt->err_ops |= 1;
   });
 }
 

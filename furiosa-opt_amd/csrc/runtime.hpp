@@ -23,6 +23,7 @@ struct fo_runtime {
   uint64_t scratch_bytes = 0;
   int32_t* err_host = nullptr;  // pinned, device-mapped error word: kernels set it only on failure
   int32_t* err_dev = nullptr;   // its device address
+  uint32_t err_ops = 0;         // ops that may have set it since the last check: bit 0 gather, 1 scatter
   // Trace spans (fo_runtime_set_trace): while a sink is set, every op brackets its launches with a
   // pair of events; the spans are read back and handed to the sink at the next synchronize.
   fo_trace_sink trace_sink = nullptr;

@@ -540,17 +540,27 @@ def test_gather_unscaled_i32(rt):
 
 @pytest.mark.parametrize("bad", [-1, 37])
 def test_scatter_gather_bad_index_is_an_error(rt, bad):
+    """A bad index is found on the device: the op returns when enqueued, the next synchronize (or
+    read) reports it once, and the valid indices were applied."""
     s = dict(K=37, D=5, G=4)
     idx = rt.upload(np.array([0, 3, bad, 1], np.int32))
+    table = np.arange(37 * 5, dtype=np.int32)
     out = rt.upload(np.zeros(4 * 5, np.int32))
-    with pytest.raises(fh.FoError, match="index"):
-        rt.gather(out, rt.upload(np.zeros(37 * 5, np.int32)), idx, I32, fh.m("K, D", **s), fh.m("G, D", **s),
-                  fh.m("G", **s), scaled=False)
+    rt.gather(out, rt.upload(table), idx, I32, fh.m("K, D", **s), fh.m("G, D", **s), fh.m("G", **s), scaled=False)
+    with pytest.raises(fh.FoError, match="gather: an index"):
+        rt.sync()
+    rt.sync()  # reported once
+    got = out.read(np.int32).reshape(4, 5)
+    want = table.reshape(37, 5)
+    assert np.array_equal(got[[0, 1, 3]], want[[0, 3, 1]]) and np.all(got[2] == 0)
     s2 = dict(G=4, D=5, K=37)
     cache = rt.upload(np.zeros(37 * 5, np.int32))
-    with pytest.raises(fh.FoError, match="index"):
-        rt.scatter(cache, rt.upload(np.ones(4 * 5, np.int32)), idx, I32, fh.m("G, D", **s2), fh.m("G", **s2),
-                   fh.m("K, D", **s2), fh.m("G", **s2), scaled=False)
+    rt.scatter(cache, rt.upload(np.ones(4 * 5, np.int32)), idx, I32, fh.m("G, D", **s2), fh.m("G", **s2),
+               fh.m("K, D", **s2), fh.m("G", **s2), scaled=False)
+    with pytest.raises(fh.FoError, match="scatter: an index"):
+        cache.read(np.int32)  # a read is a synchronization point too
+    got = cache.read(np.int32).reshape(37, 5)
+    assert np.all(got[[0, 3, 1]] == 1) and got.sum() == 3 * 5
 
 
 # ---- safetensors loading (tensor/memory.rs:190-223) ------------------------------------------------
