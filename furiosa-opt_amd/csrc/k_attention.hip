@@ -50,6 +50,17 @@ __device__ __forceinline__ f32x16_t mma(const i32x4_t& a, const i32x4_t& b, cons
                                                  0, 0);
 }
 
+// The two values of lanes l and l ^ 32 (v_permlane32_swap: lanes below 32 get {own, l + 32},
+// lanes from 32 get {l - 32, own}, so both halves see the pair in the same order).
+struct LanePair {
+  float lo, hi;
+};
+__device__ __forceinline__ LanePair half_pair(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+
 // Two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   f32x2_t v = {a, b};
@@ -120,7 +131,10 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
 #pragma unroll
     for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(xs[kt][r], xs[kt][r + 1]));
   }
-  bmax = __builtin_fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+  {
+    const LanePair b = half_pair(bmax);  // the query's other 32 keys live in lane ^ 32
+    bmax = __builtin_fmaxf(b.lo, b.hi);
+  }
   bmax = __builtin_bit_cast(float, pack_bf16(bmax, 0.f) << 16);
   // Online softmax step with a lazy reference max: O and the sum are rescaled only when some
   // lane's block max exceeds its reference max by more than kTau, so p = exp(s - m_run) stays
@@ -304,7 +318,8 @@ __global__ void __launch_bounds__(256, 2) k_attn_fwd(uint16_t* __restrict__ out,
   // out[myq][d] = bf16( bf16(o) / (l + EPS) ); lane holds d = 32t + 8*(r/4) + 4g + r%4. The
   // quotient is correctly rounded (l >= 1, so it is finite and the divisor normal); both narrows
   // are the hardware's round-to-nearest-even (finite inputs give finite, normal-or-zero o).
-  const float l_run = l_part + __shfl_xor(l_part, 32, 64);
+  const LanePair lp = half_pair(l_part);
+  const float l_run = lp.lo + lp.hi;
   if (myq < seq) {
     const float denom = l_run + kEps;
     const float rinv = __fdiv_rn(1.0f, denom);
