@@ -121,10 +121,13 @@ __global__ void __launch_bounds__(256) k_relayout_tiled(T* __restrict__ dst, con
 // scatter in, 16-byte reads out).
 // TS0 x TSJ tiles (elements along wheel 0 x wheel jw): 64 x 64, or one chunk wide on the side
 // whose run is one chunk long, with as many elements as a 64 x 64 tile.
+// Wheel bw (if >= 0) is a broadcast axis (src stride 0): the tile is read once and written once
+// per live position of it, instead of a block per position re-reading the same source tile.
 template <typename T, int TS0, int TSJ>
 __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, const T* __restrict__ src,
                                                           int64_t dst_base, int64_t src_base, Wheels<1> w, int jw,
-                                                          uint32_t outer_count, uint32_t tiles0, uint32_t tilesj) {
+                                                          uint32_t outer_count, uint32_t tiles0, uint32_t tilesj,
+                                                          int bw) {
   typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
   constexpr int V = 16 / sizeof(T);  // elements per 16-byte chunk
   constexpr int CPR = TSJ / V;       // chunks per tile row on the read side (along j)
@@ -136,7 +139,7 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
   uint32_t tj = bid % tilesj;
   uint32_t outer = bid / tilesj;
   if (outer >= outer_count) return;
-  int64_t soff = 0, dpos = 0, place = 1, place_j = 0;
+  int64_t soff = 0, dpos = 0, place = 1, place_j = 0, place_b = 0;
   bool live_outer = true;
   uint32_t q = outer;
   for (int i = 0; i < w.n; ++i) {
@@ -144,8 +147,8 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
       place *= w.size[0];
       continue;
     }
-    if (i == jw) {
-      place_j = place;
+    if (i == jw || i == bw) {
+      (i == jw ? place_j : place_b) = place;
       place *= w.size[i];
       continue;
     }
@@ -159,6 +162,7 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
   }
   if (!live_outer) return;  // uniform: a dead outer digit leaves the whole tile unwritten
   const uint32_t n0 = w.size[0], nj = w.size[jw];
+  const uint32_t nb = bw >= 0 ? w.live[bw] : 1;
   const int64_t s0 = w.stride[0][0];
   for (int c = threadIdx.x; c < TS0 * CPR; c += 256) {
     const int r = c / CPR, cc = c % CPR;  // src row d0 = r, chunk cc along j
@@ -174,7 +178,11 @@ __global__ void __launch_bounds__(256) k_relayout_tiled16(T* __restrict__ dst, c
   for (int c = threadIdx.x; c < TSJ * CPW; c += 256) {
     const int r = c / CPW, cc = c % CPW;  // dst row j = r, chunk cc along d0
     const uint32_t dj = tj * TSJ + r, d0 = t0 * TS0 + cc * V;
-    if (dj < nj && d0 < n0) *(vec_t*)(dst + dst_base + dpos + (int64_t)dj * place_j + d0) = *(const vec_t*)&tile[r][cc * V];
+    if (dj < nj && d0 < n0) {
+      const vec_t v = *(const vec_t*)&tile[r][cc * V];
+      T* o = dst + dst_base + dpos + (int64_t)dj * place_j + d0;
+      for (uint32_t b = 0; b < nb; ++b) *(vec_t*)(o + (int64_t)b * place_b) = v;
+    }
   }
 }
 
@@ -327,6 +335,12 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
   if (jw > 0 && total == count) {
     uint32_t tiles0 = (w.size[0] + ts0 - 1) / ts0, tilesj = (w.size[jw] + tsj - 1) / tsj;
     uint32_t outer = (uint32_t)(total / ((int64_t)w.size[0] * w.size[jw]));
+    // The largest broadcast (src stride 0) outer wheel is looped inside the 16-byte kernel's blocks.
+    int bw = -1;
+    for (int i = 1; i < w.n; ++i)
+      if (i != jw && w.stride[0][i] == 0 && w.size[i] > 1 && (bw < 0 || w.size[i] > w.size[bw])) bw = i;
+    const uint32_t outer16 = bw >= 0 ? outer / w.size[bw] : outer;
+    const int64_t blocks16 = (int64_t)tiles0 * tilesj * outer16;
     int64_t blocks = (int64_t)tiles0 * tilesj * outer;
     if (blocks < (1ll << 31)) {
       // 16-byte path: whole chunks along both tile axes, every base, stride and place a multiple
@@ -338,14 +352,14 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
         if (i != jw) v16 = (w.stride[0][i] % VEC) == 0;
       if (v16 || !chunk_run) {
         if (v16 && ts0 == VEC)
-          hipLaunchKernelGGL((k_relayout_tiled16<T, VEC, 4096 / VEC>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
-                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+          hipLaunchKernelGGL((k_relayout_tiled16<T, VEC, 4096 / VEC>), dim3((uint32_t)blocks16), dim3(256), 0, s,
+                             (T*)dst, (const T*)src, dst_base, src_base, w, jw, outer16, tiles0, tilesj, bw);
         else if (v16 && tsj == VEC)
-          hipLaunchKernelGGL((k_relayout_tiled16<T, 4096 / VEC, VEC>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
-                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+          hipLaunchKernelGGL((k_relayout_tiled16<T, 4096 / VEC, VEC>), dim3((uint32_t)blocks16), dim3(256), 0, s,
+                             (T*)dst, (const T*)src, dst_base, src_base, w, jw, outer16, tiles0, tilesj, bw);
         else if (v16)
-          hipLaunchKernelGGL((k_relayout_tiled16<T, 64, 64>), dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst,
-                             (const T*)src, dst_base, src_base, w, jw, outer, tiles0, tilesj);
+          hipLaunchKernelGGL((k_relayout_tiled16<T, 64, 64>), dim3((uint32_t)blocks16), dim3(256), 0, s, (T*)dst,
+                             (const T*)src, dst_base, src_base, w, jw, outer16, tiles0, tilesj, bw);
         else
           hipLaunchKernelGGL(k_relayout_tiled<T>, dim3((uint32_t)blocks), dim3(256), 0, s, (T*)dst, (const T*)src,
                              dst_base, src_base, w, jw, outer, tiles0, tilesj);
