@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(64 * kSplit) k_rmsnorm_softmax_split(uint16_t*
   if (threadIdx.x == 0) g_bad = 0;
   __syncthreads();
   // Gain staged once per block, widened by the reference rule; at or above 2^120 in magnitude it
-  // takes the exact path, as in k_rmsnorm_softmax.
+  // takes the exact path, as in k_rmsnorm_softmax_dma.
   int bad_local = 0;
   for (int i = threadIdx.x; i < cols; i += blockDim.x) {
     float gv = bf16_to_f32(gain[i]);

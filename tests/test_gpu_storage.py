@@ -139,6 +139,14 @@ def test_transpose_short_src_runs(rt, dt, shape):
     run_transpose(rt, sizes, a, b, dt[0], dt[1], allow_broadcast=True)
 
 
+@pytest.mark.parametrize("dt", [(BF16, np.uint16), (I32, np.int32)], ids=["bf16", "i32"])
+@pytest.mark.parametrize("dst", ["C, X, R", "C, X # 4, R", "X, C, R", "C, R, X"])
+def test_transpose_tiled_broadcast(rt, dt, dst):
+    # A tiled transpose whose destination adds a broadcast axis X (padded to 4 in one case): the
+    # 16-byte tiled kernel reads each source tile once and writes it once per live X position.
+    run_transpose(rt, dict(R=64, C=136, X=3), "R, C", dst, dt[0], dt[1], allow_broadcast=True)
+
+
 @pytest.mark.parametrize("case", SEQ_TABLES, ids=[c[2] for c in SEQ_TABLES])
 def test_transpose_doc_tables(rt, case):
     sizes, mem, stream, _ = case
