@@ -456,10 +456,12 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
     return e ? atoi(e) : 0;
   }();
   int64_t tiles256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
-  // The 8-bit float kinds carry 32-byte fragments: 16 waves of 64x64 exceed 128 VGPRs and spill,
-  // so their large tile is 8 waves of 128x64 (measured 1850 TFLOP/s at 4096^3 against 367 spilled).
-  constexpr bool wide_frag = KIND == kF8E4M3 || KIND == kF8E5M2;
-  int choice = forced ? forced : (tiles256 >= 128 ? (wide_frag ? 2568 : 25616) : 128);
+  // Large problems: 8 waves of 128x64 for bf16 (1-1.5% above 16 waves of 64x64 at 4096^3, same
+  // boxes, 200-launch runs) and for the 8-bit floats, whose 32-byte fragments make 16 waves of 64x64
+  // exceed 128 VGPRs and spill (1850 TFLOP/s against 367); 16 waves of 64x64 for i8 (2030 against
+  // 1960-1970 TOP/s for the W8A8 config).
+  constexpr bool eight_waves = KIND != kI8;
+  int choice = forced ? forced : (tiles256 >= 128 ? (eight_waves ? 2568 : 25616) : 128);
   if (choice == 2568) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 25616) return gemm_launch_cfg<KIND, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 256) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);
