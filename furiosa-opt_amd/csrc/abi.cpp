@@ -310,6 +310,7 @@ void fo_runtime_free(fo_runtime* rt) {
   }
   if (rt->trace_base) (void)hipEventDestroy(rt->trace_base);
   if (rt->scratch) (void)hipFree(rt->scratch);
+  if (rt->scatter_win) (void)hipFree(rt->scatter_win);
   if (rt->err_host) (void)hipHostFree(rt->err_host);
   if (rt->stream) (void)hipStreamDestroy(rt->stream);
   delete rt;
@@ -774,11 +775,25 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     set_device(rt);
     TraceScope trace_span(rt, "scatter");
     int32_t* flag = error_word(rt);
-    int32_t* win = (int32_t*)scratch(rt, (uint64_t)axis_size * 4);
-    FO_HIP(hipMemsetAsync(win, 0xff, (size_t)axis_size * 4, rt->stream));  // -1: no key yet
+    // Winner words: grown (and zeroed) when too short, and zeroed again when the 32-bit generation
+    // wraps; otherwise each call only takes the next generation.
+    if (rt->scatter_win_slots < (uint64_t)axis_size || rt->scatter_gen == UINT32_MAX) {
+      FO_HIP(hipStreamSynchronize(rt->stream));
+      if (rt->scatter_win_slots < (uint64_t)axis_size) {
+        if (rt->scatter_win) FO_HIP(hipFree(rt->scatter_win));
+        rt->scatter_win = nullptr;
+        rt->scatter_win_slots = 0;
+        FO_HIP(hipMalloc((void**)&rt->scatter_win, (size_t)axis_size * 8));
+        rt->scatter_win_slots = (uint64_t)axis_size;
+      }
+      FO_HIP(hipMemsetAsync(rt->scatter_win, 0, (size_t)rt->scatter_win_slots * 8, rt->stream));
+      rt->scatter_gen = 0;
+    }
+    const uint32_t gen = ++rt->scatter_gen;
     const int mem[1] = {0};
     launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,
-                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), win, flag);
+                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd),
+                   rt->scatter_win, gen, flag);
     rt->err_ops |= 2;
   });
 }

@@ -516,14 +516,14 @@ __global__ void __launch_bounds__(kBlock) k_gather_vec(uint8_t* __restrict__ dst
 template <int V>
 __global__ void __launch_bounds__(kBlock) k_scatter_vec(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
                                                         int64_t eb, const int32_t* __restrict__ idx,
-                                                        const int32_t* __restrict__ win, uint32_t total, FastDiv cdiv,
-                                                        uint32_t keys, uint32_t axis_size, int32_t div, Wheels<1> ws,
-                                                        Wheels<1> wd) {
+                                                        const uint64_t* __restrict__ win, uint64_t tag, uint32_t total,
+                                                        FastDiv cdiv, uint32_t keys, uint32_t axis_size, int32_t div,
+                                                        Wheels<1> ws, Wheels<1> wd) {
   typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
   for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
     uint32_t k = cdiv.div(t), c = t - k * cdiv.d;
     int32_t a = decode_index(idx, k, div, axis_size);
-    if (a < 0 || win[a] != (int32_t)k) continue;
+    if (a < 0 || win[a] != (tag | k)) continue;
     const uint32_t p = c * V;
     *(vec_t*)(dst + wheel_offset(wd, p * axis_size + (uint32_t)a) * eb) =
         *(const vec_t*)(src + wheel_offset(ws, p * keys + k) * eb);
@@ -541,29 +541,31 @@ bool payload_vec_ok(const Wheels<1>& w, int inner_slot_wheels, int V) {
   return true;
 }
 
-// win[a] = the last key slot whose index is a: the serial scatter's last write wins.
+// win[a] = tag | the last key slot whose index is a: the serial scatter's last write wins. `tag` is
+// the call's generation in the high word, so entries of earlier calls (lower generations) lose to
+// any key of this one and the array never needs clearing between calls.
 __global__ void __launch_bounds__(kBlock) k_scatter_winners(const int32_t* __restrict__ idx, uint32_t keys,
-                                                            uint32_t axis_size, int32_t div, int32_t* __restrict__ win,
-                                                            int32_t* __restrict__ flag) {
+                                                            uint32_t axis_size, int32_t div, uint64_t* __restrict__ win,
+                                                            uint64_t tag, int32_t* __restrict__ flag) {
   for (uint32_t k = blockIdx.x * kBlock + threadIdx.x; k < keys; k += gridDim.x * kBlock) {
     int32_t a = decode_index(idx, k, div, axis_size);
     if (a < 0)
       *flag = 1;
     else
-      atomicMax(win + a, (int32_t)k);
+      atomicMax((unsigned long long*)(win + a), (unsigned long long)(tag | k));
   }
 }
 
 // dst[off_d(p, index[k])] = src[off_s(p, k)] for the winning key slot k of each target.
 template <typename T>
 __global__ void __launch_bounds__(kBlock) k_scatter(T* __restrict__ dst, const T* __restrict__ src,
-                                                    const int32_t* __restrict__ idx, const int32_t* __restrict__ win,
-                                                    uint32_t total, FastDiv kdiv, uint32_t axis_size, int32_t div,
-                                                    Wheels<1> ws, Wheels<1> wd) {
+                                                    const int32_t* __restrict__ idx, const uint64_t* __restrict__ win,
+                                                    uint64_t tag, uint32_t total, FastDiv kdiv, uint32_t axis_size,
+                                                    int32_t div, Wheels<1> ws, Wheels<1> wd) {
   for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
     uint32_t p = kdiv.div(t), k = t - p * kdiv.d;
     int32_t a = decode_index(idx, k, div, axis_size);
-    if (a < 0 || win[a] != (int32_t)k) continue;
+    if (a < 0 || win[a] != (tag | k)) continue;
     dst[wheel_offset(wd, p * axis_size + (uint32_t)a)] = src[wheel_offset(ws, t)];
   }
 }
@@ -1377,9 +1379,11 @@ void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx
 
 void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                     int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* win, int32_t* flag) {
+                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, uint64_t* win, uint32_t gen,
+                    int32_t* flag) {
+  const uint64_t tag = (uint64_t)gen << 32;
   hipLaunchKernelGGL(k_scatter_winners, dim3(grid_for(keys)), dim3(kBlock), 0, s, idx, (uint32_t)keys,
-                     (uint32_t)axis_size, div, win, flag);
+                     (uint32_t)axis_size, div, win, tag, flag);
   FO_HIP(hipGetLastError());
   const int V = (int)(16 / elem_bytes);
   if (((uintptr_t)dst | (uintptr_t)src) % 16 == 0 && payload_vec_ok(ws, ws_slot_wheels, V) &&
@@ -1388,14 +1392,14 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
     dim3 g(grid_for(total)), b(kBlock);
     const FastDiv cdiv(nch);
     if (V == 8)
-      hipLaunchKernelGGL(k_scatter_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, total,
-                         cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+      hipLaunchKernelGGL(k_scatter_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, tag,
+                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
     else if (V == 4)
-      hipLaunchKernelGGL(k_scatter_vec<4>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, total,
-                         cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+      hipLaunchKernelGGL(k_scatter_vec<4>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, tag,
+                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
     else
       hipLaunchKernelGGL(k_scatter_vec<16>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win,
-                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+                         tag, total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
     FO_HIP(hipGetLastError());
     return;
   }
@@ -1404,15 +1408,15 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
   const FastDiv kdiv((uint32_t)keys);
   switch (elem_bytes) {
     case 1:
-      hipLaunchKernelGGL(k_scatter<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, idx, win, total, kdiv,
+      hipLaunchKernelGGL(k_scatter<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, idx, win, tag, total, kdiv,
                          (uint32_t)axis_size, div, ws, wd);
       break;
     case 2:
-      hipLaunchKernelGGL(k_scatter<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, idx, win, total, kdiv,
+      hipLaunchKernelGGL(k_scatter<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, idx, win, tag, total, kdiv,
                          (uint32_t)axis_size, div, ws, wd);
       break;
     case 4:
-      hipLaunchKernelGGL(k_scatter<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, idx, win, total, kdiv,
+      hipLaunchKernelGGL(k_scatter<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, idx, win, tag, total, kdiv,
                          (uint32_t)axis_size, div, ws, wd);
       break;
     default:

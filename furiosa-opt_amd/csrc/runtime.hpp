@@ -23,6 +23,11 @@ struct fo_runtime {
   uint64_t scratch_bytes = 0;
   int32_t* err_host = nullptr;  // pinned, device-mapped error word: kernels set it only on failure
   int32_t* err_dev = nullptr;   // its device address
+  // Scatter's last-key-per-target words (see k_scatter_winners): zeroed when allocated, then tagged
+  // with a per-call generation instead of cleared per call.
+  uint64_t* scatter_win = nullptr;
+  uint64_t scatter_win_slots = 0;
+  uint32_t scatter_gen = 0;
   uint32_t err_ops = 0;         // ops that may have set it since the last check: bit 0 gather, 1 scatter
   // Trace spans (fo_runtime_set_trace): while a sink is set, every op brackets its launches with a
   // pair of events; the spans are read back and handed to the sink at the next synchronize.
@@ -142,7 +147,8 @@ void launch_gather(hipStream_t s, void* dst, const void* src, const int32_t* idx
 // repeated index (win: axis_size i32 set to -1 beforehand); bad indices skipped, *flag = 1.
 void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* idx, int64_t elem_bytes,
                     int64_t payload, int64_t keys, int64_t axis_size, int32_t div, const Wheels<1>& ws,
-                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, int32_t* win, int32_t* flag);
+                    const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, uint64_t* win, uint32_t gen,
+                    int32_t* flag);
 // Transmute: dst live rank k <- src live rank k; dst padding zeroed.
 void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_count,
                       const Wheels<1>& dst_self, const Wheels<1>& src_self);
