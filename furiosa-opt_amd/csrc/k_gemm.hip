@@ -357,7 +357,8 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   // DMA issue, with its MFMAs queued behind, for ~1000 of the ~3600 clocks of a stage (per-stage
   // timestamps); split and placed this way the bf16 GEMM runs 9-10% faster. The scheduling
   // barriers keep the MFMAs on their side of the readiness barrier and of the first part.
-  constexpr int NP = KST < 2 ? KST : 2;
+  // Two k-steps per stage (the 8-bit floats): one part after the MFMAs measured 3-4% faster.
+  constexpr int NP = KST <= 2 ? 1 : 2;
   // S (a constant at each inlined call): s >= 1 and every stage refilled here is full.
   auto stage = [&](int s, bool S) __attribute__((always_inline)) {
 #pragma unroll
@@ -484,7 +485,7 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   FO_HIP(hipGetLastError());
 }
 
-// Tile choice: 256x256 with 16 waves of 64x64 (one tile per CU at 4096^2, four waves per SIMD)
+// Tile choice: 256x256 with 8 waves of 128x64 (one tile per CU at 4096^2, two waves per SIMD)
 // when the problem is large, 128x128 otherwise (measured best on MI355X among 128, 256 with 4, 8
 // and 16 waves). FO_GEMM_TILE overrides it for measurement: 128, 256 (4 waves of 128x128),
 // 2568 (8 waves of 128x64) or 25616 (16 waves).
@@ -496,12 +497,11 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
     return e ? atoi(e) : 0;
   }();
   int64_t tiles256 = ((d.M + 255) / 256) * ((d.N + 255) / 256) * d.batch;
-  // Large problems: 8 waves of 128x64 for bf16 (1-1.5% above 16 waves of 64x64 at 4096^3, same
-  // boxes, 200-launch runs) and for the 8-bit floats, whose 32-byte fragments make 16 waves of 64x64
-  // exceed 128 VGPRs and spill (1850 TFLOP/s against 367); 16 waves of 64x64 for i8 (2030 against
-  // 1960-1970 TOP/s for the W8A8 config).
-  constexpr bool eight_waves = KIND != kI8;
-  int choice = forced ? forced : (tiles256 >= 128 ? (eight_waves ? 2568 : 25616) : 128);
+  // Large problems: 8 waves of 128x64 for every kind: bf16 1-1.5% above 16 waves of 64x64 at
+  // 4096^3 (same boxes, 200-launch runs); the 8-bit floats' 32-byte fragments make 16 waves of
+  // 64x64 exceed 128 VGPRs and spill (1850 TFLOP/s against 367); i8 (the W8A8 config) 2175-2186
+  // against 2135-2142 TOP/s with the refill split in parts.
+  int choice = forced ? forced : (tiles256 >= 128 ? 2568 : 128);
   if (choice == 2568) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 25616) return gemm_launch_cfg<KIND, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 256) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);
