@@ -171,6 +171,16 @@ __device__ __forceinline__ void* uniform_ptr(const void* p) {
 }
 __device__ __forceinline__ int uniform_i32(int64_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
 
+// Two 4-column groups of 16-bit outputs (vg and vg + 1 of an MFMA tile: lanes l < 32 hold columns
+// 8 vg + 0..3 of row l, lanes l + 32 columns 8 vg + 4..7) regrouped across the wave halves by
+// v_permlane32_swap: lane l < 32 gets columns 8 vg + 0..7 of row l, lane l + 32 columns
+// 8 (vg + 1) + 0..7, so each lane stores 16 contiguous bytes.
+__device__ __forceinline__ i32x4_t regroup8(i32x2_t a, i32x2_t b) {
+  const auto r0 = __builtin_amdgcn_permlane32_swap((uint32_t)a[0], (uint32_t)b[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap((uint32_t)a[1], (uint32_t)b[1], false, false);
+  return i32x4_t{(int)r0[0], (int)r1[0], (int)r0[1], (int)r1[1]};
+}
+
 template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   using M = MfmaT<KIND>;
@@ -400,6 +410,42 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   constexpr int OB = (int)sizeof(out_t);
   const bool vec = g.ldc_n == 1 && (g.ldc_m * OB) % (4 * OB) == 0 && (cb * OB) % (4 * OB) == 0 &&
                    ((uintptr_t)g.c % (4 * OB)) == 0 && (OUT != 4 || ((uintptr_t)g.scale % 16) == 0);
+  if constexpr (OB == 2) {
+    // 16-bit outputs of a wave tile wholly inside C: 16-byte stores of 8 columns (two per row
+    // and instruction) instead of 8-byte ones.
+    const bool wide = vec && g.ldc_m % 8 == 0 && cb % 8 == 0 && ((uintptr_t)g.c % 16) == 0 &&
+                      (OUT != 4 || !g.acc_out) && m0 + wm * TWM + TWM <= g.M && n0 + wn * TWN + TWN <= g.N;
+    if (wide) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int64_t row = m0 + wm * TWM + i * 32 + frow;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int vp = 0; vp < 4; vp += 2) {
+            i32x2_t w[2];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+              const int vg = vp + d;
+              float sc[4] = {0.f, 0.f, 0.f, 0.f};
+              if constexpr (OUT == 4) {
+                typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+                f32x4_t s4 = *(const f32x4_t*)(g.scale + n0 + wn * TWN + j * 32 + 8 * vg + 4 * half);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sc[e] = s4[e];
+              }
+              out_t o4[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o4[e] = convert_out<KIND, OUT>(acc[i][j], vg * 4 + e, sc[e]);
+              w[d] = __builtin_bit_cast(i32x2_t, o4);
+            }
+            const int64_t col = n0 + wn * TWN + j * 32 + 8 * vp + 8 * half;
+            *(i32x4_t*)(C + cb + row * g.ldc_m + col) = regroup8(w[0], w[1]);
+          }
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t row = m0 + wm * TWM + i * 32 + frow;
