@@ -66,6 +66,15 @@ __device__ __forceinline__ LanePair half_pair(float v) {
   return {__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
 }
 
+// Two 4-column bf16 groups of an MFMA output row (lanes l < 32 hold columns c + 0..3, lanes l + 32
+// columns c + 4..7, for group a at c and group b at c + 8) regrouped across the wave halves: lane
+// l < 32 gets columns c + 0..7 of its row, lane l + 32 columns c + 8..15, one 16-byte store each.
+__device__ __forceinline__ i32x4_t regroup8(i32x2_t a, i32x2_t b) {
+  const auto r0 = __builtin_amdgcn_permlane32_swap((uint32_t)a[0], (uint32_t)b[0], false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap((uint32_t)a[1], (uint32_t)b[1], false, false);
+  return i32x4_t{(int)r0[0], (int)r1[0], (int)r0[1], (int)r1[1]};
+}
+
 // Two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   f32x2_t v = {a, b};
@@ -325,24 +334,28 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
   // are the hardware's round-to-nearest-even (finite inputs give finite, normal-or-zero o).
   const LanePair lp = half_pair(l_part);
   const float l_run = lp.lo + lp.hi;
-  if (myq < seq) {
-    const float denom = l_run + kEps;
-    const float rinv = __fdiv_rn(1.0f, denom);
-    uint16_t* orow = out + head * (int64_t)seq * D + (int64_t)myq * D;
+  // Every lane computes (a query past the end sees every key, so its l >= 1 too); lanes l and
+  // l + 32 hold the same query row, so the regrouped 16-byte stores share one condition.
+  const float denom = l_run + kEps;
+  const float rinv = __fdiv_rn(1.0f, denom);
+  uint16_t* orow = out + head * (int64_t)seq * D + (int64_t)myq * D;
 #pragma unroll
-    for (int t = 0; t < C::DT; ++t)
+  for (int t = 0; t < C::DT; ++t)
 #pragma unroll
-      for (int blk = 0; blk < 4; ++blk) {
-        i32x2_t wv;
+    for (int bp = 0; bp < 4; bp += 2) {
+      i32x2_t wv[2];
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
+          const int blk = bp + d;
           const uint32_t ob = pack_bf16(o[t][blk * 4 + 2 * e], o[t][blk * 4 + 2 * e + 1]);
           const float a = __builtin_bit_cast(float, ob << 16), b = __builtin_bit_cast(float, ob & 0xffff0000u);
-          wv[e] = (int)pack_bf16(div_cr(a, denom, rinv), div_cr(b, denom, rinv));
+          wv[d][e] = (int)pack_bf16(div_cr(a, denom, rinv), div_cr(b, denom, rinv));
         }
-        *(i32x2_t*)(orow + t * 32 + 8 * blk + 4 * g) = wv;
-      }
-  }
+      const i32x4_t q4 = regroup8(wv[0], wv[1]);
+      if (myq < seq) *(i32x4_t*)(orow + t * 32 + 8 * bp + 8 * g) = q4;
+    }
 }
 
 template <int D>
