@@ -175,6 +175,11 @@ __device__ __forceinline__ int uniform_i32(int64_t v) { return __builtin_amdgcn_
 // 8 vg + 0..3 of row l, lanes l + 32 columns 8 vg + 4..7) regrouped across the wave halves by
 // v_permlane32_swap: lane l < 32 gets columns 8 vg + 0..7 of row l, lane l + 32 columns
 // 8 (vg + 1) + 0..7, so each lane stores 16 contiguous bytes.
+// The same regrouping for 8-bit outputs: 4 columns are one dword, 8 columns 8 bytes.
+__device__ __forceinline__ i32x2_t regroup8_b(uint32_t a, uint32_t b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  return i32x2_t{(int)r[0], (int)r[1]};
+}
 __device__ __forceinline__ i32x4_t regroup8(i32x2_t a, i32x2_t b) {
   const auto r0 = __builtin_amdgcn_permlane32_swap((uint32_t)a[0], (uint32_t)b[0], false, false);
   const auto r1 = __builtin_amdgcn_permlane32_swap((uint32_t)a[1], (uint32_t)b[1], false, false);
@@ -410,6 +415,33 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   constexpr int OB = (int)sizeof(out_t);
   const bool vec = g.ldc_n == 1 && (g.ldc_m * OB) % (4 * OB) == 0 && (cb * OB) % (4 * OB) == 0 &&
                    ((uintptr_t)g.c % (4 * OB)) == 0 && (OUT != 4 || ((uintptr_t)g.scale % 16) == 0);
+  if constexpr (OB == 1) {
+    // 8-bit outputs of a wave tile wholly inside C: 8-byte stores of 8 columns.
+    const bool wide = vec && g.ldc_m % 8 == 0 && cb % 8 == 0 && ((uintptr_t)g.c % 8) == 0 &&
+                      m0 + wm * TWM + TWM <= g.M && n0 + wn * TWN + TWN <= g.N;
+    if (wide) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int64_t row = m0 + wm * TWM + i * 32 + frow;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int vp = 0; vp < 4; vp += 2) {
+            uint32_t w[2];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+              out_t o4[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o4[e] = convert_out<KIND, OUT>(acc[i][j], (vp + d) * 4 + e, 0.f);
+              w[d] = __builtin_bit_cast(uint32_t, o4);
+            }
+            const int64_t col = n0 + wn * TWN + j * 32 + 8 * vp + 8 * half;
+            *(i32x2_t*)(C + cb + row * g.ldc_m + col) = regroup8_b(w[0], w[1]);
+          }
+      }
+      return;
+    }
+  }
   if constexpr (OB == 2) {
     // 16-bit outputs of a wave tile wholly inside C: 16-byte stores of 8 columns (two per row
     // and instruction) instead of 8-byte ones.
