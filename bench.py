@@ -249,7 +249,7 @@ def bench_mlp(fh, rt, steps, warmup, rng):
     return dict(ms=ev, wall_ms=wall, us=ev * 1e3, flop=2.0 * B * (I * Hd + Hd * O))
 
 
-def cpu_baseline_gemm(target_s: float = 12.0):
+def cpu_baseline_gemm(target_s: float = 30.0):
     """The oracle's contraction_in fold (oracle/fo_cpu.c) on a bounded row sample of the same GEMM."""
     from oracle import emulator as emu
 
