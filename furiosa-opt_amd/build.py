@@ -25,6 +25,7 @@ SOURCES = [
     "mapping.cpp",
     "abi.cpp",
     "k_storage.hip",
+    "k_vector.hip",
     "k_gemm.hip",
     "k_rowops.hip",
     "k_attention.hip",

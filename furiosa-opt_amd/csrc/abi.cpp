@@ -165,9 +165,15 @@ void raise_device_errors(fo_runtime* rt) {
   rt->err_ops = 0;
   if (__atomic_load_n(rt->err_host, __ATOMIC_ACQUIRE) == 0) return;
   __atomic_store_n(rt->err_host, 0, __ATOMIC_RELEASE);
-  throw InvalidArg(std::string(ops == 1 ? "gather" : ops == 2 ? "scatter" : "gather or scatter") +
-                   ": an index is negative or past the indexed axis (in an op issued since the last "
-                   "synchronization; the valid indices were applied)");
+  // Each op that may have set the word names its own failure (the word does not say which op set it).
+  std::string msg;
+  if (ops & 3u)
+    msg = std::string((ops & 3u) == 1u ? "gather" : (ops & 3u) == 2u ? "scatter" : "gather or scatter") +
+          ": an index is negative or past the indexed axis (the valid indices were applied)";
+  if (ops & 4u)
+    msg += std::string(msg.empty() ? "" : "; or ") +
+           "zip3_slots: a tag byte above 15 is not an execution id (that cell passed through)";
+  throw InvalidArg(msg + " -- in an op issued since the last synchronization");
 }
 
 // Shared set-up of scatter / gather: the stream wheels of one side, all digits live.
@@ -536,7 +542,7 @@ int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, con
     check_buf(data, "data");
     check_buf(tag_u8, "tag");
     require(slots != nullptr, "slots is NULL");
-    require(slots->n_regs >= 0 && slots->n_regs <= 4, "n_regs must be 0..4");
+    require(slots->n_regs >= 0 && slots->n_regs <= 3, "zip3_slots: a pass has 0..3 immediate register slots");
     require(t == FO_F32 || t == FO_I32, "zip3_slots: dtype must be f32 or i32");
     int64_t eb = dtype_bytes(t);
     require(n * eb <= dst->bytes && n * eb <= data->bytes && n <= tag_u8->bytes, "zip3_slots: n exceeds a buffer");
@@ -547,8 +553,26 @@ int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, con
     if (n == 0) return;
     set_device(rt);
     TraceScope trace_span(rt, "zip3_slots");
+    int32_t* flag = error_word(rt);
     launch_zip3_slots(rt->stream, dst->ptr, data->ptr, slots->has_port ? port->ptr : nullptr,
-                      (const uint8_t*)tag_u8->ptr, t, n, *slots);
+                      (const uint8_t*)tag_u8->ptr, t, n, *slots, flag);
+    rt->err_ops |= 4;
+  });
+}
+
+int32_t fo_branch_tag(fo_runtime* rt, fo_buffer* tag_u8, const fo_buffer* src, fo_dtype t, uint64_t n,
+                      const fo_cmp* cmps) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(tag_u8, "tag");
+    check_buf(src, "src");
+    require(cmps != nullptr, "cmps is NULL");
+    require(t == FO_F32 || t == FO_I32, "branch_tag: dtype must be f32 or i32");
+    require(n <= tag_u8->bytes && n * 4 <= src->bytes, "branch_tag: n exceeds a buffer");
+    if (n == 0) return;
+    set_device(rt);
+    TraceScope trace_span(rt, "branch_tag");
+    launch_branch_tag(rt->stream, (uint8_t*)tag_u8->ptr, src->ptr, t, n, cmps);
   });
 }
 

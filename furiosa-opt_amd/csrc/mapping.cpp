@@ -43,28 +43,38 @@ void check_ident(const std::string& s) {
 // Construction / serialization (MappingSerde, lib.rs:433-543)
 // ---------------------------------------------------------------------------------------------
 
+namespace {
+// Every size, stride, modulo, resize and padding of a mapping is a positive count; a zero would
+// divide by zero in Mapping::size and the resolver, so it is rejected where the JSON is read.
+int64_t positive(const json::Value& b, const char* key) {
+  int64_t n = b.at(key).as_int();
+  if (n <= 0) throw Error(std::string("mapping: '") + key + "' must be positive, got " + std::to_string(n));
+  return n;
+}
+}  // namespace
+
 NodeP from_json(const json::Value& v) {
   if (v.kind != json::Value::Object || v.obj.size() != 1) throw Error("mapping: expected a one-key object");
   const std::string& tag = v.obj[0].first;
   const json::Value& b = v.obj[0].second;
   if (tag == "Symbol") {
-    auto p = mk(Node::Symbol, b.at("size").as_int());
+    auto p = mk(Node::Symbol, positive(b, "size"));
     auto q = std::const_pointer_cast<Node>(p);
     q->sym = b.at("symbol").as_str();
     check_ident(q->sym);
     return p;
   }
-  if (tag == "Stride") return mk(Node::Stride, b.at("stride").as_int(), from_json(b.at("inner")));
-  if (tag == "Modulo") return mk(Node::Modulo, b.at("modulo").as_int(), from_json(b.at("inner")));
-  if (tag == "Resize") return mk(Node::Resize, b.at("resize").as_int(), from_json(b.at("inner")));
+  if (tag == "Stride") return mk(Node::Stride, positive(b, "stride"), from_json(b.at("inner")));
+  if (tag == "Modulo") return mk(Node::Modulo, positive(b, "modulo"), from_json(b.at("inner")));
+  if (tag == "Resize") return mk(Node::Resize, positive(b, "resize"), from_json(b.at("inner")));
   if (tag == "Padding") {
-    auto p = mk(Node::Padding, b.at("padding").as_int(), from_json(b.at("inner")));
+    auto p = mk(Node::Padding, positive(b, "padding"), from_json(b.at("inner")));
     const json::Value* k = b.get("kind");
     std::const_pointer_cast<Node>(p)->pad = k ? pad_from(k->as_str()) : Pad::Top;
     return p;
   }
   if (tag == "Pair") return mk(Node::Pair, 0, from_json(b.at("left")), from_json(b.at("right")));
-  if (tag == "Broadcast") return mk(Node::Broadcast, b.at("size").as_int());
+  if (tag == "Broadcast") return mk(Node::Broadcast, positive(b, "size"));
   throw Error("mapping: unknown node '" + tag + "'");
 }
 
@@ -122,7 +132,10 @@ struct TextParser {
     size_t s = p;
     while (p < t.size() && std::isdigit((unsigned char)t[p])) ++p;
     if (s == p) fail("expected a number");
-    return std::stoll(t.substr(s, p - s));
+    if (p - s > 18) fail("number too large");
+    int64_t n = std::stoll(t.substr(s, p - s));
+    if (n <= 0) fail("a size, stride, modulo or padding must be positive");
+    return n;
   }
   NodeP m0() {
     NodeP l = m1();

@@ -28,7 +28,7 @@ struct fo_runtime {
   uint64_t* scatter_win = nullptr;
   uint64_t scatter_win_slots = 0;
   uint32_t scatter_gen = 0;
-  uint32_t err_ops = 0;         // ops that may have set it since the last check: bit 0 gather, 1 scatter
+  uint32_t err_ops = 0;  // ops that may have set it since the last check: bit 0 gather, 1 scatter, 2 zip3_slots
   // Trace spans (fo_runtime_set_trace): while a sink is set, every op brackets its launches with a
   // pair of events; the spans are read back and handed to the sink at the next synchronize.
   fo_trace_sink trace_sink = nullptr;
@@ -159,8 +159,10 @@ void launch_unpack_i4(hipStream_t s, int8_t* dst, const void* src, uint64_t nbyt
 void launch_pack_i4(hipStream_t s, void* dst, const int32_t* src, uint64_t n);
 void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
                 const fo_op& op);
+// *flag = 1 when a tag byte is above 15 (not an execution id).
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,
-                       uint64_t n, const fo_slots& slots);
+                       uint64_t n, const fo_slots& slots, int32_t* flag);
+void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t, uint64_t n, const fo_cmp* cmps);
 
 // Reduce over a plan: out wheels (memory strides into src) and residue wheels.
 void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,

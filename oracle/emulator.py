@@ -16,7 +16,8 @@ Functions and their reference anchors:
   reduce           BufStorage::reduce           storage/buf.rs:331-376
   contraction      BufStorage::contraction_in   storage/buf.rs:401-447 (ReadPlan :680-753)
   transmute        BufStorage::transmute        storage/buf.rs:592-601
-  map / zip / zip3_slots                        storage/buf.rs:203-250, vector_tensor.rs:892-938
+  map / zip / zip3_slots                        storage/buf.rs:203-250, vector_tensor.rs:892-952
+  branch_tag       apply_branch_config           engine/vector/branch.rs:199-215
   rmsnorm_softmax, attention_prefill, w8a8, mlp, gemm_rows   the chains of fo_cpu.c
 
 Parity status of each function is recorded in tests/test_oracle_golden.py (what pins it).
@@ -66,7 +67,8 @@ def _load():
         "ref_reduce": (None, [P, C.c_int, P, I64, P, I64, P, C.c_int, U32, I64]),
         "ref_map": (None, [P, C.c_int, P, C.c_int, I64, C.c_int, U32, U32, U32]),
         "ref_zip": (None, [P, C.c_int, P, P, C.c_int, I64, C.c_int, U32, U32]),
-        "ref_zip3_slots": (None, [P, P, P, P, C.c_int, I64, C.c_int, U32, C.c_int, P, P, P, C.c_int, U32, U32]),
+        "ref_zip3_slots": (C.c_int, [P, P, P, P, C.c_int, I64, C.c_int, U32, C.c_int, P, P, P, C.c_int, U32, U32]),
+        "ref_branch_tag": (None, [P, P, C.c_int, I64, P, P]),
         "ref_rmsnorm_softmax": (None, [P, P, P, I64, I64, F]),
         "ref_attention_prefill": (None, [P, P, P, P, I64, I64, I64, F, C.c_int, I64, I64, C.c_int]),
         "ref_w8a8": (None, [P, P, P, P, P, I64, I64, I64, I64, I64]),
@@ -142,12 +144,14 @@ def transpose(dst: np.ndarray, src: np.ndarray, src_view: dict, dst_view: dict, 
 
 def _additive(pos: np.ndarray, out_live: np.ndarray):
     """Split a brute-force plan into ReadPlan's base(o) + delta(r) (buf.rs:680-753), checking
-    additivity on every cell that resolves."""
+    additivity on every cell that resolves. A dead (padding) output cell gets base -1: it has no
+    reads, so the fold leaves it at the identity (reduce) or zero (contraction), buf.rs:355-368
+    and :425-437."""
     n_out, n_res = pos.shape
     base = np.full(n_out, -1, dtype=np.int64)
     if n_out == 0 or n_res == 0:
         return base, np.zeros(n_res, dtype=np.int64)
-    good = np.all(pos >= 0, axis=1)
+    good = np.all(pos >= 0, axis=1) & np.asarray(out_live, dtype=bool)
     rows = np.nonzero(good)[0]
     if len(rows) == 0:
         return base, np.zeros(n_res, dtype=np.int64)
@@ -262,16 +266,38 @@ def zip_(a: np.ndarray, b: np.ndarray, in_t: int, dst_t: int, code: int, flags: 
 
 
 def zip3_slots(data, port, tag, t, code, flags, reg_guard, reg_op0, reg_op1, has_port, port_guard, port_op1):
+    """apply_slots over (data, port, tag): at most three register slots (guard masks over the 16
+    execution ids, operands as raw 32-bit words) then the port slot. A tag above 15 raises, as
+    the reference's exec_id panics."""
     n = len(data)
+    if len(reg_guard) > 3:
+        raise ValueError("a VE pass has three immediate register slots")
     out = np.zeros(n, dtype=NP[t])
-    g = np.array(list(reg_guard) + [0] * (4 - len(reg_guard)), dtype=np.uint32)
-    o0 = np.array(list(reg_op0) + [0] * (4 - len(reg_op0)), dtype=np.uint32)
-    o1 = np.array(list(reg_op1) + [0] * (4 - len(reg_op1)), dtype=np.uint32)
+    g = np.array(list(reg_guard) + [0] * (3 - len(reg_guard)), dtype=np.uint32)
+    o0 = np.array(list(reg_op0) + [0] * (3 - len(reg_op0)), dtype=np.uint32)
+    o1 = np.array(list(reg_op1) + [0] * (3 - len(reg_op1)), dtype=np.uint32)
     d = np.ascontiguousarray(data)
     p = np.ascontiguousarray(port) if port is not None else None
     tg = np.ascontiguousarray(tag, dtype=np.uint8)
-    lib.ref_zip3_slots(_p(out), _p(d), _p(p), _p(tg), t, n, code, flags, len(reg_guard), _p(g), _p(o0), _p(o1),
-                       int(has_port), port_guard, port_op1)
+    st = lib.ref_zip3_slots(_p(out), _p(d), _p(p), _p(tg), t, n, code, flags, len(reg_guard), _p(g), _p(o0), _p(o1),
+                            int(has_port), port_guard, port_op1)
+    if st < 0:
+        raise ValueError("an execution id is four bits, but the tag tensor holds a larger byte")
+    return out
+
+
+CMP_KINDS = dict(EQUAL=0, LESS=1, GREATER=2, LESS_UNSIGNED=3, GREATER_UNSIGNED=4, TRUE=5, FALSE=6)
+
+
+def branch_tag(src: np.ndarray, t: int, cmps) -> np.ndarray:
+    """apply_branch_config, TagMode::Comparison (branch.rs:199-215): `cmps` four (kind, boundary)
+    pairs; the boundary is a Python float for f32 streams, an int for i32 streams."""
+    s = np.ascontiguousarray(src).view(np.uint32)
+    kinds = np.array([CMP_KINDS[k] for k, _ in cmps], np.int32)
+    bounds = np.array([np.float32(b).view(np.uint32) if isinstance(b, float) else np.int64(b) & 0xFFFFFFFF
+                       for _, b in cmps], np.uint32)
+    out = np.zeros(len(s), np.uint8)
+    lib.ref_branch_tag(_p(out), _p(s), t, len(s), _p(kinds), _p(bounds))
     return out
 
 

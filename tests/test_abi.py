@@ -44,3 +44,16 @@ def test_null_runtime_is_invalid():
     lib.fo_buffer_free(None)  # no-op
     lib.fo_runtime_free.argtypes = [ctypes.c_void_p]
     lib.fo_runtime_free(None)  # no-op
+
+
+def test_zero_counts_in_mappings_are_rejected():
+    # a zero stride / size / modulo would divide by zero in the resolver: refused at parse time
+    zero_stride = '{"Stride":{"stride":0,"inner":{"Symbol":{"symbol":"A","size":4}}}}'
+    with pytest.raises(fh.FoError, match="must be positive"):
+        fh.sequence(zero_stride, fh.m("A", A=4))
+    with pytest.raises(fh.FoError, match="must be positive"):
+        fh.sequence('{"Symbol":{"symbol":"A","size":0}}', fh.m("A", A=4))
+    with pytest.raises(fh.FoError, match="must be positive"):
+        fh.m("A / 0", A=4)
+    with pytest.raises(fh.FoError, match="must be positive"):
+        fh.m("A % 0", A=4)

@@ -5,6 +5,10 @@ every intermediate is exact (or rounds in a known way) give outputs computed her
 with numpy, and a wrong order of the steps, a missing or misplaced rounding, a transposed operand
 or a wrong mask fails one of them.
 """
+import json
+import struct
+from pathlib import Path
+
 import numpy as np
 import pytest
 
@@ -214,3 +218,38 @@ def test_mlp_relu_and_weight_orientation():
     pred, logits = mlp(x.ravel(), w1.ravel(), b1, w2.ravel(), np.zeros(h), batch, i, h, h)
     want = np.roll(np.maximum(c + b1, 0.0), -1)
     assert np.all(logits == want[None, :]) and np.all(pred == int(np.argmax(want)))
+
+
+# ---- the reference's MNIST answer key (furiosa-opt-examples/tests/mnist_tests.rs:7-53) -------------
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def read_safetensors(path):
+    """{name: (dtype string, shape, raw bytes)} of a safetensors file, parsed as plain data."""
+    raw = Path(path).read_bytes()
+    n = struct.unpack("<Q", raw[:8])[0]
+    header = json.loads(raw[8:8 + n])
+    return {k: (v["dtype"], v["shape"], raw[8 + n + v["data_offsets"][0]:8 + n + v["data_offsets"][1]])
+            for k, v in header.items() if k != "__metadata__"}
+
+
+def mnist_key():
+    """The fixture's weights, the ten images stacked as a batch, and the labels."""
+    t = read_safetensors(GOLDEN / "mnist_hw.safetensors")
+    u16 = lambda name: np.frombuffer(t[name][2], np.uint16)
+    x = np.concatenate([u16(f"hw.image_{i}") for i in range(10)])
+    labels = [int(np.frombuffer(t[f"label_{i}"][2], np.int32)[0]) for i in range(10)]
+    return x, u16("hw.fc1.weight"), u16("fc1.bias"), u16("hw.fc2.weight"), u16("hw.fc2.bias"), labels
+
+
+def first10_argmax(logits):
+    """mnist_tests.rs:38-48: max_by(total_cmp) over the first ten logits (the last maximum wins)."""
+    rows = emu.bf16_to_f32(logits).reshape(10, 16)[:, :10]
+    return [int(9 - np.argmax(r[::-1])) for r in rows]
+
+
+def test_mnist_answer_key():
+    x, w1, b1, w2, b2, labels = mnist_key()
+    assert labels == [7, 2, 1, 0, 4, 1, 4, 9, 5, 9]
+    _, logits = emu.mlp(x, w1, b1, w2, b2, 10, 800, 256, 16)
+    assert first10_argmax(logits) == labels

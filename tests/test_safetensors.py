@@ -66,3 +66,29 @@ def test_corrupt_files_are_errors(tmp_path):
         fh.safetensors_info(p, "w")
     with pytest.raises(fh.FoError, match="cannot open"):
         fh.safetensors_info(tmp_path / "none.safetensors", "w")
+
+
+def test_hostile_headers_are_errors_not_crashes(tmp_path):
+    # A header nested far deeper than any real one is refused (no unbounded recursion).
+    p = tmp_path / "deep.safetensors"
+    h = b'{"w": ' + b"[" * 100000 + b"]" * 100000 + b"}"
+    h += b" " * (-len(h) % 8)
+    p.write_bytes(struct.pack("<Q", len(h)) + h)
+    with pytest.raises(fh.FoError, match="nesting too deep"):
+        fh.safetensors_info(p, "w")
+    # An offset that is a double far outside int64 is refused, not cast.
+    h = b'{"w": {"dtype": "F32", "shape": [1], "data_offsets": [0, 1e300]}}'
+    h += b" " * (-len(h) % 8)
+    p.write_bytes(struct.pack("<Q", len(h)) + h + b"\0" * 4)
+    with pytest.raises(fh.FoError):
+        fh.safetensors_info(p, "w")
+
+
+def test_escaped_tensor_names_decode(tmp_path):
+    # JSON \u escapes (including a surrogate pair) decode to the UTF-8 name a caller passes.
+    p = tmp_path / "esc.safetensors"
+    h = b'{"w\\u00e9\\ud83d\\ude00": {"dtype": "I8", "shape": [2], "data_offsets": [0, 2]}}'
+    h += b" " * (-len(h) % 8)
+    p.write_bytes(struct.pack("<Q", len(h)) + h + b"\x05\x06")
+    dt, shape, _ = fh.safetensors_info(p, "wé\U0001F600")
+    assert dt == fh.I8 and shape == [2]
