@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -12,7 +13,42 @@
 using namespace fo;
 namespace fm = fo::mapping;
 
+// The no-alloc entry point's working memory (fo_contraction_noalloc): one array per GPU, resident
+// from the library's first use on that GPU until the process ends. In host code `scratch` only
+// names the symbol; its device address comes from hipGetSymbolAddress (static_scratch_init).
+constexpr uint64_t kStaticScratchBytes = 64ull << 20;
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_scratch_mu;
+void* g_static_scratch[kMaxDevices] = {};
+
+// Resolves `scratch` on the current device (`device`) once; called by fo_runtime_init.
+void static_scratch_init(int device) {
+  require(device >= 0 && device < kMaxDevices, "device index beyond the static scratch table");
+  std::lock_guard<std::mutex> lock(g_static_scratch_mu);
+  if (g_static_scratch[device]) return;
+  void* p = nullptr;
+  FO_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  require(p != nullptr, "static scratch: no device address");
+  g_static_scratch[device] = p;
+}
+
+// The device address of `scratch` on the runtime's GPU, checked against the request.
+void* static_scratch(const fo_runtime* rt, uint64_t bytes, const char* what) {
+  require(bytes <= kStaticScratchBytes, std::string(what) + ": needs " + std::to_string(bytes) +
+                                            " bytes of scratch, more than the " +
+                                            std::to_string(kStaticScratchBytes >> 20) + " MiB static scratch");
+  void* p = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_static_scratch_mu);
+    p = g_static_scratch[rt->device];
+  }
+  require(p != nullptr, "static scratch not resolved for this device (fo_runtime_init resolves it)");
+  return p;
+}
 
 thread_local std::string g_last_error;
 
@@ -130,7 +166,7 @@ int64_t max_live_offset(const std::vector<fm::Wheel>& ws, int k) {
 }
 
 // The runtime's device scratch, at least `bytes` long (grown after the stream drains).
-void* scratch(fo_runtime* rt, uint64_t bytes) {
+void* runtime_scratch(fo_runtime* rt, uint64_t bytes) {
   if (rt->scratch_bytes < bytes) {
     FO_HIP(hipStreamSynchronize(rt->stream));
     if (rt->scratch) FO_HIP(hipFree(rt->scratch));
@@ -290,6 +326,7 @@ int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
     rt->device = device_index;
     try {
       FO_HIP(hipSetDevice(device_index));
+      static_scratch_init(device_index);
       FO_HIP(hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking));
       for (auto& e : rt->events) FO_HIP(hipEventCreate(&e));
       hipDeviceProp_t prop;
@@ -713,7 +750,7 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
           int64_t most = 0;
           for (int k = 1; k < steps; ++k) most = std::max(most, fm::size(v[k]));
           half = ((uint64_t)most * eb + 255) & ~(uint64_t)255;
-          sc = (uint8_t*)scratch(rt, 2 * half);
+          sc = (uint8_t*)runtime_scratch(rt, 2 * half);
         }
         c.total = (uint32_t)fm::size(v[k1]);
         c.zero_unwritten = 1;
@@ -893,10 +930,17 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
   });
 }
 
-int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs, fo_dtype in_t,
-                       fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
-                       const char* out_map) {
-  return guard([&] {
+}  // extern "C"
+
+namespace {
+
+// Backend::contraction behind both entry points. `noalloc`: working memory (the i4 unpack and the
+// i32 staging of an i4 result) comes from the static scratch instead of the runtime's, so the call
+// allocates no device memory.
+void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs, fo_dtype in_t,
+                      fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
+                      const char* out_map, bool noalloc) {
+  {
     check_rt(rt);
     check_buf(out, "out");
     check_buf(lhs, "lhs");
@@ -931,7 +975,8 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     if (in_t == FO_I4) {
       auto up = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
       const uint64_t la = up(lhs->bytes * 2), ra = up(rhs->bytes * 2), oa = out_t == FO_I4 ? (uint64_t)out_count * 4 : 0;
-      uint8_t* sc = (uint8_t*)scratch(rt, la + ra + oa);
+      uint8_t* sc = noalloc ? (uint8_t*)static_scratch(rt, la + ra + oa, "contraction_noalloc")
+                            : (uint8_t*)runtime_scratch(rt, la + ra + oa);
       launch_unpack_i4(rt->stream, (int8_t*)sc, lhs->ptr, lhs->bytes);
       launch_unpack_i4(rt->stream, (int8_t*)(sc + la), rhs->ptr, rhs->bytes);
       L = sc;
@@ -1003,6 +1048,26 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
     };
     run();
     if (in_t == FO_I4 && out_t == FO_I4) launch_pack_i4(rt->stream, out->ptr, (const int32_t*)O, (uint64_t)out_count);
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs, fo_dtype in_t,
+                       fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
+                       const char* out_map) {
+  return guard([&] {
+    contraction_impl(rt, out, lhs, rhs, in_t, out_t, lhs_map, rhs_map, pre_reduce, out_map, false);
+  });
+}
+
+int32_t fo_contraction_noalloc(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs,
+                               fo_dtype in_t, fo_dtype out_t, const char* lhs_map, const char* rhs_map,
+                               const char* pre_reduce, const char* out_map) {
+  return guard([&] {
+    contraction_impl(rt, out, lhs, rhs, in_t, out_t, lhs_map, rhs_map, pre_reduce, out_map, true);
   });
 }
 

@@ -113,6 +113,10 @@ _sig = {
         C.c_int32,
         [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p],
     ),
+    "fo_contraction_noalloc": (
+        C.c_int32,
+        [_P, _P, _P, _P, C.c_int32, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p],
+    ),
     "fo_transmute": (C.c_int32, [_P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p]),
     "fo_scatter": (C.c_int32, [_P, _P, _P, _P, C.c_int32, C.c_char_p, C.c_char_p, C.c_char_p, C.c_char_p,
                                C.c_int32]),
@@ -284,6 +288,11 @@ class Runtime:
                     rhs_map: str, pre_reduce: str, out_map: str):
         _check(_lib.fo_contraction(self.h, out.h, lhs.h, rhs.h, in_t, out_t, lhs_map.encode(), rhs_map.encode(),
                                    pre_reduce.encode(), out_map.encode()))
+
+    def contraction_noalloc(self, out: "Buffer", lhs: "Buffer", rhs: "Buffer", in_t: int, out_t: int, lhs_map: str,
+                            rhs_map: str, pre_reduce: str, out_map: str):
+        _check(_lib.fo_contraction_noalloc(self.h, out.h, lhs.h, rhs.h, in_t, out_t, lhs_map.encode(),
+                                           rhs_map.encode(), pre_reduce.encode(), out_map.encode()))
 
     def transmute(self, dst: "Buffer", src: "Buffer", dtype: int, src_map: str, dst_map: str):
         _check(_lib.fo_transmute(self.h, dst.h, src.h, dtype, src_map.encode(), dst_map.encode()))

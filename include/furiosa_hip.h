@@ -291,6 +291,18 @@ int32_t fo_contraction(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, con
                        fo_dtype out_t, const char* lhs_map, const char* rhs_map, const char* pre_reduce,
                        const char* out_map);
 
+/* fo_contraction without device allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. Same arguments, results and errors as fo_contraction; the working memory
+ * an i4 contraction needs (each operand unpacked to one byte per element, plus an i32 staging of an
+ * i4 result) comes from a static 64 MiB device array per GPU, resident from fo_runtime_init until
+ * the process ends, instead of the runtime's grown scratch. A contraction needing more than 64 MiB
+ * of it is FO_ERR_INVALID. The array is shared by every call on that GPU: calls that overlap on one
+ * GPU (two runtimes' streams) race and must be serialized by the caller. */
+int32_t fo_contraction_noalloc(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, const fo_buffer* rhs,
+                               fo_dtype in_t, fo_dtype out_t, const char* lhs_map, const char* rhs_map,
+                               const char* pre_reduce, const char* out_map);
+
 /* Lazy relayout fusion: the chain src -> views[1] -> ... -> views[n_views-1] of full-view
  * transposes as Tensor::transpose runs them (tensor/mod.rs:302-306: each intermediate a fresh zeroed
  * storage; BufStorage::transpose, storage/buf.rs:257-313), with only the last materialized, in dst.
