@@ -27,6 +27,7 @@ SOURCES = [
     "k_storage.hip",
     "k_vector.hip",
     "k_gemm.hip",
+    "k_gemm_wheels.hip",
     "k_rowops.hip",
     "k_attention.hip",
     "k_mlp.hip",

@@ -52,6 +52,46 @@ void* static_scratch(const fo_runtime* rt, uint64_t bytes, const char* what) {
 
 thread_local std::string g_last_error;
 
+// Pending widens. The engine widens both contraction operands with Backend::map before
+// contraction_prewidened (contract_outer, engine/contraction/outer/mod.rs:145-163), so a
+// contraction over f32 (i32) operands usually reads buffers that are exact casts of bf16 or 8-bit
+// float (i8) data. fo_map records each such cast (dst, src, source type, element count); a
+// contraction whose two operands both have a record of the same source type reads the narrow
+// sources instead -- the MFMA kernels consume them directly, and the generic fold widens them the
+// same way the map did, so its result is unchanged. Any op that writes a buffer (or frees it)
+// drops the records naming it as either side. Records are process-wide, as buffers are.
+struct WidenRecord {
+  const fo_buffer* dst;
+  const fo_buffer* src;
+  fo_dtype src_t;
+  uint64_t n;
+};
+std::mutex g_widen_mu;
+std::vector<WidenRecord> g_widen;
+
+void note_write(const fo_buffer* b) {
+  if (!b) return;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
+                               [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
+                g_widen.end());
+}
+
+void record_widen(const fo_buffer* dst, const fo_buffer* src, fo_dtype src_t, uint64_t n) {
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  g_widen.push_back({dst, src, src_t, n});
+}
+
+bool find_widen(const fo_buffer* dst, WidenRecord* out) {
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == dst) {
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
 template <typename F>
 int32_t guard(F&& f) {
   try {
@@ -418,6 +458,7 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
 
 void fo_buffer_free(fo_buffer* buf) {
   if (!buf) return;
+  note_write(buf);
   if (buf->ptr) {
     (void)hipSetDevice(buf->device);
     (void)hipDeviceSynchronize();
@@ -445,6 +486,7 @@ int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* ds
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     require(host != nullptr || bytes == 0, "host pointer is NULL");
     require(bytes <= dst->bytes, "write of " + std::to_string(bytes) + " bytes exceeds the buffer");
     set_device(rt);
@@ -543,6 +585,7 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     require(op != nullptr, "op is NULL");
     require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
@@ -550,6 +593,12 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     set_device(rt);
     TraceScope trace_span(rt, "map");
     launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
+    // An exact widening cast (the engine's contract_outer widen) leaves a record for the
+    // contraction that follows.
+    const bool widen = op->code == FO_OP_CAST && dst != src &&
+                       ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
+                        (dst_t == FO_I32 && src_t == FO_I8));
+    if (widen) record_widen(dst, src, src_t, n);
   });
 }
 
@@ -558,6 +607,7 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(a, "a");
     check_buf(b, "b");
     require(op != nullptr, "op is NULL");
@@ -576,6 +626,7 @@ int32_t fo_zip3_slots(fo_runtime* rt, fo_buffer* dst, const fo_buffer* data, con
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(data, "data");
     check_buf(tag_u8, "tag");
     require(slots != nullptr, "slots is NULL");
@@ -602,6 +653,7 @@ int32_t fo_branch_tag(fo_runtime* rt, fo_buffer* tag_u8, const fo_buffer* src, f
   return guard([&] {
     check_rt(rt);
     check_buf(tag_u8, "tag");
+    note_write(tag_u8);
     check_buf(src, "src");
     require(cmps != nullptr, "cmps is NULL");
     require(t == FO_F32 || t == FO_I32, "branch_tag: dtype must be f32 or i32");
@@ -621,6 +673,7 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     fm::Factors sv = flat(src_view, "src_view"), dv = flat(dst_view, "dst_view");
     // transpose_broadcast (backend/op_prep.rs:18-28): the dst leftover after carving out src.
@@ -673,6 +726,7 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     require(n_views >= 2 && views != nullptr, "transpose_chain: needs at least two views");
     const int64_t eb = dtype_bytes(t);
@@ -769,6 +823,7 @@ int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     fm::Factors sm = flat(src_map, "src_map"), dm = flat(dst_map, "dst_map");
     int64_t eb = dtype_bytes(t);
@@ -808,6 +863,7 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     check_buf(index, "index");
     fm::Factors sm = flat(src_map, "src_map"), km = flat(key_map, "key_map"), dm = flat(dst_map, "dst_map"),
@@ -864,6 +920,7 @@ int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     check_buf(index, "index");
     fm::Factors sm = flat(src_map, "src_map"), dm = flat(dst_map, "dst_map"), im = flat(idx_map, "idx_map");
@@ -901,6 +958,7 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     check_buf(src, "src");
     require(t == FO_F32 || t == FO_I32 || t == FO_BF16, "reduce: dtype must be f32, i32 or bf16");
     require(op >= FO_RED_ADD && op <= FO_RED_ADD_SAT, "reduce: unknown op");
@@ -943,6 +1001,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
   {
     check_rt(rt);
     check_buf(out, "out");
+    note_write(out);
     check_buf(lhs, "lhs");
     check_buf(rhs, "rhs");
     bool ok_types = (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
@@ -972,6 +1031,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     const void *L = lhs->ptr, *R = rhs->ptr;
     void* O = out->ptr;
     int64_t lhs_len, rhs_len;
+    WidenRecord wl{}, wr{};
     if (in_t == FO_I4) {
       auto up = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
       const uint64_t la = up(lhs->bytes * 2), ra = up(rhs->bytes * 2), oa = out_t == FO_I4 ? (uint64_t)out_count * 4 : 0;
@@ -988,58 +1048,108 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
       }
       lhs_len = (int64_t)lhs->bytes * 2;
       rhs_len = (int64_t)rhs->bytes * 2;
+    } else if ((in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) && find_widen(rhs, &wr) &&
+               wl.src_t == wr.src_t && (int64_t)wl.n >= fm::size(l) && (int64_t)wr.n >= fm::size(r)) {
+      // contraction_prewidened of two widened operands: contract their narrow sources (the
+      // pending-widen records above), accumulating in the same type.
+      ct = wl.src_t;
+      L = wl.src->ptr;
+      R = wr.src->ptr;
+      lhs_len = (int64_t)wl.n;
+      rhs_len = (int64_t)wr.n;
     } else {
       lhs_len = (int64_t)(lhs->bytes / dtype_bytes(in_t));
       rhs_len = (int64_t)(rhs->bytes / dtype_bytes(in_t));
     }
 
     auto run = [&] {
-      // MFMA path: out wheels split into rows (lhs only) and columns (rhs only), one contiguous
-      // contracted wheel, no padding, every read in bounds.
-      if (gemm_supported(ct, co)) {
-        std::vector<fm::Wheel> mw, nw, bw;
-        int64_t place = 1;
-        std::vector<int64_t> mplace, nplace, bplace;
-        bool shape_ok = true;
-        for (auto& w : ow) {
-          if (w.live != w.size) shape_ok = false;
-          bool la = w.stride[0] != 0, rb = w.stride[1] != 0;
-          if (la && !rb) {
-            mw.push_back(w);
-            mplace.push_back(place);
-          } else if (!la && rb) {
-            nw.push_back(w);
-            nplace.push_back(place);
-          } else if (la && rb) {
-            bw.push_back(w);
-            bplace.push_back(place);
-          } else {
-            mw.push_back(w);  // an output axis neither operand reads: rows that repeat
-            mplace.push_back(place);
-          }
-          place *= w.size;
-        }
-        shape_ok = shape_ok && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1 && rw.size() == 1 &&
-                   rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
-        if (shape_ok) {
+      // Out wheels split into rows (read by lhs only, or by neither operand: repeated rows),
+      // columns (rhs only) and batch cells (both), with the place of each in the dense out stream.
+      struct Part {
+        fm::Wheel w;
+        int64_t place;
+      };
+      std::vector<Part> mw, nw, bw;
+      bool padded = false;
+      int64_t place = 1;
+      for (auto& w : ow) {
+        padded |= w.live != w.size;
+        const bool la = w.stride[0] != 0, rb = w.stride[1] != 0;
+        (la && rb ? bw : (!la && rb) ? nw : mw).push_back({w, place});
+        place *= w.size;
+      }
+      const bool unit_k = rw.size() == 1 && rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
+      if (gemm_supported(ct, co) && unit_k) {
+        // The tiled kernel: one affine row, column and batch wheel each, no padding.
+        if (!padded && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1) {
           GemmDesc d;
-          d.M = mw.empty() ? 1 : mw[0].size;
-          d.N = nw.empty() ? 1 : nw[0].size;
+          d.M = mw.empty() ? 1 : mw[0].w.size;
+          d.N = nw.empty() ? 1 : nw[0].w.size;
           d.K = rw[0].size;
-          d.batch = bw.empty() ? 1 : bw[0].size;
-          d.lda = mw.empty() ? 0 : mw[0].stride[0];
-          d.ldb = nw.empty() ? 0 : nw[0].stride[1];
-          d.ldc_m = mw.empty() ? 0 : mplace[0];
-          d.ldc_n = nw.empty() ? 0 : nplace[0];
-          d.a_batch = bw.empty() ? 0 : bw[0].stride[0];
-          d.b_batch = bw.empty() ? 0 : bw[0].stride[1];
-          d.c_batch = bw.empty() ? 0 : bplace[0];
+          d.batch = bw.empty() ? 1 : bw[0].w.size;
+          d.lda = mw.empty() ? 0 : mw[0].w.stride[0];
+          d.ldb = nw.empty() ? 0 : nw[0].w.stride[1];
+          d.ldc_m = mw.empty() ? 0 : mw[0].place;
+          d.ldc_n = nw.empty() ? 0 : nw[0].place;
+          d.a_batch = bw.empty() ? 0 : bw[0].w.stride[0];
+          d.b_batch = bw.empty() ? 0 : bw[0].w.stride[1];
+          d.c_batch = bw.empty() ? 0 : bw[0].place;
           int64_t amax = (d.batch - 1) * d.a_batch + (d.M - 1) * d.lda + d.K - 1;
           int64_t bmax = (d.batch - 1) * d.b_batch + (d.N - 1) * d.ldb + d.K - 1;
           if (amax < lhs_len && bmax < rhs_len && gemm_aligned(L, R, ct, d)) {
             launch_gemm(rt->stream, O, L, R, ct, co, d);
             return;
           }
+        }
+        // The wheel-decoded kernel: rows, columns and batch cells over any number of wheels
+        // (live digits only; dead out cells zeroed first), when a 32 x 32 tile is at least a
+        // quarter used and every read stays inside the operands.
+        int64_t M = 1, N = 1, B = 1, amax = rw[0].size - 1, bmax = rw[0].size - 1, align = rw[0].size;
+        auto gcd = [](int64_t x, int64_t y) {
+          while (y) {
+            int64_t t = x % y;
+            x = y;
+            y = t;
+          }
+          return x;
+        };
+        for (auto& p : mw) M *= p.w.live, amax += (p.w.live - 1) * p.w.stride[0], align = gcd(align, p.w.stride[0]);
+        for (auto& p : nw) N *= p.w.live, bmax += (p.w.live - 1) * p.w.stride[1], align = gcd(align, p.w.stride[1]);
+        for (auto& p : bw) {
+          B *= p.w.live;
+          amax += (p.w.live - 1) * p.w.stride[0];
+          bmax += (p.w.live - 1) * p.w.stride[1];
+          align = gcd(gcd(align, p.w.stride[0]), p.w.stride[1]);
+        }
+        const int nwheels_ok = (int)std::max({mw.size(), nw.size(), bw.size()}) <= kMaxWheels;
+        if (nwheels_ok && M >= 8 && N >= 8 && amax < lhs_len && bmax < rhs_len &&
+            gemm_wheels_supported(ct, co, rw[0].size, align)) {
+          Wheels<2> dm{}, dn{};
+          Wheels<3> db{};
+          auto fill2 = [](Wheels<2>& d, const std::vector<Part>& ps, int k) {
+            for (auto& p : ps) {
+              if (p.w.live <= 1) continue;
+              const int i = d.n++;
+              d.size[i] = d.live[i] = (uint32_t)p.w.live;
+              d.div[i] = FastDiv((uint32_t)p.w.live);
+              d.stride[0][i] = p.w.stride[k];
+              d.stride[1][i] = p.place;
+            }
+          };
+          fill2(dm, mw, 0);
+          fill2(dn, nw, 1);
+          for (auto& p : bw) {
+            if (p.w.live <= 1) continue;
+            const int i = db.n++;
+            db.size[i] = db.live[i] = (uint32_t)p.w.live;
+            db.div[i] = FastDiv((uint32_t)p.w.live);
+            db.stride[0][i] = p.w.stride[0];
+            db.stride[1][i] = p.w.stride[1];
+            db.stride[2][i] = p.place;
+          }
+          if (padded) launch_zero(rt->stream, O, span_bytes(co, (uint64_t)out_count));
+          launch_gemm_wheels(rt->stream, O, L, R, ct, co, M, N, rw[0].size, B, dm, dn, db);
+          return;
         }
       }
       const int mem[2] = {0, 1};
@@ -1078,6 +1188,7 @@ int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, c
   return guard([&] {
     check_rt(rt);
     check_buf(out, "out");
+    note_write(out);
     check_buf(x, "x");
     check_buf(gain, "gain");
     require(rows > 0 && cols > 0, "rmsnorm_softmax: empty shape");
@@ -1097,6 +1208,7 @@ int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q,
   return guard([&] {
     check_rt(rt);
     check_buf(out, "out");
+    note_write(out);
     check_buf(q, "q");
     check_buf(k, "k");
     check_buf(v, "v");
@@ -1117,6 +1229,8 @@ int32_t fo_gemm_w8a8_dequant(fo_runtime* rt, fo_buffer* out, fo_buffer* acc_out,
   return guard([&] {
     check_rt(rt);
     check_buf(out, "out");
+    note_write(out);
+    note_write(acc_out);
     check_buf(a, "a");
     check_buf(w, "w");
     check_buf(scale, "scale");
@@ -1141,6 +1255,8 @@ int32_t fo_mlp(fo_runtime* rt, fo_buffer* pred_i32, fo_buffer* logits, const fo_
   return guard([&] {
     check_rt(rt);
     check_buf(pred_i32, "pred");
+    note_write(pred_i32);
+    note_write(logits);
     check_buf(x, "x");
     check_buf(w1, "w1");
     check_buf(b1, "b1");
@@ -1185,6 +1301,7 @@ int32_t fo_safetensors_load(fo_runtime* rt, fo_buffer* dst, const char* path, co
   return guard([&] {
     check_rt(rt);
     check_buf(dst, "dst");
+    note_write(dst);
     require(path != nullptr && name != nullptr && element_map != nullptr, "safetensors: NULL argument");
     fm::NodeP m = fm::parse_json(element_map);
     File file(path);

@@ -695,6 +695,52 @@ struct RedT<Bf16Red> {
   }
 };
 
+// Residue reads batched per fold step (see k_reduce_thread / k_contract_generic).
+constexpr int kBatch = 16;
+
+// One tick of an odometer over wheels w (innermost first): the digits and the offsets into each
+// of the NMEM memories advance to the next position.
+template <int NMEM>
+__device__ __forceinline__ void odometer_step(const Wheels<NMEM>& w, uint32_t* digit, int64_t (&off)[NMEM]) {
+  for (int i = 0; i < w.n; ++i) {
+    if (digit[i] + 1 < w.size[i]) {
+      digit[i]++;
+#pragma unroll
+      for (int k = 0; k < NMEM; ++k) off[k] += w.stride[k][i];
+      return;
+    }
+#pragma unroll
+    for (int k = 0; k < NMEM; ++k) off[k] -= (int64_t)digit[i] * w.stride[k][i];
+    digit[i] = 0;
+  }
+}
+
+// Lane `lane`'s 64-bit value, for every lane (`lane` a compile-time constant).
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// Wire offsets of output cell o (decoded from the out wheels) into each memory; dead when a digit
+// is padding (or o is past the output).
+template <int NMEM>
+__device__ __forceinline__ bool cell_base(const Wheels<NMEM>& ow, uint32_t o, uint32_t count, int64_t (&b)[NMEM]) {
+  bool dead = o >= count;
+#pragma unroll
+  for (int k = 0; k < NMEM; ++k) b[k] = 0;
+  uint32_t q = dead ? 0 : o;
+  for (int i = 0; i < ow.n; ++i) {
+    const uint32_t nq = ow.div[i].div(q);
+    const uint32_t d = q - nq * ow.size[i];
+    dead |= d >= ow.live[i];
+#pragma unroll
+    for (int k = 0; k < NMEM; ++k) b[k] += (int64_t)d * ow.stride[k][i];
+    q = nq;
+  }
+  return dead;
+}
+
 template <typename Tag>
 __global__ void __launch_bounds__(kBlock) k_reduce_thread(void* dst, const void* src, int64_t src_len,
                                                           uint32_t out_count, Wheels<1> ow, Wheels<1> rw, int op,
@@ -717,20 +763,24 @@ __global__ void __launch_bounds__(kBlock) k_reduce_thread(void* dst, const void*
       continue;
     }
     uint32_t digit[kMaxWheels] = {};
-    int64_t off = base;
+    int64_t off[1] = {base};
     uint32_t total = 1;
     for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
-    for (uint32_t r = 0; r < total; ++r) {
-      if (off >= 0 && off < src_len) acc = R::apply(op, acc, R::load(src, off));
-      for (int i = 0; i < rw.n; ++i) {
-        if (digit[i] + 1 < rw.size[i]) {
-          digit[i]++;
-          off += rw.stride[0][i];
-          break;
-        }
-        off -= (int64_t)digit[i] * rw.stride[0][i];
-        digit[i] = 0;
+    // kBatch reads are issued before they are folded (still in wire order), so a long residue is
+    // not one memory latency per element.
+    for (uint32_t r0 = 0; r0 < total; r0 += kBatch) {
+      decltype(R::load(src, 0)) v[kBatch];
+      bool ok[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const bool in = r0 + u < total;
+        ok[u] = in && off[0] >= 0 && off[0] < src_len;
+        v[u] = ok[u] ? R::load(src, off[0]) : R::from_bits(0);
+        if (in) odometer_step(rw, digit, off);
       }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (ok[u]) acc = R::apply(op, acc, v[u]);
     }
     R::store(dst, o, acc);
   }
@@ -778,19 +828,91 @@ __global__ void __launch_bounds__(kBlock) k_reduce_wave(void* dst, const void* s
   }
 }
 
+// BufStorage::reduce's per-cell fold with coalesced reads, organised as k_contract_tiled: one wave
+// per 64 output cells, 64 residue positions at a time read by consecutive lanes and staged in LDS,
+// then folded per cell in residue order from the identity.
+template <typename Tag>
+__global__ void __launch_bounds__(256) k_reduce_tiled(void* dst, const void* __restrict__ src, int64_t src_len,
+                                                      uint32_t out_count, Wheels<1> ow, Wheels<1> rw, int op,
+                                                      uint32_t identity, uint32_t total) {
+  using R = RedT<Tag>;
+  using V = decltype(R::load(src, 0));
+  __shared__ V vals[4][64][65];
+  __shared__ uint64_t valid[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (uint64_t g0 = ((uint64_t)blockIdx.x * 4 + wave) * 64; g0 < out_count; g0 += (uint64_t)gridDim.x * 256) {
+    const uint32_t o = (uint32_t)g0 + lane;
+    int64_t b[1];
+    const bool dead = cell_base(ow, o, out_count, b);
+    auto acc = R::from_bits(identity);
+    for (uint32_t r0 = 0; r0 < total; r0 += 64) {
+      const bool rin = r0 + lane < total;
+      int64_t d = 0;
+      if (rin) {
+        uint32_t q = r0 + lane;
+        for (int i = 0; i < rw.n; ++i) {
+          const uint32_t nq = rw.div[i].div(q);
+          d += (int64_t)(q - nq * rw.size[i]) * rw.stride[0][i];
+          q = nq;
+        }
+      }
+#pragma unroll
+      for (int cg = 0; cg < 64; cg += 16) {
+        V v[16];
+        bool ok[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int64_t a = readlane64(b[0], cg + u) + d;
+          ok[u] = rin && a >= 0 && a < src_len;
+          v[u] = R::load(src, ok[u] ? a : 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          vals[wave][cg + u][lane] = v[u];
+          const uint64_t mask = __ballot(ok[u]);
+          if (lane == 0) valid[wave][cg + u] = mask;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint64_t vm = valid[wave][lane];
+      const int cnt = (int)min(64u, total - r0);
+      if (!dead)
+        for (int j = 0; j < cnt; ++j)
+          if ((vm >> j) & 1u) acc = R::apply(op, acc, vals[wave][lane][j]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (o < out_count) R::store(dst, o, acc);
+  }
+}
+
 template <typename Tag>
 void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_t out_count, const Wheels<1>& ow,
               const Wheels<1>& rw, int op, uint32_t identity) {
   int64_t total = 1;
   for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
   require(total < (1ll << 31), "reduce: residue larger than 2^31");
-  // Thread-per-cell keeps the emulator's exact fold order; use it whenever it fills the GPU, always
-  // for bf16, whose per-step rounding makes any regrouping visible, and for the saturating add,
-  // which is not associative. The wave path regroups, which is exact for the other integer ops.
+  // The thread and tile forms keep the emulator's exact fold order: short residues take the thread
+  // form, long ones the tile form. Fewer than 1024 output cells with a long residue take the wave
+  // form, which splits each cell's residue over 64 lanes -- a regrouping, exact for the integer ops
+  // (reassociated for f32, as BufStorage::reduce's own contract allows, buf.rs:316-330) -- except
+  // for bf16, whose per-step rounding makes any regrouping visible, and the saturating add, which is
+  // not associative.
   constexpr bool is_f32 = std::is_same<Tag, float>::value;
-  if (out_count >= 16384 || total < 64 || std::is_same<Tag, Bf16Red>::value || op == FO_RED_ADD_SAT) {
+  const bool exact_only = std::is_same<Tag, Bf16Red>::value || op == FO_RED_ADD_SAT;
+  if ((total < 32 || src_len == 0) && (out_count >= 1024 || exact_only || total < 64)) {
     hipLaunchKernelGGL(k_reduce_thread<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
                        (uint32_t)out_count, ow, rw, op, identity);
+  } else if ((out_count >= 1024 || exact_only || total < 64) && src_len > 0) {
+    // Long residues over enough cells (or any residue whose fold must stay serial): the coalesced
+    // tile form, in the thread form's exact order.
+    int64_t blocks = (out_count + 255) / 256;
+    if (blocks > 65535ll * 16) blocks = 65535ll * 16;
+    hipLaunchKernelGGL(k_reduce_tiled<Tag>, dim3((unsigned)blocks), dim3(256), 0, s, dst, src, src_len,
+                       (uint32_t)out_count, ow, rw, op, identity, (uint32_t)total);
   } else {
     // The op's neutral element (-0 for the f32 add, so that a -0 sum keeps its sign).
     uint32_t neutral = 0;
@@ -950,30 +1072,120 @@ __global__ void __launch_bounds__(kBlock) k_contract_generic(Out* __restrict__ o
       continue;
     }
     uint32_t digit[kMaxWheels] = {};
-    int64_t ol = bl, orr = br;
-    for (uint32_t r = 0; r < total; ++r) {
-      if (ol < lhs_len && orr < rhs_len) acc = M::mac(acc, M::widen(lhs[ol]), M::widen(rhs[orr]));
-      for (int i = 0; i < rw.n; ++i) {
-        if (digit[i] + 1 < rw.size[i]) {
-          digit[i]++;
-          ol += rw.stride[0][i];
-          orr += rw.stride[1][i];
-          break;
+    int64_t off[2] = {bl, br};
+    // kBatch pairs of reads are issued before they are folded, in wire order.
+    for (uint32_t r0 = 0; r0 < total; r0 += kBatch) {
+      In va[kBatch], vb[kBatch];
+      bool ok[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const bool in = r0 + u < total;
+        ok[u] = in && off[0] < lhs_len && off[1] < rhs_len;
+        if (ok[u]) {
+          va[u] = lhs[off[0]];
+          vb[u] = rhs[off[1]];
         }
-        ol -= (int64_t)digit[i] * rw.stride[0][i];
-        orr -= (int64_t)digit[i] * rw.stride[1][i];
-        digit[i] = 0;
+        if (in) odometer_step(rw, digit, off);
       }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (ok[u]) acc = M::mac(acc, M::widen(va[u]), M::widen(vb[u]));
     }
     out[o] = narrow<In, Acc, Out>(acc);
+  }
+}
+
+// The product and the sum of contraction_in, as separate roundings (no fused multiply-add).
+__device__ __forceinline__ float mul_of(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_of(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ int32_t mul_of(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
+__device__ __forceinline__ int32_t add_of(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+
+// The same fold with coalesced reads: one wave per 64 consecutive output cells, the residue taken
+// 64 positions at a time. Lane l decodes residue position r0 + l; for each of the wave's cells in
+// turn every lane reads that cell's operands at position r0 + l (consecutive lanes, consecutive
+// positions when the residue is contiguous) and leaves the product in LDS; then lane c folds its
+// cell's 64 products in residue order. The arithmetic and its order are k_contract_generic's.
+constexpr int kTileW = 4;  // waves per block
+template <typename In, typename Acc, typename Out>
+__global__ void __launch_bounds__(64 * kTileW) k_contract_tiled(Out* __restrict__ out, const In* __restrict__ lhs,
+                                                              const In* __restrict__ rhs, int64_t lhs_len,
+                                                              int64_t rhs_len, uint32_t out_count, Wheels<2> ow,
+                                                              Wheels<2> rw, uint32_t total) {
+  using M = MacT<In, Acc>;
+  __shared__ Acc prod[kTileW][64][65];     // a padded row per cell: lane c's reads hit distinct banks
+  __shared__ uint64_t valid[kTileW][64];   // per cell, the residue positions whose reads are in range
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (uint64_t g0 = ((uint64_t)blockIdx.x * kTileW + wave) * 64; g0 < out_count;
+       g0 += (uint64_t)gridDim.x * kTileW * 64) {
+    const uint32_t o = (uint32_t)g0 + lane;
+    int64_t b[2];
+    const bool dead = cell_base(ow, o, out_count, b);
+    Acc acc = Acc(0);
+    for (uint32_t r0 = 0; r0 < total; r0 += 64) {
+      const bool rin = r0 + lane < total;
+      int64_t d[2] = {0, 0};
+      if (rin) {
+        uint32_t q = r0 + lane;
+        for (int i = 0; i < rw.n; ++i) {
+          const uint32_t nq = rw.div[i].div(q);
+          const uint32_t dg = q - nq * rw.size[i];
+          d[0] += (int64_t)dg * rw.stride[0][i];
+          d[1] += (int64_t)dg * rw.stride[1][i];
+          q = nq;
+        }
+      }
+      // 16 cells at a time: their reads are all issued before the first is used.
+#pragma unroll
+      for (int cg = 0; cg < 64; cg += 16) {
+        In va[16], vb[16];
+        bool ok[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int64_t al = readlane64(b[0], cg + u) + d[0], ar = readlane64(b[1], cg + u) + d[1];
+          ok[u] = rin && al < lhs_len && ar < rhs_len;
+          va[u] = lhs[ok[u] ? al : 0];
+          vb[u] = rhs[ok[u] ? ar : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          prod[wave][cg + u][lane] = mul_of(M::widen(va[u]), M::widen(vb[u]));
+          const uint64_t mask = __ballot(ok[u]);
+          if (lane == 0) valid[wave][cg + u] = mask;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint64_t vm = valid[wave][lane];
+      const int cnt = (int)min(64u, total - r0);
+      if (!dead)
+        for (int j = 0; j < cnt; ++j)
+          if ((vm >> j) & 1u) acc = add_of(acc, prod[wave][lane][j]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    if (o < out_count) out[o] = narrow<In, Acc, Out>(acc);
   }
 }
 
 template <typename In, typename Acc, typename Out>
 void contract_t(hipStream_t s, void* out, const void* lhs, const void* rhs, int64_t ll, int64_t rl, int64_t n,
                 const Wheels<2>& ow, const Wheels<2>& rw) {
-  hipLaunchKernelGGL((k_contract_generic<In, Acc, Out>), dim3(grid_for(n)), dim3(kBlock), 0, s, (Out*)out,
-                     (const In*)lhs, (const In*)rhs, ll, rl, (uint32_t)n, ow, rw);
+  int64_t total = 1;
+  for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
+  if (total >= 32 && ll > 0 && rl > 0) {
+    // Long residues: the coalesced tile form (its reads of each 64-position chunk are in flight
+    // together instead of one memory latency per element).
+    int64_t blocks = (n + kTileW * 64 - 1) / (kTileW * 64);
+    if (blocks > 65535ll * 16) blocks = 65535ll * 16;
+    hipLaunchKernelGGL((k_contract_tiled<In, Acc, Out>), dim3((unsigned)blocks), dim3(64 * kTileW), 0, s, (Out*)out,
+                       (const In*)lhs, (const In*)rhs, ll, rl, (uint32_t)n, ow, rw, (uint32_t)total);
+  } else {
+    hipLaunchKernelGGL((k_contract_generic<In, Acc, Out>), dim3(grid_for(n)), dim3(kBlock), 0, s, (Out*)out,
+                       (const In*)lhs, (const In*)rhs, ll, rl, (uint32_t)n, ow, rw);
+  }
   FO_HIP(hipGetLastError());
 }
 

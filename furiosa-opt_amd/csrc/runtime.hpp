@@ -177,20 +177,27 @@ void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const
 struct GemmDesc {
   int64_t M = 0, N = 0, K = 0;
   int64_t batch = 1;
-  // element offsets: A(m,k) = a_batch*b + a_row(m) + k ; B(n,k) = b_batch*b + b_row(n) + k ;
-  // C(m,n) = c_batch*b + c_row(m) + c_col(n). Rows/cols are affine (stride) unless a table is given.
+  // element offsets: A(m,k) = a_batch*b + lda*m + k ; B(n,k) = b_batch*b + ldb*n + k ;
+  // C(m,n) = c_batch*b + ldc_m*m + ldc_n*n.
   int64_t a_batch = 0, b_batch = 0, c_batch = 0;
   int64_t lda = 0, ldb = 0, ldc_m = 0, ldc_n = 1;
-  const int64_t* a_rows = nullptr;  // device tables (nullptr = affine)
-  const int64_t* b_rows = nullptr;
-  const int64_t* c_rows = nullptr;
-  const int64_t* c_cols = nullptr;
 };
 // in_t FO_BF16 -> out FO_BF16 / FO_F32; in_t FO_I8 -> out FO_I8 / FO_I32.
 void launch_gemm(hipStream_t s, void* c, const void* a, const void* b, fo_dtype in_t, fo_dtype out_t,
                  const GemmDesc& d);
 bool gemm_supported(fo_dtype in_t, fo_dtype out_t);
 bool gemm_aligned(const void* a, const void* b, fo_dtype in_t, const GemmDesc& d);
+
+// MFMA contraction over wheel-decoded rows / columns / batch cells (k_gemm_wheels.hip):
+// A(b, m, k) = off_a(b) + off_a(m) + k, B(b, n, k) = off_b(b) + off_b(n) + k,
+// C(b, m, n) = off_c(b) + off_c(m) + off_c(n); mw strides {A, C}, nw {B, C}, bw {A, B, C}; wheels
+// hold live digits only. `elem_align`: the gcd of the operand strides and K (in elements).
+bool gemm_wheels_supported(fo_dtype in_t, fo_dtype out_t, int64_t K, int64_t elem_align);
+void launch_gemm_wheels(hipStream_t s, void* c, const void* a, const void* b, fo_dtype in_t, fo_dtype out_t,
+                        int64_t M, int64_t N, int64_t K, int64_t batches, const Wheels<2>& mw, const Wheels<2>& nw,
+                        const Wheels<3>& bw);
+// Zeroes `bytes` bytes at a 16-byte aligned device address (a fill kernel, not hipMemsetAsync).
+void launch_zero(hipStream_t s, void* p, uint64_t bytes);
 
 void launch_w8a8(hipStream_t s, uint16_t* out, int32_t* acc_out, const int8_t* a, const int8_t* w, const float* scale,
                  int64_t m, int64_t n, int64_t k);

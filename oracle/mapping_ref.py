@@ -276,15 +276,42 @@ def _inverse_table(memory: dict):
     return msyms, radix, keys[order], mpos[live][order]
 
 
+def _project(memory: dict, s: str, c: np.ndarray) -> np.ndarray:
+    """Symbol s's coordinate restricted to the digits `memory` holds: a digit of s the memory's
+    mapping does not cover is read with stride 0 (a broadcast), as the sequencer reads a stream
+    piece that no memory piece covers. A covered digit (weight w, radix p) keeps its value
+    (c // w) % p; a symbol the memory covers whole keeps c."""
+    spans = [(x["w"], x["p"]) for x in factors(memory) if x["kind"] == "T" and x["sym"] == s]
+    top = _tiled_to(spans)
+    if top is not None and top >= _sym_sizes(memory)[s]:
+        return c
+    out = np.zeros_like(c)
+    for w, p in spans:
+        out += ((c // w) % p) * w
+    return out
+
+
+def _tiled_to(spans):
+    """The coordinate bound the digits (weight, radix) cover when they tile it from weight 1
+    without a gap, else None."""
+    cur = 1
+    for w, p in sorted(spans):
+        if w != cur:
+            return None
+        cur = w * p
+    return cur
+
+
 def lookup(memory: dict, coords: Dict[str, np.ndarray], n: int) -> np.ndarray:
     """For each of `n` coordinate tuples, the memory position holding those coordinates
-    (restricted to the memory's own symbols), or -1 where the memory holds no such live cell."""
+    (restricted to the memory's own symbols, and to the digits of each it holds), or -1 where the
+    memory holds no such live cell."""
     msyms, radix, keys, positions = _inverse_table(memory)
     q = np.zeros(n, dtype=np.int64)
     bad = np.zeros(n, dtype=bool)
     for s in msyms:
         c = coords.get(s)
-        c = np.zeros(n, dtype=np.int64) if c is None else c
+        c = np.zeros(n, dtype=np.int64) if c is None else _project(memory, s, c)
         bad |= c >= radix
         q = q * radix + np.minimum(c, radix - 1)
     idx = np.searchsorted(keys, q)

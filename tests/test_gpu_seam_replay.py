@@ -1,0 +1,167 @@
+"""Replays of the Backend call streams that reference kernels issue, through the C ABI.
+
+An unchanged `#[device]` kernel reaches this backend only as a sequence of seam calls: every DMA
+and stage change is a `Tensor::transpose` into a fresh zeroed storage (`to_dm` / `to_hbm`,
+tensor/memory.rs:365-422; fetch, collect, commit), and a contraction is `contract_outer`'s two
+`map(widen)` calls followed by `contract_lane`'s `contraction_prewidened` onto
+[Chip, Cluster, Slice, Lane, Time, Packet] (engine/contraction/outer/mod.rs:145-163,
+engine/contraction/lane.rs:60-79), a `transpose(false)` and the cast. The mappings below are the
+ones those stages build from each kernel's type parameters.
+
+  * base-template/src/kernel/gemm_kernel.rs:11-50 (I = J = 512, K = 64; Slice m![I / 32, J / 32],
+    Lane m![J % 8], Cluster m![1 # 2]): the contraction has 1024 batch cells (I / 32, J / 32 and the
+    DM copies along J / 8 % 4), rows I % 32, columns J % 8 and a padded cluster axis -- the
+    wheel-decoded MFMA kernel runs it on the bf16 sources of the widened operands.
+  * furiosa-opt-examples/src/mnist/mod.rs:8-34 (fc1, X = 800, H = 256): 256 batch cells of one
+    800-long dot product each (M = N = 1), which the generic fold runs, bit-exact, on the bf16
+    sources.
+"""
+import numpy as np
+import pytest
+
+import furiosa_hip as fh
+from oracle import emulator as emu
+from test_gpu_storage import close
+
+pytestmark = pytest.mark.gpu
+
+BF16, F32 = fh.BF16, fh.F32
+
+
+def mapping_size(js):
+    """Mapping::size (furiosa-mapping-types/src/lib.rs:208-219) of a MappingSerde JSON string."""
+    import json
+
+    def size(node):
+        (tag, b), = node.items()
+        if tag == "Symbol":
+            return b["size"]
+        if tag == "Stride":
+            return size(b["inner"]) // b["stride"]
+        if tag == "Pair":
+            return size(b["left"]) * size(b["right"])
+        return b[{"Modulo": "modulo", "Resize": "resize", "Padding": "padding", "Broadcast": "size"}[tag]]
+    return size(json.loads(js))
+
+
+def relayout(rt, src, sizes, views, allow_broadcast=None, dtype=BF16):
+    """A chain of Tensor::transpose calls (each into a fresh zeroed storage of the next view)."""
+    ms = [fh.m(v, **sizes) for v in views]
+    out = rt.upload(np.zeros(mapping_size(ms[-1]), fh.NP_DTYPE[dtype]))
+    rt.transpose_chain(out, src, dtype, ms, allow_broadcast)
+    return out
+
+
+def widen(rt, src, n):
+    """contract_outer's `map(|v| v.cast())` to the f32 accumulator."""
+    out = rt.alloc(n * 4)
+    rt.map(out, F32, src, BF16, n, fh.op("CAST"))
+    return out
+
+
+GEMM = dict(I=512, J=512, K=64)
+CHIP_CLUSTER = "1, 1 # 2"
+
+
+def gemm_kernel_stream(rt, a, b):
+    s = GEMM
+    # to_dm: the operands spread over 256 slices (A copied along J / 32, B along I / 32)
+    a_dm = relayout(rt, a, s, ["I, K", f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, K"], [True])
+    b_dm = relayout(rt, b, s, ["J, K", f"{CHIP_CLUSTER}, I / 32, J / 32, J % 32, K"], [True])
+    # sub: fetch -> collect -> to_trf of B: TRF [Chip, Cluster, Slice, Lane = J % 8, J / 8 % 4, K]
+    trf = relayout(rt, b_dm, s, [f"{CHIP_CLUSTER}, I / 32, J / 32, J % 32, K",
+                                 f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, J / 8 % 4, K",
+                                 f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, J / 8 % 4, K / 16, K % 16",
+                                 f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, J / 8 % 4, K"])
+    # main: fetch (J / 8 % 4 broadcast into time) -> collect of A
+    lhs_view = f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, J / 8 % 4, K / 16, K % 16"
+    lhs = relayout(rt, a_dm, s, [f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, K",
+                                 f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, J / 8 % 4, K", lhs_view], [True, False])
+    rhs_view = f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, J / 8 % 4, K"
+    n_l, n_r = mapping_size(fh.m(lhs_view, **s)), mapping_size(fh.m(rhs_view, **s))
+    lw, rw = widen(rt, lhs, n_l), widen(rt, trf, n_r)
+    pre = f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, I % 32, J / 8 % 4, K / 32, K % 32"
+    out_view = f"{CHIP_CLUSTER}, I / 32, J / 32, J % 8, I % 32, J / 8 % 4"
+    acc = rt.upload(np.full(mapping_size(fh.m(out_view, **s)), 7.0, np.float32))  # dead cells must become 0
+    rt.contraction(acc, lw, rw, F32, F32, *(fh.m(t, **s) for t in (lhs_view, rhs_view, pre, out_view)))
+    raw = acc.read(np.float32)
+    # transpose(false) to [Chip, Cluster, Slice, OutTime, OutPacket], the cast, commit, to_hbm
+    ct_view = f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, J / 8 % 4, J % 8"
+    acc_t = relayout(rt, acc, s, [out_view, ct_view], dtype=F32)
+    n_ct = mapping_size(fh.m(ct_view, **s))
+    cast = rt.alloc(n_ct * 2)
+    rt.map(cast, BF16, acc_t, F32, n_ct, fh.op("CAST"))
+    c = relayout(rt, cast, s, [ct_view, f"{CHIP_CLUSTER}, I / 32, J / 32, I % 32, J % 32", "I, J"])
+    return raw, c.read(np.uint16)
+
+
+def test_gemm_kernel_seam_stream(rt):
+    s = GEMM
+    rng = np.random.default_rng(40)
+    a = emu.f32_to_bf16(rng.standard_normal(512 * 64).astype(np.float32))
+    b = emu.f32_to_bf16(rng.standard_normal(512 * 64).astype(np.float32))
+    acc, c = gemm_kernel_stream(rt, rt.upload(a), rt.upload(b))
+    # The emulator's sequential f32 fold (gemm_rows: lhs [I, K], rhs [J, K]) with one bf16 narrow.
+    want = emu.bf16_to_f32(emu.gemm_rows(a, b, 512, 512, 64, 0, 512)).reshape(512, 512)
+    close(emu.bf16_to_f32(c).reshape(512, 512), want)
+    want_f32 = emu.gemm_rows(a, b, 512, 512, 64, 0, 512, out_t=F32).reshape(512, 512)
+    # the f32 contraction result in its own layout [cluster(2, 1 live), I/32, J/32, J%8, I%32, J/8%4]
+    got = acc.reshape(2, 16, 16, 8, 32, 4)[0]
+    got = got.transpose(0, 3, 1, 4, 2).reshape(512, 512)  # rows I/32 I%32, cols J/32 J/8%4 J%8
+    close(got, want_f32, rel=1e-5)
+    assert np.all(acc.reshape(2, -1)[1] == 0)  # the padded cluster half was zeroed
+
+
+def test_mnist_fc1_seam_stream(rt):
+    s = dict(X=800, H=256)
+    rng = np.random.default_rng(41)
+    x = emu.f32_to_bf16(rng.uniform(0, 1, 800).astype(np.float32))
+    w1 = emu.f32_to_bf16((0.05 * rng.standard_normal(256 * 800)).astype(np.float32))
+    w_dm = relayout(rt, rt.upload(w1), s, ["H, X", f"{CHIP_CLUSTER}, H, X"], [True])
+    x_dm = relayout(rt, rt.upload(x), s, ["X", f"{CHIP_CLUSTER}, H, X"], [True])
+    trf = relayout(rt, x_dm, s, [f"{CHIP_CLUSTER}, H, X", f"{CHIP_CLUSTER}, H, X / 16, X % 16",
+                                 f"{CHIP_CLUSTER}, H, X"])
+    lhs_view = f"{CHIP_CLUSTER}, H, X / 16, X % 16"
+    lhs = relayout(rt, w_dm, s, [f"{CHIP_CLUSTER}, H, X", lhs_view])
+    n = mapping_size(fh.m(lhs_view, **s))
+    lw, rw = widen(rt, lhs, n), widen(rt, trf, n)
+    out_view = f"{CHIP_CLUSTER}, H"
+    acc = rt.upload(np.full(512, 3.0, np.float32))  # dead cells must become 0
+    rt.contraction(acc, lw, rw, F32, F32, fh.m(lhs_view, **s), fh.m(f"{CHIP_CLUSTER}, H, X", **s),
+                   fh.m(f"{CHIP_CLUSTER}, H, X / 32, X % 32", **s), fh.m(out_view, **s))
+    cast = rt.alloc(512 * 2)
+    rt.map(cast, BF16, acc, F32, 512, fh.op("CAST"))
+    h = cast.read(np.uint16)
+    want = emu.gemm_rows(x, w1, 1, 256, 800, 0, 1)  # h = bf16(sum_k f32 x f32 w1), the sequential fold
+    assert np.array_equal(h[:256], want)             # bit-exact
+    assert np.all(h[256:] == 0)                       # dead cluster half
+
+
+def test_widen_record_dropped_when_the_source_is_rewritten(rt):
+    """After map(widen) the f32 copy is the operand; rewriting its bf16 source afterwards must not
+    change what the contraction reads."""
+    s = dict(M=64, N=64, K=64)
+    rng = np.random.default_rng(42)
+    a = emu.f32_to_bf16(rng.standard_normal(64 * 64).astype(np.float32))
+    b = emu.f32_to_bf16(rng.standard_normal(64 * 64).astype(np.float32))
+    da, db = rt.upload(a), rt.upload(b)
+    la, lb = widen(rt, da, 64 * 64), widen(rt, db, 64 * 64)
+    da.write(np.zeros_like(a))  # the source changes after the widen
+    maps = [fh.m(t, **s) for t in ("M, K", "N, K", "M, N, K", "M, N")]
+    out = rt.alloc(64 * 64 * 4)
+    rt.contraction(out, la, lb, F32, F32, *maps)
+    want = emu.gemm_rows(a, b, 64, 64, 64, 0, 64, out_t=F32)
+    assert np.array_equal(out.read(np.float32), want)  # the generic fold over the f32 copies: exact
+
+
+def test_widened_contraction_matches_the_f32_fold(rt):
+    """contraction_prewidened over two widened bf16 operands: through the narrow sources, the generic
+    fold is bit-exact with the f32 fold (M = 4 < 8 keeps it off the MFMA kernels)."""
+    s = dict(M=4, N=96, K=160)
+    rng = np.random.default_rng(43)
+    a = emu.f32_to_bf16(rng.standard_normal(4 * 160).astype(np.float32))
+    b = emu.f32_to_bf16(rng.standard_normal(96 * 160).astype(np.float32))
+    la, lb = widen(rt, rt.upload(a), 4 * 160), widen(rt, rt.upload(b), 96 * 160)
+    out = rt.alloc(4 * 96 * 4)
+    rt.contraction(out, la, lb, F32, F32, *(fh.m(t, **s) for t in ("M, K", "N, K", "M, N, K", "M, N")))
+    assert np.array_equal(out.read(np.float32), emu.gemm_rows(a, b, 4, 96, 160, 0, 4, out_t=F32))

@@ -570,27 +570,54 @@ MFMA_CASES = [
     (dict(M=200, K=96, N=136), "M, K", "N, K", "M, N, K", "M, N"),       # ragged tiles
     (dict(M=128, K=256, N=96), "M, K", "N, K", "M, N, K", "N, M"),       # reordered output
     (dict(B=4, M=64, K=128, N=64), "B, M, K", "B, N, K", "B, M, N, K", "B, M, N"),  # batched
+    # wheel-decoded kernel: rows / columns over several wheels, padded and reordered outputs,
+    # batch cells over several wheels, an output axis neither operand reads (stride 0)
+    (dict(M=96, K=64, N=40), "M, K", "N, K", "M / 32, N, M % 32, K", "M / 32, N, M % 32"),
+    (dict(M=64, K=96, N=48), "M, K", "N, K", "M, N, K", "N / 8, M # 72, N % 8"),
+    (dict(A=4, B=3, M=32, K=64, N=16), "A, B, M, K", "B, A, N, K", "A, B, M, N, K", "B # 4, N, A, M"),
+    (dict(G=5, M=40, K=32, N=24), "M, K", "N, K", "G, M, N, K", "M, G, N"),
+    (dict(I=64, J=64, K=64), "1 # 2, I / 32, J / 32, I % 32, J / 8 % 4, K", "1 # 2, I / 32, J / 32, J % 8, J / 8 % 4, K",
+     "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4, K", "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4"),
 ]
 
 
+# (in_t, out_t, widened): `widened` passes the operands as contract_outer does -- map(widen) to the
+# f32 / i32 accumulator first, then contraction_prewidened -- and the contraction reads their narrow
+# sources; that form's output is the accumulator type.
+MFMA_TYPES = [(BF16, BF16, False), (BF16, F32, False), (I8, I32, False), (I8, I8, False), (fh.F8E4M3, F32, False),
+              (BF16, F32, True), (I8, I32, True), (fh.F8E4M3, F32, True)]
+
+
 @pytest.mark.parametrize("case", MFMA_CASES, ids=[f"{c[1]}.{c[2]}->{c[4]}" for c in MFMA_CASES])
-@pytest.mark.parametrize("types", [(BF16, BF16), (BF16, F32), (I8, I32), (I8, I8)], ids=["bf16", "bf16w", "i8w", "i8"])
+@pytest.mark.parametrize("types", MFMA_TYPES, ids=["bf16", "bf16w", "i8w", "i8", "e4m3w", "bf16w-widened",
+                                                   "i8w-widened", "e4m3w-widened"])
 def test_contraction_mfma(rt, case, types):
     sizes, l_t, r_t, p_t, o_t = case
-    in_t, out_t = types
+    in_t, out_t, widened = types
     lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
     rng = np.random.default_rng(19)
     if in_t == BF16:
         lhs = emu.f32_to_bf16(rng.standard_normal(mr.size(lo)).astype(np.float32))
         rhs = emu.f32_to_bf16(rng.standard_normal(mr.size(ro)).astype(np.float32))
+    elif in_t == fh.F8E4M3:  # small integers: every product and partial sum exact in f32
+        lhs = emu.f32_to_f8(rng.integers(-4, 5, mr.size(lo)).astype(np.float32), in_t)
+        rhs = emu.f32_to_f8(rng.integers(-4, 5, mr.size(ro)).astype(np.float32), in_t)
     else:
         lhs = rng.integers(-127, 128, mr.size(lo)).astype(np.int8)
         rhs = rng.integers(-127, 128, mr.size(ro)).astype(np.int8)
     want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
-    out = rt.alloc(mr.size(oo) * np.dtype(fh.NP_DTYPE[out_t]).itemsize)
-    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[out_t]))  # dead cells must come out zero
+    maps = [fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)]
+    if widened:
+        acc_t = F32 if out_t == F32 else I32
+        wl, wr = rt.alloc(len(lhs) * 4), rt.alloc(len(rhs) * 4)
+        rt.map(wl, acc_t, rt.upload(lhs), in_t, len(lhs), fh.op("CAST"))
+        rt.map(wr, acc_t, rt.upload(rhs), in_t, len(rhs), fh.op("CAST"))
+        rt.contraction(out, wl, wr, acc_t, acc_t, *maps)
+    else:
+        rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *maps)
     got = out.read(out_t)
-    if in_t == I8:
+    if in_t in (I8, fh.F8E4M3):
         assert np.array_equal(got, want)
     elif out_t == F32:
         close(got, want, rel=1e-3)
