@@ -55,6 +55,23 @@ def timed(rt, fn, steps: int, warmup: int):
     return wall, ev
 
 
+def timed_steady(rt, fn, steps: int, warmup: int, min_warm_ms: float = 50.0, min_timed_ms: float = 20.0):
+    """timed() for the configs other than the headline: at least `warmup` launches and at least
+    `min_warm_ms` of them before timing (the clocks settle after an idle gap -- host-side input
+    generation between configs), then at least `steps` launches and at least `min_timed_ms`."""
+    for _ in range(max(1, warmup)):
+        fn()
+    rt.sync()
+    t0 = time.perf_counter()
+    fn()
+    rt.sync()
+    one = max(time.perf_counter() - t0, 1e-6) * 1e3
+    extra = int(min_warm_ms / one)
+    for _ in range(extra):
+        fn()
+    return timed(rt, fn, max(steps, int(min_timed_ms / one) + 1), 0)
+
+
 def traffic_from_profiles(kernel_key: str):
     """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE (profiles/traffic.json,
     written from the committed counter summaries), or None if not measured."""
@@ -95,7 +112,7 @@ def bench_gemm_f8(fh, rt, steps, warmup, rng):
     for name, out_t, ob in (("f32", fh.F32, 4), ("f8e4m3", fh.F8E4M3, 1)):
         c = rt.alloc(M * N * ob)
         fn = lambda: rt.contraction(c, a, b, fh.F8E4M3, out_t, *maps)
-        wall, ev = timed(rt, fn, steps, warmup)
+        wall, ev = timed_steady(rt, fn, steps, warmup)
         flop = 2.0 * M * N * K
         out[name] = dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=2 * M * K + M * N * ob)
     # i4 operands (two per byte), i32 result: unpack to i8 in scratch, then the i8 MFMA GEMM
@@ -103,7 +120,7 @@ def bench_gemm_f8(fh, rt, steps, warmup, rng):
     b4 = rt.upload(rng.integers(0, 256, N * K // 2, dtype=np.uint8))
     c = rt.alloc(M * N * 4)
     fn = lambda: rt.contraction(c, a4, b4, fh.I4, fh.I32, *maps)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     flop = 2.0 * M * N * K
     out["i4_i32"] = dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=M * K + M * N * 4)
     return out
@@ -115,7 +132,7 @@ def bench_norm(fh, rt, steps, warmup, rng):
     g = rt.upload(f32_to_bf16(1.0 + 0.1 * rng.standard_normal(Cc, dtype=np.float32)))
     out = rt.alloc(R * Cc * 2)
     fn = lambda: rt.rmsnorm_softmax(out, x, g, R, Cc, 1e-6)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 2 * R * Cc * 2 + Cc * 2
     return dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
 
@@ -126,7 +143,7 @@ def bench_attention(fh, rt, steps, warmup, rng):
     q, k, v = (rt.upload(f32_to_bf16(rng.standard_normal(n, dtype=np.float32))) for _ in range(3))
     out = rt.alloc(n * 2)
     fn = lambda: rt.attention_prefill(out, q, k, v, B, H, S, D, 11.313708, True)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     flop = 4.0 * B * H * D * S * (S + 1) / 2
     return dict(ms=ev, wall_ms=wall, tflops=flop / (ev * 1e-3) / 1e12, flop=flop, bytes=4 * n * 2)
 
@@ -138,7 +155,7 @@ def bench_w8a8(fh, rt, steps, warmup, rng):
     sc = rt.upload(rng.uniform(1e-3, 1e-2, N).astype(np.float32))
     out = rt.alloc(M * N * 2)
     fn = lambda: rt.gemm_w8a8_dequant(out, None, a, w, sc, M, N, K)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     op = 2.0 * M * N * K
     return dict(ms=ev, wall_ms=wall, tops=op / (ev * 1e-3) / 1e12, op=op, bytes=M * K + N * K + N * 4 + M * N * 2)
 
@@ -155,7 +172,7 @@ def bench_relayout(fh, rt, steps, warmup, rng):
     out = {}
     for name, dv in (("copy", rc), ("transpose", cr)):
         fn = lambda dv=dv: rt.transpose(dst, src, fh.BF16, rc, dv)
-        wall, ev = timed(rt, fn, steps, warmup)
+        wall, ev = timed_steady(rt, fn, steps, warmup)
         nbytes = 2 * R * C * 2
         out[name] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     return out
@@ -174,7 +191,7 @@ def bench_chain(fh, rt, steps, warmup, rng):
     views = [fh.m(t, **s) for t in ("R, C", "R / 8, C, R % 8", "C / 64, R, C % 64", "C, R")]
     mids = [rt.alloc(R * C * 2) for _ in range(2)]
     fn = lambda: rt.transpose_chain(dst, src, fh.BF16, views)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 2 * R * C * 2
     out["chain3_fused"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
 
@@ -182,15 +199,27 @@ def bench_chain(fh, rt, steps, warmup, rng):
         rt.transpose(mids[0], src, fh.BF16, views[0], views[1])
         rt.transpose(mids[1], mids[0], fh.BF16, views[1], views[2])
         rt.transpose(dst, mids[1], fh.BF16, views[2], views[3])
-    wall, ev = timed(rt, stepwise, steps, warmup)
+    wall, ev = timed_steady(rt, stepwise, steps, warmup)
     out["chain3_stepwise"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+
+    def stepwise_fresh():
+        # as Tensor::transpose runs it (tensor/mod.rs:302-306): each step into a fresh zeroed storage
+        m0 = rt.alloc(R * C * 2)
+        rt.transpose(m0, src, fh.BF16, views[0], views[1])
+        m1 = rt.alloc(R * C * 2)
+        rt.transpose(m1, m0, fh.BF16, views[1], views[2])
+        m0.free()
+        rt.transpose(dst, m1, fh.BF16, views[2], views[3])
+        m1.free()
+    wall, ev = timed_steady(rt, stepwise_fresh, steps, warmup)
+    out["chain3_stepwise_fresh"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     # a chain that broadcasts X = 2 in its last step (R,C -> C,R -> C,X,R; 128 MiB in, 256 MiB out):
     # it too collapses to one transpose
     s2 = dict(R=R, C=C, X=2)
     gviews = [fh.m(t, **s2) for t in ("R, C", "C, R", "C, X, R")]
     gdst = rt.alloc(2 * R * C * 2)
     fn = lambda: rt.transpose_chain(gdst, src, fh.BF16, gviews, [False, True])
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 3 * R * C * 2
     out["chain_broadcast"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     del mids, gdst
@@ -202,7 +231,7 @@ def bench_chain(fh, rt, steps, warmup, rng):
     sdst = rt.alloc(4 * 16 * 16 * 512 * 64 * 2)
     sv, dv = fh.m("A, B, C, K", **sw), fh.m("A, B / 4, X, C, B % 4, K", **sw)
     fn = lambda: rt.transpose(sdst, ssrc, fh.BF16, sv, dv, allow_broadcast=True)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 5 * 16 * 16 * 512 * 64 * 2
     out["switch_broadcast"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     return out
@@ -221,7 +250,7 @@ def bench_scatter_gather(fh, rt, steps, warmup, rng):
     blocks = rt.upload((rng.permutation(2048) * (16 * 8 * 128 * 2)).astype(np.int32))
     maps = [fh.m(t, **s) for t in ("NBlocks, KvHeads, PBlock, HeadDim", "NBlocks, PBlock, KvHeads, HeadDim", "NBlocks")]
     fn = lambda: rt.gather(dst, pool, blocks, fh.BF16, *maps, scaled=True)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 2 * n * 2 + 2048 * 4
     out["gather_paged_kv"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     s = dict(K=131072, D=128, C=163840)
@@ -230,9 +259,42 @@ def bench_scatter_gather(fh, rt, steps, warmup, rng):
     rows = rt.upload((rng.permutation(163840)[:131072] * (128 * 2)).astype(np.int32))
     maps = [fh.m(t, **s) for t in ("K, D", "K", "C, D", "K")]
     fn = lambda: rt.scatter(cache, data, rows, fh.BF16, *maps, scaled=True)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     nbytes = 2 * 131072 * 128 * 2 + 131072 * 4
     out["scatter_rows"] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
+    return out
+
+
+def bench_vector(fh, rt, steps, warmup, rng):
+    """The standalone vector-engine seam ops at HBM scale (64 Mi elements): Backend::map (a cast and
+    an f32 exp), zip_with, the tag-guarded zip3 slot pass, the branch unit's tag pass, and reduce
+    over contiguous rows and over strided columns of an [8192, 8192] f32 tensor. GB/s counts each
+    op's bytes read and written once."""
+    n = 64 << 20
+    out = {}
+    x16 = rt.upload(f32_to_bf16(rng.standard_normal(n, dtype=np.float32)))
+    x32 = rt.upload(rng.standard_normal(n, dtype=np.float32))
+    y32 = rt.upload(rng.standard_normal(n, dtype=np.float32))
+    tag = rt.upload(rng.integers(0, 16, n, dtype=np.uint8))
+    d32 = rt.alloc(n * 4)
+    cases = [
+        ("map_cast_bf16_f32", lambda: rt.map(d32, fh.F32, x16, fh.BF16, n, fh.op("CAST")), 6 * n),
+        ("map_exp_f32", lambda: rt.map(d32, fh.F32, x32, fh.F32, n, fh.op("EXP")), 8 * n),
+        ("zip_add_f32", lambda: rt.zip_with(d32, fh.F32, x32, y32, fh.F32, n, fh.op("ADD_F")), 12 * n),
+    ]
+    sl = fh.slots(fh.op("FMA_F"), [(0x000F, 2.0, 1.0), (0x00F0, -1.0, 0.5), (0x0F00, 0.5, 0.0)], (0xF000, 3.0))
+    cases.append(("zip3_slots_fma_f32", lambda: rt.zip3_slots(d32, x32, y32, tag, fh.F32, n, sl), 13 * n))
+    cmps = [("LESS", 0.0), ("GREATER", 1.0), ("EQUAL", 0.0), ("LESS_UNSIGNED", -0.0)]
+    t8 = rt.alloc(n)
+    cases.append(("branch_tag_f32", lambda: rt.branch_tag(t8, x32, fh.F32, n, cmps), 5 * n))
+    s = dict(R=8192, C=8192)
+    rc, r_only, c_only = fh.m("R, C", **s), fh.m("R", **s), fh.m("C", **s)
+    red = rt.alloc(8192 * 4)
+    cases.append(("reduce_rows_f32", lambda: rt.reduce(red, x32, fh.F32, rc, r_only, fh.RED["ADD"], 0), 4 * n + 4 * 8192))
+    cases.append(("reduce_cols_f32", lambda: rt.reduce(red, x32, fh.F32, rc, c_only, fh.RED["ADD"], 0), 4 * n + 4 * 8192))
+    for name, fn, nbytes in cases:
+        wall, ev = timed_steady(rt, fn, steps, warmup)
+        out[name] = dict(ms=ev, wall_ms=wall, gbs=nbytes / (ev * 1e-3) / 1e9, bytes=nbytes)
     return out
 
 
@@ -245,7 +307,7 @@ def bench_mlp(fh, rt, steps, warmup, rng):
     b2 = rt.upload(f32_to_bf16(0.05 * rng.standard_normal(O, dtype=np.float32)))
     pred = rt.alloc(B * 4)
     fn = lambda: rt.mlp(pred, None, x, w1, b1, w2, b2, B, I, Hd, O)
-    wall, ev = timed(rt, fn, steps, warmup)
+    wall, ev = timed_steady(rt, fn, steps, warmup)
     return dict(ms=ev, wall_ms=wall, us=ev * 1e3, flop=2.0 * B * (I * Hd + Hd * O))
 
 
@@ -268,6 +330,95 @@ def cpu_baseline_gemm(target_s: float = 30.0):
     flop = 2.0 * rows * N * K
     return dict(value=flop / dt / 1e12, unit="TFLOP/s", cores=emu.num_threads(), kind="port",
                 sample=f"{rows} of 4096 output rows of the 4096^3 bf16 contraction ({dt:.1f} s)")
+
+
+def host_info():
+    """nproc and the lscpu model name of this host (the CPU baseline's hardware)."""
+    model = ""
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), "")
+    except Exception:
+        pass
+    return dict(nproc=os.cpu_count(), model=model)
+
+
+def median_time(fn, reps: int = 3):
+    fn()  # warm-up
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baselines():
+    """The oracle (the C restatement of the emulator's folds and chains, oracle/fo_cpu.c) on a
+    bounded sample of each config, timed as a median of 3 after one warm-up on all of this host's
+    cores, and once more on one thread. Rates are in each config's GPU unit, over the sample's work."""
+    from oracle import emulator as emu
+
+    rng = np.random.default_rng(7)
+    cores = emu.num_threads()
+    out = {}
+
+    def record(name, fn, work, unit, sample):
+        t_all = median_time(fn)
+        emu.set_threads(1)
+        try:
+            t0 = time.perf_counter()
+            fn()
+            t_one = time.perf_counter() - t0
+        finally:
+            emu.set_threads(cores)
+        scale = 1e12 if unit in ("TFLOP/s", "TOP/s") else 1e9
+        out[name] = dict(value=work / t_all / scale, unit=unit, cores=cores, kind="port", median_of=3,
+                         seconds=t_all, one_thread_value=work / t_one / scale, one_thread_seconds=t_one,
+                         sample=sample)
+
+    M = N = K = 4096
+    a = f32_to_bf16(rng.standard_normal(M * K, dtype=np.float32))
+    b = f32_to_bf16(rng.standard_normal(N * K, dtype=np.float32))
+    rows = 16
+    record("mapped_gemm_4096", lambda: emu.gemm_rows(a, b, M, N, K, 0, rows), 2.0 * rows * N * K, "TFLOP/s",
+           f"{rows} of 4096 output rows of the 4096^3 bf16 contraction")
+    R, Cc = 8192, 4096
+    x = f32_to_bf16(rng.standard_normal(256 * Cc, dtype=np.float32))
+    g = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(Cc, dtype=np.float32))
+    record("rmsnorm_softmax_8192x4096", lambda: emu.rmsnorm_softmax(x, g, 256, Cc, 1e-6), 2 * 256 * Cc * 2 + Cc * 2,
+           "GB/s", "256 of 8192 rows")
+    B, H, S, D = 4, 32, 2048, 128
+    hq = 2
+    q, k, v = (f32_to_bf16(rng.standard_normal(hq * S * D, dtype=np.float32)) for _ in range(3))
+    q0, q1 = S - 64, S
+    flop = 4.0 * hq * D * sum(i + 1 for i in range(q0, q1))
+    record("attention_prefill_b4h32s2048d128",
+           lambda: emu.attention_prefill(q, k, v, hq, S, D, 11.313708, True, q0, q1), flop, "TFLOP/s",
+           f"the last 64 queries (each over 1985-2048 keys) of {hq} of 128 heads")
+    Mw, Nw, Kw = 2048, 8192, 8192
+    aw = rng.integers(-127, 128, 2 * Kw, dtype=np.int8)
+    ww = rng.integers(-127, 128, Nw * Kw, dtype=np.int8)
+    sc = rng.uniform(1e-3, 1e-2, Nw).astype(np.float32)
+    record("w8a8_2048x8192x8192", lambda: emu.w8a8(aw, ww, sc, 2, Nw, Kw), 2.0 * 2 * Nw * Kw, "TOP/s",
+           "2 of 2048 output rows")
+    Bm, I, Hd, O = 64, 784, 128, 10
+    xm = f32_to_bf16(rng.uniform(0, 1, Bm * I).astype(np.float32))
+    w1 = f32_to_bf16(0.05 * rng.standard_normal(Hd * I, dtype=np.float32))
+    b1 = f32_to_bf16(0.05 * rng.standard_normal(Hd, dtype=np.float32))
+    w2 = f32_to_bf16(0.05 * rng.standard_normal(O * Hd, dtype=np.float32))
+    b2 = f32_to_bf16(0.05 * rng.standard_normal(O, dtype=np.float32))
+    t_all = median_time(lambda: emu.mlp(xm, w1, b1, w2, b2, Bm, I, Hd, O))
+    emu.set_threads(1)
+    t0 = time.perf_counter()
+    emu.mlp(xm, w1, b1, w2, b2, Bm, I, Hd, O)
+    t_one = time.perf_counter() - t0
+    emu.set_threads(cores)
+    out["mlp_64x784x128x10"] = dict(value=t_all * 1e6, unit="us", cores=cores, kind="port", median_of=3,
+                                    seconds=t_all, one_thread_value=t_one * 1e6, one_thread_seconds=t_one,
+                                    sample="the whole batch of 64")
+    return out
 
 
 def main():
@@ -295,7 +446,7 @@ def main():
     for name, fnb in (("gemm", bench_gemm), ("gemm_f8", bench_gemm_f8), ("norm", bench_norm),
                       ("attention", bench_attention), ("chain", bench_chain),
                       ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout),
-                      ("scatter_gather", bench_scatter_gather)):
+                      ("scatter_gather", bench_scatter_gather), ("vector", bench_vector)):
         if only and name not in only:
             continue
         res[name] = fnb(fh, rt, args.steps, args.warmup, rng)
@@ -326,6 +477,8 @@ def main():
     if "scatter_gather" in res:
         for k, r in res["scatter_gather"].items():
             configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
+    for k, r in res.get("vector", {}).items():
+        configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     for group in ("relayout", "chain"):
         for k, r in res.get(group, {}).items():
             name = "switch_broadcast_256x512x64_x4_bf16" if k == "switch_broadcast" else f"relayout_{k}_8192x8192_bf16"
@@ -337,6 +490,13 @@ def main():
     cpu = None
     if not args.no_cpu and g:
         cpu = cpu_baseline_gemm()
+    if not args.no_cpu:
+        host = host_info()
+        for name, cb in cpu_baselines().items():
+            if name in configs:
+                configs[name]["cpu_baseline"] = dict(cb, host=host)
+        if cpu is not None:
+            cpu["host"] = host
 
     traffic = traffic_from_profiles("gemm_bf16_4096")
     line = {

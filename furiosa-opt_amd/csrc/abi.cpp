@@ -364,6 +364,8 @@ int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
             "device index " + std::to_string(device_index) + " out of range (" + std::to_string(n) + " devices)");
     auto* rt = new fo_runtime();
     rt->device = device_index;
+    rt->pool = std::make_shared<fo_pool>();
+    rt->pool->device = device_index;
     try {
       FO_HIP(hipSetDevice(device_index));
       static_scratch_init(device_index);
@@ -393,6 +395,13 @@ void fo_runtime_free(fo_runtime* rt) {
   }
   if (rt->trace_base) (void)hipEventDestroy(rt->trace_base);
   if (rt->scratch) (void)hipFree(rt->scratch);
+  if (rt->pool) {
+    std::lock_guard<std::mutex> lock(rt->pool->mu);
+    for (auto& kv : rt->pool->cached) (void)hipFree(kv.second);
+    rt->pool->cached.clear();
+    rt->pool->cached_bytes = 0;
+    rt->pool->orphaned = true;
+  }
   if (rt->scatter_win) (void)hipFree(rt->scatter_win);
   if (rt->err_host) (void)hipHostFree(rt->err_host);
   if (rt->stream) (void)hipStreamDestroy(rt->stream);
@@ -442,17 +451,44 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
     require(out != nullptr, "out is NULL");
     *out = nullptr;
     set_device(rt);
-    auto* b = new fo_buffer();
+    // Size classes: 512-byte multiples below 1 MiB, 2 MiB multiples above. A cached block serves
+    // a request of its class, or a large request up to a quarter smaller than the block.
+    const uint64_t need = bytes ? bytes : 1;
+    const uint64_t cls = need < (1ull << 20) ? (need + 511) & ~511ull : (need + (2ull << 20) - 1) & ~((2ull << 20) - 1);
+    auto b = std::make_unique<fo_buffer>();
     b->bytes = bytes;
     b->device = rt->device;
-    hipError_t e = hipMalloc(&b->ptr, bytes ? bytes : 1);
-    if (e != hipSuccess) {
-      delete b;
-      throw OomError("hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+    b->pool = rt->pool;
+    {
+      std::lock_guard<std::mutex> lock(rt->pool->mu);
+      auto it = rt->pool->cached.lower_bound(cls);
+      if (it != rt->pool->cached.end() && (it->first == cls || (cls >= (1ull << 20) && it->first - it->first / 4 <= cls))) {
+        b->ptr = it->second;
+        b->capacity = it->first;
+        rt->pool->cached_bytes -= it->first;
+        rt->pool->cached.erase(it);
+      }
     }
-    FO_HIP(hipMemsetAsync(b->ptr, 0, bytes ? bytes : 1, rt->stream));
-    FO_HIP(hipStreamSynchronize(rt->stream));
-    *out = b;
+    if (!b->ptr) {
+      hipError_t e = hipMalloc(&b->ptr, cls);
+      if (e != hipSuccess) {
+        // Release the cache (after the stream drains) and try once more.
+        (void)hipGetLastError();
+        FO_HIP(hipStreamSynchronize(rt->stream));
+        std::lock_guard<std::mutex> lock(rt->pool->mu);
+        for (auto& kv : rt->pool->cached) (void)hipFree(kv.second);
+        rt->pool->cached.clear();
+        rt->pool->cached_bytes = 0;
+        e = hipMalloc(&b->ptr, cls);
+      }
+      if (e != hipSuccess)
+        throw OomError("hipMalloc(" + std::to_string(cls) + ") failed: " + hipGetErrorString(e));
+      b->capacity = cls;
+    }
+    // Zero-filled (Backend::zeroed): a fill kernel on the runtime's stream orders the zeros before
+    // every later op of this runtime, including a reuse's previous owner's last reads.
+    launch_zero(rt->stream, b->ptr, (cls + 15) & ~15ull);
+    *out = b.release();
   });
 }
 
@@ -460,9 +496,20 @@ void fo_buffer_free(fo_buffer* buf) {
   if (!buf) return;
   note_write(buf);
   if (buf->ptr) {
-    (void)hipSetDevice(buf->device);
-    (void)hipDeviceSynchronize();
-    (void)hipFree(buf->ptr);
+    bool direct = true;
+    if (buf->pool) {
+      std::lock_guard<std::mutex> lock(buf->pool->mu);
+      if (!buf->pool->orphaned && buf->pool->cached_bytes + buf->capacity <= fo_pool::kMaxCached) {
+        buf->pool->cached.emplace(buf->capacity, buf->ptr);
+        buf->pool->cached_bytes += buf->capacity;
+        direct = false;
+      }
+    }
+    if (direct) {
+      (void)hipSetDevice(buf->device);
+      (void)hipDeviceSynchronize();
+      (void)hipFree(buf->ptr);
+    }
   }
   delete buf;
 }

@@ -810,15 +810,29 @@ __global__ void __launch_bounds__(kBlock) k_reduce_wave(void* dst, const void* s
     // Each lane folds its strided slice from the op's neutral element, so the caller's identity
     // enters the result exactly once, after the lanes combine.
     auto acc = R::from_bits(neutral);
-    for (uint32_t r = lane; r < total && !dead; r += 64) {
-      int64_t off = base;
-      uint32_t rr = r;
-      for (int i = 0; i < rw.n; ++i) {
-        uint32_t nr = rw.div[i].div(rr);
-        off += (int64_t)(rr - nr * rw.size[i]) * rw.stride[0][i];
-        rr = nr;
+    if (rw.n == 1 && rw.stride[0][0] == 1) {
+      // One contiguous residue run: 8 coalesced reads per lane in flight, no odometer.
+      const int64_t lim = dead ? 0 : min((int64_t)total, src_len - base);
+      int64_t r = lane;
+      for (; r + 7 * 64 < lim; r += 8 * 64) {
+        decltype(R::load(src, 0)) v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = R::load(src, base + r + 64 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = R::apply(op, acc, v[u]);
       }
-      if (off >= 0 && off < src_len) acc = R::apply(op, acc, R::load(src, off));
+      for (; r < lim; r += 64) acc = R::apply(op, acc, R::load(src, base + r));
+    } else {
+      for (uint32_t r = lane; r < total && !dead; r += 64) {
+        int64_t off = base;
+        uint32_t rr = r;
+        for (int i = 0; i < rw.n; ++i) {
+          uint32_t nr = rw.div[i].div(rr);
+          off += (int64_t)(rr - nr * rw.size[i]) * rw.stride[0][i];
+          rr = nr;
+        }
+        if (off >= 0 && off < src_len) acc = R::apply(op, acc, R::load(src, off));
+      }
     }
     for (int m = 32; m >= 1; m >>= 1) {
       auto other = __shfl_xor(acc, m, 64);
@@ -889,49 +903,109 @@ __global__ void __launch_bounds__(256) k_reduce_tiled(void* dst, const void* __r
   }
 }
 
+// Reduce with the residue split into kSeg segments per cell: block = 64 consecutive output cells
+// (lanes; consecutive cells sit at consecutive addresses when the out wheel is contiguous) x kSeg
+// waves, each folding its segment of the residue from the op's neutral element, kBatch reads in
+// flight per step; the segments then combine in order through LDS, and the caller's identity enters
+// once. A regrouping: exact for the integer ops, reassociated for f32.
+constexpr int kSeg = 16;
+template <typename Tag>
+__global__ void __launch_bounds__(64 * kSeg) k_reduce_cols(void* dst, const void* __restrict__ src, int64_t src_len,
+                                                           uint32_t out_count, Wheels<1> ow, Wheels<1> rw, int op,
+                                                           uint32_t identity, uint32_t neutral, uint32_t total) {
+  using R = RedT<Tag>;
+  using V = decltype(R::load(src, 0));
+  __shared__ V part[kSeg][64];
+  const int seg = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t o = blockIdx.x * 64 + lane;
+  int64_t b[1];
+  const bool dead = cell_base(ow, o, out_count, b);
+  auto acc = R::from_bits(neutral);
+  const uint32_t len = (total + kSeg - 1) / kSeg;
+  const uint32_t r_begin = min(total, (uint32_t)seg * len), r_end = min(total, r_begin + len);
+  if (!dead && r_begin < r_end) {
+    // the odometer at r_begin
+    uint32_t digit[kMaxWheels] = {};
+    int64_t off[1] = {b[0]};
+    uint32_t q = r_begin;
+    for (int i = 0; i < rw.n; ++i) {
+      const uint32_t nq = rw.div[i].div(q);
+      digit[i] = q - nq * rw.size[i];
+      off[0] += (int64_t)digit[i] * rw.stride[0][i];
+      q = nq;
+    }
+    for (uint32_t r0 = r_begin; r0 < r_end; r0 += kBatch) {
+      V v[kBatch];
+      bool ok[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const bool in = r0 + u < r_end;
+        ok[u] = in && off[0] >= 0 && off[0] < src_len;
+        v[u] = ok[u] ? R::load(src, off[0]) : R::from_bits(0);
+        if (in) odometer_step(rw, digit, off);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (ok[u]) acc = R::apply(op, acc, v[u]);
+    }
+  }
+  part[seg][lane] = acc;
+  __syncthreads();
+  if (seg == 0 && o < out_count) {
+    auto total_acc = R::from_bits(identity);
+    if (!dead)
+      for (int k = 0; k < kSeg; ++k) total_acc = R::apply(op, total_acc, part[k][lane]);
+    R::store(dst, o, total_acc);
+  }
+}
+
 template <typename Tag>
 void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_t out_count, const Wheels<1>& ow,
               const Wheels<1>& rw, int op, uint32_t identity) {
   int64_t total = 1;
   for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
   require(total < (1ll << 31), "reduce: residue larger than 2^31");
-  // The thread and tile forms keep the emulator's exact fold order: short residues take the thread
-  // form, long ones the tile form. Fewer than 1024 output cells with a long residue take the wave
-  // form, which splits each cell's residue over 64 lanes -- a regrouping, exact for the integer ops
-  // (reassociated for f32, as BufStorage::reduce's own contract allows, buf.rs:316-330) -- except
-  // for bf16, whose per-step rounding makes any regrouping visible, and the saturating add, which is
-  // not associative.
+  // Folds that must keep the emulator's exact serial order -- bf16 (`half` arithmetic rounds every
+  // step, so any regrouping shows) and the saturating add (not associative) -- take the thread form
+  // or, for a long residue contiguous in the source, the coalesced tile form. The other folds
+  // (f32, and the integer ops, which are exact in any order) regroup a long residue for
+  // parallelism: a wave per cell when the residue is contiguous, 64 cells x kSeg segments per block
+  // when the cells are. For f32 that reassociates the sum, which BufStorage::reduce's own contract
+  // accepts (buf.rs:316-330) and the f32 tolerance covers.
   constexpr bool is_f32 = std::is_same<Tag, float>::value;
   const bool exact_only = std::is_same<Tag, Bf16Red>::value || op == FO_RED_ADD_SAT;
-  if ((total < 32 || src_len == 0) && (out_count >= 1024 || exact_only || total < 64)) {
-    hipLaunchKernelGGL(k_reduce_thread<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
-                       (uint32_t)out_count, ow, rw, op, identity);
-  } else if ((out_count >= 1024 || exact_only || total < 64) && src_len > 0) {
-    // Long residues over enough cells (or any residue whose fold must stay serial): the coalesced
-    // tile form, in the thread form's exact order.
+  const bool res_contig = rw.n > 0 && rw.stride[0][0] == 1;
+  const bool cells_contig = ow.n > 0 && ow.stride[0][0] == 1;
+  // The op's neutral element (-0 for the f32 add, so that a -0 sum keeps its sign).
+  uint32_t neutral = 0;
+  switch (op) {
+    case FO_RED_ADD:
+      neutral = is_f32 ? 0x80000000u : 0u;
+      break;
+    case FO_RED_MAX:
+      neutral = is_f32 ? 0xff800000u : 0x80000000u;
+      break;
+    case FO_RED_MIN:
+      neutral = is_f32 ? 0x7f800000u : 0x7fffffffu;
+      break;
+    default:
+      neutral = is_f32 ? 0x3f800000u : 1u;
+      break;
+  }
+  if (!exact_only && total >= 64 && res_contig && out_count <= (1 << 20)) {
+    hipLaunchKernelGGL(k_reduce_wave<Tag>, dim3(grid_for(out_count * 64)), dim3(kBlock), 0, s, dst, src, src_len,
+                       (uint32_t)out_count, ow, rw, op, identity, neutral);
+  } else if (!exact_only && total >= 64 && cells_contig) {
+    hipLaunchKernelGGL(k_reduce_cols<Tag>, dim3((unsigned)((out_count + 63) / 64)), dim3(64 * kSeg), 0, s, dst, src,
+                       src_len, (uint32_t)out_count, ow, rw, op, identity, neutral, (uint32_t)total);
+  } else if (total >= 32 && res_contig && src_len > 0) {
     int64_t blocks = (out_count + 255) / 256;
     if (blocks > 65535ll * 16) blocks = 65535ll * 16;
     hipLaunchKernelGGL(k_reduce_tiled<Tag>, dim3((unsigned)blocks), dim3(256), 0, s, dst, src, src_len,
                        (uint32_t)out_count, ow, rw, op, identity, (uint32_t)total);
   } else {
-    // The op's neutral element (-0 for the f32 add, so that a -0 sum keeps its sign).
-    uint32_t neutral = 0;
-    switch (op) {
-      case FO_RED_ADD:
-        neutral = is_f32 ? 0x80000000u : 0u;
-        break;
-      case FO_RED_MAX:
-        neutral = is_f32 ? 0xff800000u : 0x80000000u;
-        break;
-      case FO_RED_MIN:
-        neutral = is_f32 ? 0x7f800000u : 0x7fffffffu;
-        break;
-      default:
-        neutral = is_f32 ? 0x3f800000u : 1u;
-        break;
-    }
-    hipLaunchKernelGGL(k_reduce_wave<Tag>, dim3(grid_for(out_count * 64)), dim3(kBlock), 0, s, dst, src, src_len,
-                       (uint32_t)out_count, ow, rw, op, identity, neutral);
+    hipLaunchKernelGGL(k_reduce_thread<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
+                       (uint32_t)out_count, ow, rw, op, identity);
   }
   FO_HIP(hipGetLastError());
 }
@@ -1175,9 +1249,10 @@ void contract_t(hipStream_t s, void* out, const void* lhs, const void* rhs, int6
                 const Wheels<2>& ow, const Wheels<2>& rw) {
   int64_t total = 1;
   for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
-  if (total >= 32 && ll > 0 && rl > 0) {
-    // Long residues: the coalesced tile form (its reads of each 64-position chunk are in flight
-    // together instead of one memory latency per element).
+  if (total >= 32 && ll > 0 && rl > 0 && rw.n > 0 && (rw.stride[0][0] == 1 || rw.stride[1][0] == 1)) {
+    // Long residues contiguous in an operand: the tile form (consecutive lanes read consecutive
+    // residue positions, and a chunk's reads are in flight together). A strided residue keeps the
+    // thread form, where consecutive lanes are consecutive output cells.
     int64_t blocks = (n + kTileW * 64 - 1) / (kTileW * 64);
     if (blocks > 65535ll * 16) blocks = 65535ll * 16;
     hipLaunchKernelGGL((k_contract_tiled<In, Acc, Out>), dim3((unsigned)blocks), dim3(64 * kTileW), 0, s, (Out*)out,

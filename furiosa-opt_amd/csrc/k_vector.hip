@@ -272,6 +272,46 @@ constexpr int lanes_for() {
   return 16 / (SB < DB ? SB : DB);
 }
 
+// map_word over V words at once, with the (wave-uniform) op dispatch hoisted out of the element
+// loop for the common ops; the rest go element by element through map_word.
+template <int V>
+__device__ __forceinline__ void map_words(const uint32_t* w, uint32_t* r, fo_dtype src_t, fo_dtype dst_t,
+                                          const fo_op& op) {
+  if (op.code == FO_OP_CAST && src_t == FO_BF16 && dst_t == FO_F32) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) r[e] = f32_bits(bf16_to_f32((uint16_t)w[e]));
+  } else if (op.code == FO_OP_CAST && src_t == FO_F32 && dst_t == FO_BF16) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) r[e] = f32_to_bf16(bits_f32(w[e]));
+  } else if (op.code == FO_OP_EXP) {
+#pragma unroll
+    for (int e = 0; e < V; ++e) r[e] = f32_bits(expf(bits_f32(w[e])));
+  } else if (op.code >= FO_OP_ADD_F && op.code <= FO_OP_DIV_F && !(op.flags & FO_OP_SWAP)) {
+    const float b = bits_f32(op.imm0);
+    switch (op.code) {
+      case FO_OP_ADD_F:
+#pragma unroll
+        for (int e = 0; e < V; ++e) r[e] = f32_bits(__fadd_rn(bits_f32(w[e]), b));
+        break;
+      case FO_OP_SUB_F:
+#pragma unroll
+        for (int e = 0; e < V; ++e) r[e] = f32_bits(__fsub_rn(bits_f32(w[e]), b));
+        break;
+      case FO_OP_MUL_F:
+#pragma unroll
+        for (int e = 0; e < V; ++e) r[e] = f32_bits(__fmul_rn(bits_f32(w[e]), b));
+        break;
+      default:
+#pragma unroll
+        for (int e = 0; e < V; ++e) r[e] = f32_bits(__fdiv_rn(bits_f32(w[e]), b));
+        break;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < V; ++e) r[e] = map_word(w[e], src_t, dst_t, op);
+  }
+}
+
 // ---- map -------------------------------------------------------------------------------------
 template <int SB, int DB>
 __global__ void __launch_bounds__(kBlock) k_map_v(void* __restrict__ dst, const void* __restrict__ src, uint64_t n,
@@ -283,9 +323,12 @@ __global__ void __launch_bounds__(kBlock) k_map_v(void* __restrict__ dst, const 
       Regs<V * SB> in;
       Regs<V * DB> out;
       in.load((const uint8_t*)src + j * V * SB);
+      uint32_t w[V], r[V];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        out.template set<DB>(e, map_word(widen_raw(in.template get<SB>(e), src_t), src_t, dst_t, op));
+      for (int e = 0; e < V; ++e) w[e] = widen_raw(in.template get<SB>(e), src_t);
+      map_words<V>(w, r, src_t, dst_t, op);
+#pragma unroll
+      for (int e = 0; e < V; ++e) out.template set<DB>(e, r[e]);
       out.store((uint8_t*)dst + j * V * DB);
     } else {
       for (uint64_t i = j * V; i < n; ++i)
@@ -391,8 +434,45 @@ __device__ __forceinline__ uint32_t tag_of(const Cmps& cs, uint32_t x, bool is_f
   return id;
 }
 
+// Bit b of V execution ids: one (wave-uniform) dispatch on the comparison's kind, then a
+// branch-free loop over the elements.
+template <int V, bool F32>
+__device__ __forceinline__ void tag_bits(const fo_cmp& c, int b, const uint32_t* x, uint32_t* id) {
+  const uint32_t bnd = c.boundary;
+  const float fb = bits_f32(bnd);
+  switch (c.kind) {
+    case FO_CMP_EQUAL:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= (uint32_t)(F32 ? bits_f32(x[e]) == fb : x[e] == bnd) << b;
+      break;
+    case FO_CMP_LESS:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= (uint32_t)(F32 ? bits_f32(x[e]) < fb : (int32_t)x[e] < (int32_t)bnd) << b;
+      break;
+    case FO_CMP_GREATER:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= (uint32_t)(F32 ? fb < bits_f32(x[e]) : (int32_t)bnd < (int32_t)x[e]) << b;
+      break;
+    case FO_CMP_LESS_UNSIGNED:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= (uint32_t)(x[e] < bnd) << b;
+      break;
+    case FO_CMP_GREATER_UNSIGNED:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= (uint32_t)(x[e] > bnd) << b;
+      break;
+    case FO_CMP_TRUE:
+#pragma unroll
+      for (int e = 0; e < V; ++e) id[e] |= 1u << b;
+      break;
+    default:
+      break;
+  }
+}
+
+template <bool F32>
 __global__ void __launch_bounds__(kBlock) k_branch_tag_v(uint8_t* __restrict__ dst, const uint32_t* __restrict__ src,
-                                                         uint64_t n, Cmps cs, int is_f32) {
+                                                         uint64_t n, Cmps cs) {
   constexpr int V = 16;
   const uint64_t nv = (n + V - 1) / V;
   for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
@@ -400,11 +480,14 @@ __global__ void __launch_bounds__(kBlock) k_branch_tag_v(uint8_t* __restrict__ d
       Regs<64> in;
       Regs<16> out;
       in.load(src + j * V);
+      uint32_t id[V] = {};
 #pragma unroll
-      for (int e = 0; e < V; ++e) out.template set<1>(e, tag_of(cs, in.w[e], is_f32));
+      for (int b = 0; b < 4; ++b) tag_bits<V, F32>(cs.c[b], b, in.w, id);
+#pragma unroll
+      for (int e = 0; e < V; ++e) out.template set<1>(e, id[e]);
       out.store(dst + j * V);
     } else {
-      for (uint64_t i = j * V; i < n; ++i) dst[i] = (uint8_t)tag_of(cs, src[i], is_f32);
+      for (uint64_t i = j * V; i < n; ++i) dst[i] = (uint8_t)tag_of(cs, src[i], F32);
     }
   }
 }
@@ -639,8 +722,12 @@ void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t,
     require(cmps[b].kind >= FO_CMP_EQUAL && cmps[b].kind <= FO_CMP_FALSE, "branch_tag: unknown comparison kind");
     cs.c[b] = cmps[b];
   }
-  hipLaunchKernelGGL(k_branch_tag_v, dim3(grid_for((int64_t)((n + 15) / 16))), dim3(kBlock), 0, s, dst,
-                     (const uint32_t*)src, n, cs, (int)(t == FO_F32));
+  if (t == FO_F32)
+    hipLaunchKernelGGL(k_branch_tag_v<true>, dim3(grid_for((int64_t)((n + 15) / 16))), dim3(kBlock), 0, s, dst,
+                       (const uint32_t*)src, n, cs);
+  else
+    hipLaunchKernelGGL(k_branch_tag_v<false>, dim3(grid_for((int64_t)((n + 15) / 16))), dim3(kBlock), 0, s, dst,
+                       (const uint32_t*)src, n, cs);
   FO_HIP(hipGetLastError());
 }
 

@@ -5,6 +5,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -13,8 +16,23 @@
 #include "common.hpp"
 #include "mapping.hpp"
 
+// Device memory cache of one runtime. Blocks freed by fo_buffer_free return here and are handed out
+// again only to buffers of the same runtime, whose every op is ordered on the runtime's one stream:
+// work enqueued with the old owner completes before any work of the new one starts, so neither
+// the free nor the reuse waits for the device. A pool outlives its runtime while buffers of it
+// remain; those then release their blocks directly.
+struct fo_pool {
+  std::mutex mu;
+  int device = 0;
+  bool orphaned = false;                  // the runtime is gone: free blocks directly
+  std::multimap<uint64_t, void*> cached;  // free blocks by capacity
+  uint64_t cached_bytes = 0;
+  static constexpr uint64_t kMaxCached = 8ull << 30;
+};
+
 struct fo_runtime {
   int device = 0;
+  std::shared_ptr<fo_pool> pool;
   hipStream_t stream = nullptr;
   hipEvent_t events[16] = {};
   int cus = 0;
@@ -44,8 +62,10 @@ struct fo_runtime {
 
 struct fo_buffer {
   void* ptr = nullptr;
-  uint64_t bytes = 0;
+  uint64_t bytes = 0;     // the size asked for
+  uint64_t capacity = 0;  // the block's size (the pool's size class)
   int device = 0;
+  std::shared_ptr<fo_pool> pool;
 };
 
 namespace fo {

@@ -79,7 +79,11 @@ int32_t fo_runtime_synchronize(fo_runtime* rt);
 int32_t fo_runtime_device_info(fo_runtime* rt, int32_t* compute_units, char* arch, uint64_t arch_cap);
 
 /* Device allocation of `bytes` (zero-filled), the storage of an `HbmTensor`.
- * Replaces Backend::alloc_hbm / zeroed (backend/mod.rs:60-66, cpu.rs:31-35). */
+ * Replaces Backend::alloc_hbm / zeroed (backend/mod.rs:60-66, cpu.rs:31-35). Stream-ordered: the
+ * zeros are written by a kernel on the runtime's stream (no host wait), and fo_buffer_free returns
+ * the block to the runtime's cache without waiting for the device; the block is reused only by
+ * buffers of the same runtime, whose ops all follow on the same stream. A buffer used on another
+ * runtime's stream must be synchronized with its own runtime first. */
 int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out);
 void fo_buffer_free(fo_buffer* buf);
 /* Device-to-device copy into a new buffer (Storage: Clone). */

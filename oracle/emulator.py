@@ -74,6 +74,7 @@ def _load():
         "ref_w8a8": (None, [P, P, P, P, P, I64, I64, I64, I64, I64]),
         "ref_mlp": (None, [P, P, P, P, P, P, P, I64, I64, I64, I64]),
         "ref_num_threads": (C.c_int, []),
+        "ref_set_threads": (None, [C.c_int]),
     }
     for n, (r, a) in sig.items():
         f = getattr(lib, n)
@@ -361,6 +362,11 @@ def gemm_rows(a: np.ndarray, b: np.ndarray, M: int, N: int, K: int, row_begin: i
 
 def num_threads() -> int:
     return int(lib.ref_num_threads())
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of the folds that follow (the CPU baseline's one-thread timing)."""
+    lib.ref_set_threads(int(n))
 
 
 # ---- scatter / gather (storage/buf.rs:485-576, backend/op_prep.rs:45-89) ---------------------------

@@ -684,3 +684,12 @@ int ref_num_threads(void) {
   return 1;
 #endif
 }
+
+/* The OpenMP team size of later folds (the CPU baseline's one-thread timing). */
+void ref_set_threads(int n) {
+#ifdef _OPENMP
+  omp_set_num_threads(n > 0 ? n : 1);
+#else
+  (void)n;
+#endif
+}

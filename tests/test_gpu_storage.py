@@ -428,6 +428,7 @@ REDUCES = [
     (dict(B=16384, S=4), "B, S", "B", False),
     (dict(A=6, B=4), "B, A", "A # 8", False),           # padded dst: dead cells keep the identity
     (dict(R=60, C=3000), "R, C", "R # 64", False),      # the same on the wave path
+    (dict(A=20000, B=96), "A, B", "A", False),          # many cells, contiguous residue
 ]
 
 
@@ -454,9 +455,11 @@ def test_reduce(rt, case, dt, opname):
     rt.reduce(out, rt.upload(src), t, fh.m(s_t, **sizes), fh.m(d_t, **sizes), fh.RED[opname], ident, bc)
     got = out.read(t)
     n_out = mr.size(do)
-    wave_path = n_out < 16384 and len(src) // max(n_out, 1) >= 64 and dt != "bf16"
+    # f32 folds of 64 or more elements are regrouped for parallelism (the f32 tolerance); integer
+    # folds are exact in any order, bf16 folds stay serial, MAX is order-free: all bit-exact.
+    regrouped = len(src) // max(n_out, 1) >= 64 and dt != "bf16"
     # whole outputs, padding cells included (a dead cell holds the identity)
-    if dt == "i32" or opname == "MAX" or not wave_path:
+    if dt == "i32" or opname == "MAX" or not regrouped:
         assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
     else:
         g = got if dt == "f32" else emu.bf16_to_f32(got)
