@@ -1,0 +1,61 @@
+"""The decode attention chain (attention.rs:226-392, stages in decode_chain.py) through the C ABI at
+the reference's shapes (N = 8, G = 2, D = 128, T = 512 keys per chunk), with the running max, sum
+and output kept in device buffers across the chunk launches, against the oracle after every chunk.
+
+Bars, stage by stage:
+  * max: bit-exact. The logits are exact (a serial f32 fold over D, an f32 division, one narrow) and
+    a max does not depend on its order.
+  * sum: relative 1e-5. The device exp is held to a tolerance, not bit parity (an ulp or two of
+    expf), and the f32 sum over 512 keys is regrouped for parallelism (buf.rs:316-330 leaves the order
+    of an f32 fold free); both are orders of magnitude inside 1e-5.
+  * out: bit-exact on at least 99.9% of the outputs and within 2 bf16 ulps everywhere. An ulp of exp
+    moves bf16(p) only when it crosses a rounding boundary of bf16 (about one key in 2^15), and
+    then one partial product by an ulp.
+and the normalised output passes the reference's own acceptance test (transformer.py:169-186)
+against the model's softmax attention.
+"""
+import numpy as np
+import pytest
+
+import decode_chain as dc
+from oracle import emulator as emu
+from test_oracle_decode import accepted
+
+pytestmark = pytest.mark.gpu
+
+
+def ulp(x):
+    """bf16 ulp of each value (the spacing at its exponent; 2^-133 below the normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def near(got_bits, want_bits):
+    g, w = emu.bf16_to_f32(got_bits).astype(np.float64), emu.bf16_to_f32(want_bits).astype(np.float64)
+    exact = np.mean(got_bits == want_bits)
+    worst = float(np.max(np.abs(g - w) / ulp(w)))
+    assert exact >= 0.999 and worst <= 2.0, (exact, worst)
+
+
+CASES = [
+    dict(seed=60, chunks=1, valid=6, uniform=True),  # transformer.py:245-256's own check
+    dict(seed=61, chunks=3, valid=300, scale=1.0),   # two full chunks, then the causal one
+    dict(seed=62, chunks=2, valid=512, scale=1.0),   # every key of the last chunk attended
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"chunks{c['chunks']}_valid{c['valid']}")
+def test_decode_chain_matches_the_oracle(rt, case):
+    q, ks, vs, masks = dc.inputs(case["seed"], case["chunks"], case["valid"], scale=case.get("scale", 1.0),
+                                 uniform=case.get("uniform", False))
+    print(f"decode chain seed {case['seed']} chunks {case['chunks']} valid {case['valid']}", flush=True)
+    got_stages, want_stages = [], []
+    _, _, _, y = dc.decode(dc.GpuOps(rt), q, ks, vs, masks, got_stages)
+    _, _, _, y_want = dc.decode(dc.CpuOps(), q, ks, vs, masks, want_stages)
+    for c, ((gm, gs, go), (wm, ws, wo)) in enumerate(zip(got_stages, want_stages)):
+        assert np.array_equal(gm.view(np.uint32), wm.view(np.uint32)), f"max after chunk {c}"
+        np.testing.assert_allclose(gs, ws, rtol=1e-5, err_msg=f"sum after chunk {c}")
+        near(go, wo)
+    near(y, y_want)
+    ok, rate = accepted(dc.softmax_attention(q, ks, vs, masks, bf16_logits=True), emu.bf16_to_f32(y))
+    assert ok and rate == 1.0, rate

@@ -170,7 +170,7 @@ def test_rmsnorm_softmax_config(rt):
 # ---- attention prefill ------------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 256, 128), (2, 1, 200, 64), (1, 1, 64, 128), (1, 3, 333, 128)])
+@pytest.mark.parametrize("shape", [(1, 2, 256, 128), (2, 1, 200, 64), (1, 1, 64, 128), (1, 3, 333, 128), (1, 2, 1000, 64)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_small(rt, shape, causal):
     b, h, s, d = shape
@@ -183,10 +183,14 @@ def test_attention_small(rt, shape, causal):
     rt.attention_prefill(out, rt.upload(q), rt.upload(k), rt.upload(v), b, h, s, d, float(sd), causal)
     got = emu.bf16_to_f32(out.read(np.uint16))
     cm = emu.bf16_to_f32(want_cm)
-    cm_bar = np.maximum(2 * bf16_ulp(cm), 1e-2 * np.abs(cm) + 1e-2 * np.sqrt(np.mean(cm.astype(np.float64) ** 2)))
-    close_chain(got, cm, hard=cm_bar, name=f"attention {shape} causal={causal} vs causal-max oracle")  # no exceptions
+    bound = attention_bound(q, k, v, b * h, s, d, sd, causal)
+    # The kernel's running max differs from the oracle's causal max by up to 8 ln 2 as well, so its
+    # bf16(p) round at another scale: attention_numpy's bound covers that for any choice of max.
+    cm_bar = np.maximum(bound, np.maximum(2 * bf16_ulp(cm), 1e-2 * np.abs(cm) +
+                                          1e-2 * np.sqrt(np.mean(cm.astype(np.float64) ** 2))))
+    close_chain(got, cm, frac_beyond=1e-3, hard=cm_bar, name=f"attention {shape} causal={causal} vs causal-max oracle")
     # Reference max before masking: bf16(p) rounds at another scale (attention_numpy's bound).
-    close_chain(got, emu.bf16_to_f32(want), frac_beyond=1e-3, hard=attention_bound(q, k, v, b * h, s, d, sd, causal),
+    close_chain(got, emu.bf16_to_f32(want), frac_beyond=1e-3, hard=bound,
                 name=f"attention {shape} causal={causal} vs oracle")
 
 

@@ -1,0 +1,101 @@
+"""The oracle's decode attention chain (decode_chain.py, attention.rs:226-392) pinned without the GPU.
+
+  * the whole chain against the model's softmax attention in float64, with the reference's own
+    acceptance test (transformer.py:169-186: |delta| <= max(0.01 |e|, 2^-8) on at least 99.5% of
+    the outputs) on its own inputs (transformer.py:245-256: one chunk, uniform [0, 1) samples, six
+    attended keys) and on sharper ones over three chunks (there with the logits rounded to bf16 in
+    the float64 restatement too, the one rounding of the chain that exceeds 1% at such logits);
+  * the stages' closed forms: the running max is the max over every key, the masked ones included
+    (attention.rs:77-95 takes it before masking_exp); the sum is the attended exp(x - max) plus EPS per
+    chunk, rescaled by alpha = exp(max - max'); masked keys contribute nothing to the output.
+  * a planted mistake (alpha taken as exp(max' - max)) that the acceptance test must reject.
+"""
+import numpy as np
+
+import decode_chain as dc
+from oracle import emulator as emu
+
+OPS = dc.CpuOps()
+
+
+def accepted(expected, actual):
+    """transformer.py:169-186's verdict, and the pass rate."""
+    e = np.asarray(expected, np.float64).reshape(-1)
+    a = np.asarray(actual, np.float64).reshape(-1)
+    rate = np.mean(np.abs(e - a) <= np.maximum(0.01 * np.abs(e), 2.0 ** -8))
+    return rate >= 0.995, rate
+
+
+def test_reference_attention_check_on_its_own_inputs():
+    q, ks, vs, masks = dc.inputs(50, 1, 6, uniform=True)  # transformer.py:252-256
+    _, _, _, y = dc.decode(OPS, q, ks, vs, masks)
+    ok, rate = accepted(dc.softmax_attention(q, ks, vs, masks), emu.bf16_to_f32(y))
+    assert ok and rate == 1.0, rate
+
+
+def test_three_chunks_against_softmax_attention_and_closed_forms():
+    q, ks, vs, masks = dc.inputs(51, 3, 300, scale=1.0)
+    stages = []
+    mx, sm, out, y = dc.decode(OPS, q, ks, vs, masks, stages)
+    ref = dc.softmax_attention(q, ks, vs, masks, bf16_logits=True)
+    ok, rate = accepted(ref, emu.bf16_to_f32(y))
+    assert ok and rate == 1.0, rate
+
+    # logits per chunk from the oracle's own qk stage, then the closed forms of the running state
+    logits = [emu.bf16_to_f32(dc.qk_scaled(OPS, OPS.put(q), OPS.put(k))).reshape(dc.N, dc.G, dc.T) for k in ks]
+    run_max = None
+    for c, (lg, (m_c, s_c, _)) in enumerate(zip(logits, stages)):
+        blk = lg.max(axis=-1)  # every key, the masked ones too
+        run_max = blk if run_max is None else np.maximum(run_max, blk)
+        assert np.array_equal(m_c.reshape(dc.N, dc.G), run_max.astype(np.float32))
+    # sum after the last chunk: sum_c (sum_t attended exp(x - m_c) + EPS) * exp(m_c - m_final)
+    want = np.zeros((dc.N, dc.G))
+    m_fin = stages[-1][0].reshape(dc.N, dc.G).astype(np.float64)
+    for c, lg in enumerate(logits):
+        m_c = stages[c][0].reshape(dc.N, dc.G).astype(np.float64)
+        e = np.exp(lg - m_c[..., None]) * masks[c][None, None, :]
+        want += (e.sum(axis=-1) + dc.EPS) * np.exp(m_c - m_fin)
+    np.testing.assert_allclose(sm.reshape(dc.N, dc.G), want, rtol=2e-5)
+
+
+def test_masked_keys_do_not_reach_the_output():
+    q, ks, vs, masks = dc.inputs(52, 1, 40, scale=2.0)
+    # the masked keys get the largest logits: they still set the max (before the mask) ...
+    k = emu.bf16_to_f32(ks[0]).reshape(dc.T, dc.N, dc.D)
+    qf = emu.bf16_to_f32(q).reshape(dc.N, dc.G, dc.D)
+    k[40:] = 3.0 * np.sign(qf[:, 0, :])[None, :, :]  # aligned with group 0 of every head
+    ks = [emu.f32_to_bf16(k.reshape(-1))]
+    mx, sm, out, y = dc.decode(OPS, q, ks, vs, masks)
+    lg = emu.bf16_to_f32(dc.qk_scaled(OPS, OPS.put(q), OPS.put(ks[0]))).reshape(dc.N, dc.G, dc.T)
+    assert np.array_equal(mx.reshape(dc.N, dc.G), lg.max(axis=-1))
+    assert np.any(lg[..., 40:].max(axis=-1) > lg[..., :40].max(axis=-1))
+    # ... and any V past key 40 leaves the output unchanged
+    v2 = emu.bf16_to_f32(vs[0]).reshape(dc.T, dc.N, dc.D).copy()
+    v2[40:] = 1000.0
+    _, _, out2, _ = dc.decode(OPS, q, ks, [emu.f32_to_bf16(v2.reshape(-1))], masks)
+    assert np.array_equal(out, out2)
+
+
+def test_planted_alpha_mistake_is_rejected():
+    q, ks, vs, masks = dc.inputs(53, 2, 200, scale=1.0)
+
+    def bad_forward(ops, q, k, v, mask, mx, sm, out):
+        qk = dc.qk_scaled(ops, q, k)
+        new = ops.zip(dc.row_max(ops, qk), mx, dc.F32, "CLIP_MAX")
+        alpha = ops.map(ops.zip(new, mx, dc.F32, "SUB_F"), dc.F32, dc.F32, "EXP")  # exp(max' - max): wrong
+        e = dc.masked_exp(ops, qk, new, mask)
+        sm = ops.zip(ops.zip(sm, alpha, dc.F32, "MUL_F"), dc.row_sum(ops, e), dc.F32, "CLIP_ADD")
+        result = ops.map(dc.weighted_sum(ops, e, v), dc.BF16, dc.F32, "CAST")
+        a = ops.relayout(alpha, dc.F32, "N, G", "N, G, D")
+        o = ops.map(ops.zip(ops.map(out, dc.BF16, dc.F32, "CAST"), a, dc.F32, "MUL_F"), dc.F32, dc.BF16, "CAST")
+        o = ops.zip(ops.map(o, dc.BF16, dc.F32, "CAST"), result, dc.F32, "CLIP_ADD")
+        return new, sm, ops.map(o, dc.F32, dc.BF16, "CAST")
+
+    good = dc.forward
+    try:
+        dc.forward = bad_forward
+        _, _, _, y = dc.decode(OPS, q, ks, vs, masks)
+    finally:
+        dc.forward = good
+    ok, _ = accepted(dc.softmax_attention(q, ks, vs, masks, bf16_logits=True), emu.bf16_to_f32(y))
+    assert not ok
