@@ -1,6 +1,7 @@
-"""The decode attention chain (attention.rs:226-392, stages in decode_chain.py) through the C ABI at
-the reference's shapes (N = 8, G = 2, D = 128, T = 512 keys per chunk), with the running max, sum
-and output kept in device buffers across the chunk launches, against the oracle after every chunk.
+"""The decode chains (attention.rs:226-392 and mlp.rs:9-150, stages in decode_chain.py) through the
+C ABI at the reference's shapes against the oracle. Attention runs at N = 8, G = 2, D = 128, T = 512
+keys per chunk, with the running max, sum and output kept in device buffers across the chunk
+launches and compared after every chunk.
 
 Bars, stage by stage:
   * max: bit-exact. The logits are exact (a serial f32 fold over D, an f32 division, one narrow) and
@@ -58,4 +59,22 @@ def test_decode_chain_matches_the_oracle(rt, case):
         near(go, wo)
     near(y, y_want)
     ok, rate = accepted(dc.softmax_attention(q, ks, vs, masks, bf16_logits=True), emu.bf16_to_f32(y))
+    assert ok and rate == 1.0, rate
+
+
+def test_mlp_matches_the_oracle(rt):
+    """mlp.rs:9-150 at H = 1024, L = 3072: up, gate and the f32 down sums bit-exact (serial folds of
+    the narrow sources); the device sigmoid (through expf) within ulps, so the product x and the
+    output carry the exp bar above."""
+    x, up_w, gate_w, down_w = dc.mlp_inputs(72)
+    print("mlp chain seed 72", flush=True)
+    got, want = {}, {}
+    y = dc.mlp(dc.GpuOps(rt, dc.MLP_SIZES), x, up_w, gate_w, down_w, got)
+    y_want = dc.mlp(dc.CpuOps(dc.MLP_SIZES), x, up_w, gate_w, down_w, want)
+    assert np.array_equal(got["up"], want["up"]) and np.array_equal(got["gate"], want["gate"])
+    near(got["x"], want["x"])
+    if np.array_equal(got["x"], want["x"]):
+        assert np.array_equal(got["down"].view(np.uint32), want["down"].view(np.uint32))
+    near(y, y_want)
+    ok, rate = accepted(dc.mlp_float(x, up_w, gate_w, down_w), emu.bf16_to_f32(y))
     assert ok and rate == 1.0, rate

@@ -1,4 +1,4 @@
-"""The oracle's decode attention chain (decode_chain.py, attention.rs:226-392) pinned without the GPU.
+"""The oracle's decode chains (decode_chain.py: attention.rs:226-392, mlp.rs:9-150) pinned on the CPU.
 
   * the whole chain against the model's softmax attention in float64, with the reference's own
     acceptance test (transformer.py:169-186: |delta| <= max(0.01 |e|, 2^-8) on at least 99.5% of
@@ -98,4 +98,45 @@ def test_planted_alpha_mistake_is_rejected():
     finally:
         dc.forward = good
     ok, _ = accepted(dc.softmax_attention(q, ks, vs, masks, bf16_logits=True), emu.bf16_to_f32(y))
+    assert not ok
+
+
+# ---- SiLU MLP (mlp.rs:9-150) ---------------------------------------------------------------------------
+
+MLP_OPS = dc.CpuOps(dc.MLP_SIZES)
+
+
+def test_mlp_against_float_and_closed_forms():
+    x, up_w, gate_w, down_w = dc.mlp_inputs(70)
+    st = {}
+    y = dc.mlp(MLP_OPS, x, up_w, gate_w, down_w, st)
+    ok, rate = accepted(dc.mlp_float(x, up_w, gate_w, down_w), emu.bf16_to_f32(y))
+    assert ok and rate == 1.0, rate
+    # up and gate: one bf16 narrow of each dot product (float64 dots differ from the serial f32 fold
+    # by far less than the half ulp that could move the narrow, except at a rounding tie)
+    f = lambda t, *shape: emu.bf16_to_f32(t).astype(np.float64).reshape(*shape)
+    for name, w in (("up", up_w), ("gate", gate_w)):
+        want = emu.f32_to_bf16((f(w, dc.L, dc.H) @ f(x, dc.H)).astype(np.float32))
+        assert np.mean(st[name] == want) > 0.999
+    # the f32 down sums are the serial fold of the narrowed product
+    h = f(st["x"], dc.L)
+    np.testing.assert_allclose(st["down"], f(down_w, dc.H, dc.L) @ h, rtol=1e-4, atol=1e-5)
+
+
+def test_planted_silu_mistake_is_rejected():
+    x, up_w, gate_w, down_w = dc.mlp_inputs(71)
+    real = MLP_OPS.zip
+
+    def zip_sigmoid_only(a, b, t, name, flags=0):  # silu = sigmoid(g) instead of sigmoid(g) * g
+        if name == "MUL_F" and zip_sigmoid_only.first:
+            zip_sigmoid_only.first = False
+            return a
+        return real(a, b, t, name, flags)
+    zip_sigmoid_only.first = True
+    MLP_OPS.zip = zip_sigmoid_only
+    try:
+        y = dc.mlp(MLP_OPS, x, up_w, gate_w, down_w)
+    finally:
+        del MLP_OPS.zip
+    ok, _ = accepted(dc.mlp_float(x, up_w, gate_w, down_w), emu.bf16_to_f32(y))
     assert not ok
