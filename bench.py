@@ -381,28 +381,29 @@ def cpu_baselines():
     M = N = K = 4096
     a = f32_to_bf16(rng.standard_normal(M * K, dtype=np.float32))
     b = f32_to_bf16(rng.standard_normal(N * K, dtype=np.float32))
-    rows = 16
+    rows = 128
     record("mapped_gemm_4096", lambda: emu.gemm_rows(a, b, M, N, K, 0, rows), 2.0 * rows * N * K, "TFLOP/s",
            f"{rows} of 4096 output rows of the 4096^3 bf16 contraction")
     R, Cc = 8192, 4096
-    x = f32_to_bf16(rng.standard_normal(256 * Cc, dtype=np.float32))
+    x = f32_to_bf16(rng.standard_normal(R * Cc, dtype=np.float32))
     g = f32_to_bf16(1.0 + 0.1 * rng.standard_normal(Cc, dtype=np.float32))
-    record("rmsnorm_softmax_8192x4096", lambda: emu.rmsnorm_softmax(x, g, 256, Cc, 1e-6), 2 * 256 * Cc * 2 + Cc * 2,
-           "GB/s", "256 of 8192 rows")
+    record("rmsnorm_softmax_8192x4096", lambda: emu.rmsnorm_softmax(x, g, R, Cc, 1e-6), 2 * R * Cc * 2 + Cc * 2,
+           "GB/s", "all 8192 rows")
     B, H, S, D = 4, 32, 2048, 128
-    hq = 2
+    hq = 8
     q, k, v = (f32_to_bf16(rng.standard_normal(hq * S * D, dtype=np.float32)) for _ in range(3))
-    q0, q1 = S - 64, S
+    q0, q1 = S - 256, S
     flop = 4.0 * hq * D * sum(i + 1 for i in range(q0, q1))
     record("attention_prefill_b4h32s2048d128",
            lambda: emu.attention_prefill(q, k, v, hq, S, D, 11.313708, True, q0, q1), flop, "TFLOP/s",
-           f"the last 64 queries (each over 1985-2048 keys) of {hq} of 128 heads")
+           f"the last 256 queries (each over 1793-2048 keys) of {hq} of 128 heads")
     Mw, Nw, Kw = 2048, 8192, 8192
-    aw = rng.integers(-127, 128, 2 * Kw, dtype=np.int8)
+    rw = 512
+    aw = rng.integers(-127, 128, rw * Kw, dtype=np.int8)
     ww = rng.integers(-127, 128, Nw * Kw, dtype=np.int8)
     sc = rng.uniform(1e-3, 1e-2, Nw).astype(np.float32)
-    record("w8a8_2048x8192x8192", lambda: emu.w8a8(aw, ww, sc, 2, Nw, Kw), 2.0 * 2 * Nw * Kw, "TOP/s",
-           "2 of 2048 output rows")
+    record("w8a8_2048x8192x8192", lambda: emu.w8a8(aw, ww, sc, rw, Nw, Kw), 2.0 * rw * Nw * Kw, "TOP/s",
+           f"{rw} of 2048 output rows")
     Bm, I, Hd, O = 64, 784, 128, 10
     xm = f32_to_bf16(rng.uniform(0, 1, Bm * I).astype(np.float32))
     w1 = f32_to_bf16(0.05 * rng.standard_normal(Hd * I, dtype=np.float32))
