@@ -86,7 +86,9 @@ int32_t fo_runtime_device_info(fo_runtime* rt, int32_t* compute_units, char* arc
  * runtime's stream must be synchronized with its own runtime first. */
 int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out);
 void fo_buffer_free(fo_buffer* buf);
-/* Device-to-device copy into a new buffer (Storage: Clone). */
+/* Device-to-device copy into a new buffer (Storage: Clone). Also Backend::reshape (backend/mod.rs:
+ * 208-219; BufStorage::reshape, storage/buf.rs:580-585): the same wire image relabelled, once the
+ * caller has checked that both mappings have the same size. */
 int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out);
 uint64_t fo_buffer_bytes(const fo_buffer* buf);
 /* Host -> device (Backend::to_hbm, backend/mod.rs:236-239; NPU: furiosa_write, device_runtime.h). */
