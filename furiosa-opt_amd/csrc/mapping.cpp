@@ -44,12 +44,26 @@ void check_ident(const std::string& s) {
 // ---------------------------------------------------------------------------------------------
 
 namespace {
+// Largest size, stride, modulo, resize, padding or wire size of a mapping (2^48 elements, far beyond
+// any storage). Bounding every count and the total where a mapping enters keeps every weight,
+// period and stride the resolver derives from them (each at most a symbol's size or the wire size)
+// inside int64.
+constexpr int64_t kMaxExtent = int64_t(1) << 48;
+
 // Every size, stride, modulo, resize and padding of a mapping is a positive count; a zero would
 // divide by zero in Mapping::size and the resolver, so it is rejected where the JSON is read.
 int64_t positive(const json::Value& b, const char* key) {
   int64_t n = b.at(key).as_int();
   if (n <= 0) throw Error(std::string("mapping: '") + key + "' must be positive, got " + std::to_string(n));
+  if (n > kMaxExtent) throw Error(std::string("mapping: '") + key + "' exceeds 2^48, got " + std::to_string(n));
   return n;
+}
+
+// a * b for two counts in [0, 2^48], rejecting a product above 2^48.
+int64_t mul_extent(int64_t a, int64_t b) {
+  int64_t r;
+  if (__builtin_mul_overflow(a, b, &r) || r > kMaxExtent) throw Error("mapping: size exceeds 2^48 elements");
+  return r;
 }
 }  // namespace
 
@@ -78,7 +92,11 @@ NodeP from_json(const json::Value& v) {
   throw Error("mapping: unknown node '" + tag + "'");
 }
 
-NodeP parse_json(const std::string& text) { return from_json(json::parse(text)); }
+NodeP parse_json(const std::string& text) {
+  NodeP m = from_json(json::parse(text));
+  (void)size(m);  // rejects a wire size above 2^48 before any resolution step
+  return m;
+}
 
 std::string to_json(const NodeP& m) {
   std::ostringstream o;
@@ -208,10 +226,13 @@ struct TextParser {
 }  // namespace
 
 NodeP parse_text(const std::string& text, const std::map<std::string, int64_t>& sizes) {
+  for (const auto& [name, n] : sizes)
+    if (n <= 0 || n > kMaxExtent) throw Error("mapping: axis '" + name + "' size must lie in [1, 2^48]");
   TextParser tp{text, sizes};
   NodeP n = tp.m0();
   tp.ws();
   if (tp.p != text.size()) tp.fail("trailing characters");
+  (void)size(n);
   return n;
 }
 
@@ -228,7 +249,7 @@ int64_t size(const NodeP& m) {
     case Node::Broadcast:
       return m->n;
     case Node::Pair:
-      return size(m->a) * size(m->b);
+      return mul_extent(size(m->a), size(m->b));
   }
   return 0;
 }
@@ -268,7 +289,7 @@ namespace {
 
 int64_t prod_extent(const Factors& f, size_t from = 0) {
   int64_t p = 1;
-  for (size_t i = from; i < f.size(); ++i) p *= f[i].extent;
+  for (size_t i = from; i < f.size(); ++i) p = mul_extent(p, f[i].extent);
   return p;
 }
 

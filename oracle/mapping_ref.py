@@ -28,7 +28,7 @@ What it restates, and from where (paths relative to the reference repository roo
 * `carve(self, piece)` -- `MappingExt::carve` (`furiosa-mapping/src/lib.rs:154-167`) restated on
   coordinates: the self factors that `piece` backs become `Top` pads.
 
-Where this module is pinned (see tests/test_oracle_mapping.py): the doc examples of
+Where this module is pinned (see tests/test_oracle_golden.py): the doc examples of
 `mapping-expressions.md` (e.g. `m![B / 64, B % 32, B / 32 % 2]`: position 67 maps to `B = 97`),
 the `m![C, D # 64]` padding table, the `pseudo.rs:92-151` stream vectors, the transpose and
 reduce vectors of `furiosa-opt-std/src/tensor/mod.rs:359-549`, and the sequencer stride tables of

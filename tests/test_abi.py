@@ -57,3 +57,18 @@ def test_zero_counts_in_mappings_are_rejected():
         fh.m("A / 0", A=4)
     with pytest.raises(fh.FoError, match="must be positive"):
         fh.m("A % 0", A=4)
+
+
+def test_oversized_mappings_are_rejected():
+    # counts and wire sizes above 2^48 would overflow the resolver's int64 weights and strides
+    # (found by the sanitizer harness): refused where the mapping enters
+    huge = '{"Symbol":{"symbol":"A","size":%d}}' % (2 ** 49)
+    with pytest.raises(fh.FoError, match="exceeds 2"):
+        fh.sequence(huge, fh.m("A", A=4))
+    pair = ('{"Pair":{"left":{"Symbol":{"symbol":"A","size":%d}},"right":{"Symbol":{"symbol":"B","size":%d}}}}'
+            % (2 ** 30, 2 ** 30))
+    with pytest.raises(fh.FoError, match="exceeds 2"):
+        fh.sequence(pair, fh.m("A", A=4))
+    with pytest.raises(fh.FoError, match="2\\^48"):
+        fh.m("A, B", A=2 ** 30, B=2 ** 30)
+    assert fh.sequence(fh.m("A, B", A=2 ** 24, B=2 ** 24), fh.m("A, B", A=2 ** 24, B=2 ** 24))  # 2^48 itself is fine
