@@ -1030,8 +1030,14 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     set_device(rt);
     TraceScope trace_span(rt, "reduce");
     const int mem[1] = {0};
-    launch_reduce(rt->stream, dst->ptr, src->ptr, t, (int64_t)(src->bytes / eb), out_count, to_desc<1>(ow, mem),
-                  to_desc<1>(rw, mem), op, identity);
+    const Wheels<1> owd = to_desc<1>(ow, mem), rwd = to_desc<1>(rw, mem);
+    const int64_t src_len = (int64_t)(src->bytes / eb);
+    const ReduceSplit split = plan_reduce_split(t, op, src->ptr, src_len, out_count, owd, rwd);
+    if (split.nchunks > 0)
+      launch_reduce_split(rt->stream, dst->ptr, src->ptr, t, out_count, owd, rwd, op, identity, split,
+                          runtime_scratch(rt, split.scratch_bytes));
+    else
+      launch_reduce(rt->stream, dst->ptr, src->ptr, t, src_len, out_count, owd, rwd, op, identity);
   });
 }
 

@@ -959,6 +959,107 @@ __global__ void __launch_bounds__(64 * kSeg) k_reduce_cols(void* dst, const void
   }
 }
 
+// The same fold for contiguous output cells split over many residue chunks (two passes): pass one
+// folds chunk c of the residue for 256 cells per block -- each lane four adjacent cells through
+// 16-byte loads, so a wave reads 1 KiB per residue step, the block's four waves splitting the chunk
+// and combining in wave order -- into partials[c][cell]; pass two folds each cell's partials in
+// chunk order, from the caller's identity. 4-byte folds that may be regrouped only (f32, and the
+// integer ops except the saturating add); the host checks the layout (cells in whole groups of
+// four, 16-byte aligned offsets, every read inside the source).
+template <typename Tag>
+struct Vec4T;
+template <>
+struct Vec4T<float> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct Vec4T<int32_t> {
+  typedef int type __attribute__((ext_vector_type(4)));
+};
+
+template <typename Tag>
+__global__ void __launch_bounds__(256) k_reduce_cols4(void* __restrict__ partials, const void* __restrict__ src,
+                                                      uint32_t groups, uint32_t out_count, Wheels<1> ow, Wheels<1> rw,
+                                                      int op, uint32_t neutral, uint32_t total, uint32_t chunk_len) {
+  using R = RedT<Tag>;
+  using V4 = typename Vec4T<Tag>::type;
+  __shared__ V4 part[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t g = blockIdx.x * 64 + lane;
+  int64_t b[1];
+  const bool dead = cell_base(ow, 4 * g, out_count, b);  // g >= groups reads as dead
+  const Tag z = R::from_bits(neutral);
+  V4 acc = {z, z, z, z};
+  const uint32_t c0 = blockIdx.y * chunk_len, c1 = min(total, c0 + chunk_len);
+  const uint32_t wlen = (chunk_len + 3) / 4;
+  const uint32_t r_begin = min(c1, c0 + wave * wlen), r_end = min(c1, r_begin + wlen);
+  if (!dead && r_begin < r_end) {
+    uint32_t digit[kMaxWheels] = {};
+    int64_t off[1] = {b[0]};
+    uint32_t q = r_begin;
+    for (int i = 0; i < rw.n; ++i) {
+      const uint32_t nq = rw.div[i].div(q);
+      digit[i] = q - nq * rw.size[i];
+      off[0] += (int64_t)digit[i] * rw.stride[0][i];
+      q = nq;
+    }
+    const V4* s4 = (const V4*)src;
+    uint32_t r = r_begin;
+    for (; r + 8 <= r_end; r += 8) {
+      V4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        v[u] = __builtin_nontemporal_load(s4 + (off[0] >> 2));
+        odometer_step(rw, digit, off);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = R::apply(op, acc[e], v[u][e]);
+    }
+    for (; r < r_end; ++r) {
+      const V4 v = __builtin_nontemporal_load(s4 + (off[0] >> 2));
+      odometer_step(rw, digit, off);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = R::apply(op, acc[e], v[e]);
+    }
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && g < groups) {
+    V4 t = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; ++w)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = R::apply(op, t[e], part[w][lane][e]);
+    ((V4*)partials)[(int64_t)blockIdx.y * groups + g] = t;
+  }
+}
+
+template <typename Tag>
+__global__ void __launch_bounds__(kBlock) k_reduce_cols4_fold(void* dst, const void* __restrict__ partials,
+                                                              uint32_t out_count, uint32_t nchunks, Wheels<1> ow, int op,
+                                                              uint32_t identity) {
+  using R = RedT<Tag>;
+  const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
+  if (o >= out_count) return;
+  int64_t b[1];
+  const bool dead = cell_base(ow, o, out_count, b);
+  auto acc = R::from_bits(identity);
+  if (!dead) {
+    uint32_t c = 0;
+    for (; c + 8 <= nchunks; c += 8) {  // eight loads in flight, folded in chunk order
+      decltype(R::load(partials, 0)) v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = R::load(partials, (int64_t)(c + u) * out_count + o);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = R::apply(op, acc, v[u]);
+    }
+    for (; c < nchunks; ++c) acc = R::apply(op, acc, R::load(partials, (int64_t)c * out_count + o));
+  }
+  R::store(dst, o, acc);
+}
+
 template <typename Tag>
 void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_t out_count, const Wheels<1>& ow,
               const Wheels<1>& rw, int op, uint32_t identity) {
@@ -1011,6 +1112,74 @@ void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_
 }
 
 }  // namespace
+
+namespace {
+constexpr int64_t kColsTargetBlocks = 2048;
+
+// The op's neutral element as bits (f32 or i32).
+uint32_t red_neutral(bool f32, int op) {
+  switch (op) {
+    case FO_RED_ADD:
+      return f32 ? 0x80000000u : 0u;
+    case FO_RED_MAX:
+      return f32 ? 0xff800000u : 0x80000000u;
+    case FO_RED_MIN:
+      return f32 ? 0x7f800000u : 0x7fffffffu;
+    default:
+      return f32 ? 0x3f800000u : 1u;
+  }
+}
+}  // namespace
+
+ReduceSplit plan_reduce_split(fo_dtype t, int op, const void* src, int64_t src_len, int64_t out_count,
+                              const Wheels<1>& ow, const Wheels<1>& rw) {
+  ReduceSplit p;
+  if (!(t == FO_F32 || (t == FO_I32 && op != FO_RED_ADD_SAT))) return p;
+  if (ow.n < 1 || rw.n < 1 || ow.stride[0][0] != 1 || ow.size[0] % 4 != 0 || ow.live[0] != ow.size[0]) return p;
+  if (rw.stride[0][0] == 1 && out_count <= (1 << 20)) return p;  // a contiguous residue: the wave form
+  if ((uintptr_t)src % 16 != 0) return p;
+  int64_t total = 1, max_off = 0;
+  for (int i = 0; i < ow.n; ++i) {
+    if (i > 0 && ow.stride[0][i] % 4 != 0) return p;
+    if (ow.live[i] > 0) max_off += (int64_t)(ow.live[i] - 1) * ow.stride[0][i];  // dead cells are never read
+  }
+  for (int i = 0; i < rw.n; ++i) {
+    if (rw.stride[0][i] % 4 != 0 || rw.stride[0][i] < 0) return p;
+    max_off += (int64_t)(rw.size[i] - 1) * rw.stride[0][i];
+    total *= rw.size[i];
+  }
+  if (total < 64 || total >= (1ll << 31) || max_off >= src_len || out_count % 4 != 0) return p;
+  const int64_t groups = out_count / 4, tiles = (groups + 63) / 64;
+  int64_t nchunks = (kColsTargetBlocks + tiles - 1) / tiles;
+  nchunks = std::max<int64_t>(1, std::min<int64_t>({nchunks, (total + 255) / 256, 65535}));
+  p.nchunks = nchunks;
+  p.chunk_len = (total + nchunks - 1) / nchunks;
+  p.nchunks = (total + p.chunk_len - 1) / p.chunk_len;
+  p.scratch_bytes = (uint64_t)p.nchunks * out_count * 4;
+  return p;
+}
+
+void launch_reduce_split(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t out_count, const Wheels<1>& ow,
+                         const Wheels<1>& rw, int op, uint32_t identity, const ReduceSplit& p, void* scratch) {
+  int64_t total = 1;
+  for (int i = 0; i < rw.n; ++i) total *= rw.size[i];
+  const uint32_t groups = (uint32_t)(out_count / 4);
+  const dim3 grid((groups + 63) / 64, (unsigned)p.nchunks);
+  const unsigned fold_blocks = (unsigned)((out_count + kBlock - 1) / kBlock);
+  const bool f32 = t == FO_F32;
+  if (f32) {
+    hipLaunchKernelGGL(k_reduce_cols4<float>, grid, dim3(256), 0, s, scratch, src, groups, (uint32_t)out_count, ow, rw,
+                       op, red_neutral(true, op), (uint32_t)total, (uint32_t)p.chunk_len);
+    hipLaunchKernelGGL(k_reduce_cols4_fold<float>, dim3(fold_blocks), dim3(kBlock), 0, s, dst, scratch,
+                       (uint32_t)out_count, (uint32_t)p.nchunks, ow, op, identity);
+  } else {
+    hipLaunchKernelGGL(k_reduce_cols4<int32_t>, grid, dim3(256), 0, s, scratch, src, groups, (uint32_t)out_count, ow,
+                       rw, op, red_neutral(false, op), (uint32_t)total, (uint32_t)p.chunk_len);
+    hipLaunchKernelGGL(k_reduce_cols4_fold<int32_t>, dim3(fold_blocks), dim3(kBlock), 0, s, dst, scratch,
+                       (uint32_t)out_count, (uint32_t)p.nchunks, ow, op, identity);
+  }
+  FO_HIP(hipGetLastError());
+}
 
 void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,
                    const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity) {

@@ -188,6 +188,18 @@ void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t,
 void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,
                    const Wheels<1>& out_w, const Wheels<1>& res_w, int op, uint32_t identity);
 
+// A reduce whose output cells are contiguous, split over residue chunks with partials in scratch
+// (4-byte regroupable folds only). nchunks == 0: the layout does not qualify.
+struct ReduceSplit {
+  int64_t nchunks = 0, chunk_len = 0;
+  uint64_t scratch_bytes = 0;
+};
+ReduceSplit plan_reduce_split(fo_dtype t, int op, const void* src, int64_t src_len, int64_t out_count,
+                              const Wheels<1>& out_w, const Wheels<1>& res_w);
+void launch_reduce_split(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t out_count,
+                         const Wheels<1>& out_w, const Wheels<1>& res_w, int op, uint32_t identity,
+                         const ReduceSplit& plan, void* scratch);
+
 // Generic contraction: out wheels / residue wheels with strides into (lhs, rhs).
 void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t,
                                 fo_dtype out_t, int64_t lhs_len, int64_t rhs_len, int64_t out_count,

@@ -511,6 +511,60 @@ def test_reduce_wave_identity(rt, case):
         assert np.array_equal(got[:8], src.reshape(8, -1).sum(1) + 5) and np.all(got[8:] == 5)
 
 
+# Contiguous output cells over a long strided residue (column folds) run in two passes: residue
+# chunks fold into partials, then each cell folds its partials in chunk order from the identity.
+# Cases: non-neutral identities (entering once), -0 sums, an outer out wheel, padded outer cells
+# (dead: the identity), a residue that does not split evenly, and layouts outside the two-pass form
+# (cells not in whole groups of four, the saturating add).
+COLS = [
+    ("R, C", "C", dict(R=300, C=1024)),
+    ("A, R, C", "A, C", dict(A=3, R=100, C=64)),
+    ("A, R, C", "A # 4, C", dict(A=3, R=100, C=64)),
+    ("R, C", "C", dict(R=4099, C=8)),
+    ("R, C", "C", dict(R=300, C=6)),
+]
+
+
+@pytest.mark.parametrize("layout", COLS, ids=[f"{c[0]} -> {c[1]} {c[2]}" for c in COLS])
+@pytest.mark.parametrize("case", ["add_id5", "max_id", "min_id", "mul_id", "add_sat", "f32_add", "f32_max_id",
+                                  "f32_add_negzero"])
+def test_reduce_cols_split(rt, layout, case):
+    s_t, d_t, sizes = layout
+    so, do = mr.parse(s_t, sizes), mr.parse(d_t, sizes)
+    n, n_out = mr.size(so), mr.size(do)
+    rng = np.random.default_rng(29)
+    t = I32
+    if case == "add_id5":
+        src, op, ident = rng.integers(-1000, 1000, n).astype(np.int32), "ADD", 5
+    elif case == "max_id":
+        src, op, ident = rng.integers(-1000, 1000, n).astype(np.int32), "MAX", 990
+    elif case == "min_id":
+        src, op, ident = rng.integers(-1000, 1000, n).astype(np.int32), "MIN", -5
+    elif case == "mul_id":
+        src = np.where(rng.random(n) < 0.99, 1, rng.choice([-1, 3], n)).astype(np.int32)
+        op, ident = "MUL", 7
+    elif case == "add_sat":
+        src, op, ident = rng.choice([2 ** 30, -(2 ** 30), 1], n).astype(np.int32), "ADD_SAT", 0
+    elif case == "f32_add":
+        t = F32
+        src, op, ident = rng.standard_normal(n).astype(np.float32), "ADD", fh.f32_bits(0.25)
+    elif case == "f32_max_id":
+        t = F32
+        src, op, ident = rng.standard_normal(n).astype(np.float32), "MAX", fh.f32_bits(3.5)
+    else:
+        t = F32
+        src, op, ident = np.full(n, -0.0, np.float32), "ADD", fh.f32_bits(-0.0)
+    ident &= 0xFFFFFFFF
+    want = emu.reduce(src, t, so, do, fh.RED[op], ident)
+    out = rt.upload(np.full(n_out, 0x5A5A5A5A, np.uint32))  # garbage: every cell, dead ones too, is written
+    rt.reduce(out, rt.upload(src), t, fh.m(s_t, **sizes), fh.m(d_t, **sizes), fh.RED[op], ident)
+    got = out.read(t)
+    if case == "f32_add":  # a regrouped f32 sum
+        close(got, want, rel=1e-4)
+    else:  # integers exact in any order (the saturating add keeps its serial fold), MAX order-free
+        assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
 def test_reduce_rejects_unrequested_broadcast(rt):
     s = dict(A=4, B=2)
     with pytest.raises(fh.FoError, match="allow_broadcast"):
