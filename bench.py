@@ -311,6 +311,44 @@ def bench_mlp(fh, rt, steps, warmup, rng):
     return dict(ms=ev, wall_ms=wall, us=ev * 1e3, flop=2.0 * B * (I * Hd + Hd * O))
 
 
+def bench_decode(fh, rt, steps, warmup, rng):
+    """The transformer's decode chains as an unchanged kernel issues them through the seam ops
+    (furiosa_hip/decode.py): attention over four 512-key chunks of a resident KV cache (forward_first,
+    three forward, norm) and the SiLU MLP, one query token each. Wall time per token, host-side
+    mapping resolution and launches included, and the GPU time of the same calls."""
+    import furiosa_hip.decode as fd
+
+    ops = fd.SeamOps(rt)
+    nd = fd.N * fd.G * fd.D
+    q = rt.upload(f32_to_bf16(rng.standard_normal(nd, dtype=np.float32)))
+    ks = [rt.upload(f32_to_bf16(rng.standard_normal(fd.T * fd.N * fd.D, dtype=np.float32))) for _ in range(4)]
+    vs = [rt.upload(f32_to_bf16(rng.standard_normal(fd.T * fd.N * fd.D, dtype=np.float32))) for _ in range(4)]
+    masks = [rt.upload(np.ones(fd.T, np.float32)) for _ in range(3)]
+    last = np.ones(fd.T, np.float32)
+    last[300:] = 0.0
+    masks.append(rt.upload(last))
+
+    def attention():
+        mx, sm, out = fd.forward_first(ops, q, ks[0], vs[0], masks[0])
+        for c in range(1, 4):
+            mx, sm, out = fd.forward(ops, q, ks[c], vs[c], masks[c], mx, sm, out)
+        return fd.norm(ops, out, sm)
+
+    mops = fd.SeamOps(rt, fd.MLP_SIZES)
+    x = rt.upload(f32_to_bf16(rng.standard_normal(fd.H, dtype=np.float32)))
+    wu, wg = (rt.upload(f32_to_bf16(rng.standard_normal(fd.L * fd.H, dtype=np.float32) / 32)) for _ in range(2))
+    wd = rt.upload(f32_to_bf16(rng.standard_normal(fd.H * fd.L, dtype=np.float32) / 55))
+    mlp = lambda: fd.mlp(mops, x, wu, wg, wd)
+    n = max(5, steps // 10)
+    aw, ae = timed(rt, attention, n, max(2, warmup // 10))
+    a_calls = ops.calls
+    mw, me = timed(rt, mlp, n, max(2, warmup // 10))
+    m_calls = mops.calls
+    per = lambda calls: calls / (n + max(2, warmup // 10))
+    return dict(attention_4x512_keys=dict(wall_us=aw * 1e3, gpu_us=ae * 1e3, keys=4 * fd.T, seam_calls=per(a_calls)),
+                mlp_silu_h1024_l3072=dict(wall_us=mw * 1e3, gpu_us=me * 1e3, seam_calls=per(m_calls)))
+
+
 def cpu_baseline_gemm(target_s: float = 30.0):
     """The oracle's contraction_in fold (oracle/fo_cpu.c) on a bounded row sample of the same GEMM."""
     from oracle import emulator as emu
@@ -447,7 +485,8 @@ def main():
     for name, fnb in (("gemm", bench_gemm), ("gemm_f8", bench_gemm_f8), ("norm", bench_norm),
                       ("attention", bench_attention), ("chain", bench_chain),
                       ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("relayout", bench_relayout),
-                      ("scatter_gather", bench_scatter_gather), ("vector", bench_vector)):
+                      ("scatter_gather", bench_scatter_gather), ("vector", bench_vector),
+                      ("decode", bench_decode)):
         if only and name not in only:
             continue
         res[name] = fnb(fh, rt, args.steps, args.warmup, rng)
@@ -480,6 +519,9 @@ def main():
             configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
     for k, r in res.get("vector", {}).items():
         configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
+    for k, r in res.get("decode", {}).items():  # latency per token through the seam ops
+        configs[f"decode_seam_{k}"] = dict(value=r["wall_us"], unit="us", gpu_us=r["gpu_us"],
+                                           seam_calls=r["seam_calls"], us_per_call=r["wall_us"] / r["seam_calls"])
     for group in ("relayout", "chain"):
         for k, r in res.get(group, {}).items():
             name = "switch_broadcast_256x512x64_x4_bf16" if k == "switch_broadcast" else f"relayout_{k}_8192x8192_bf16"

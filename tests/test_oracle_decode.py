@@ -91,12 +91,12 @@ def test_planted_alpha_mistake_is_rejected():
         o = ops.zip(ops.map(o, dc.BF16, dc.F32, "CAST"), result, dc.F32, "CLIP_ADD")
         return new, sm, ops.map(o, dc.F32, dc.BF16, "CAST")
 
-    good = dc.forward
+    good = dc.fd.forward  # decode() calls the module's forward
     try:
-        dc.forward = bad_forward
+        dc.fd.forward = bad_forward
         _, _, _, y = dc.decode(OPS, q, ks, vs, masks)
     finally:
-        dc.forward = good
+        dc.fd.forward = good
     ok, _ = accepted(dc.softmax_attention(q, ks, vs, masks, bf16_logits=True), emu.bf16_to_f32(y))
     assert not ok
 
