@@ -37,6 +37,9 @@ N, G, D, T = 8, 2, 128, 512
 SIZES = dict(N=N, G=G, D=D, T=T)
 H, L = 1024, 3072  # axes.rs: hidden and MLP widths
 MLP_SIZES = dict(H=H, L=L)
+# RMSNorm of one token: the hidden state [H] (X, a unit row axis), q [N, G, D] and k [N, D]
+RMS_SIZES = dict(N=N, G=G, D=D, H=H, X=1)
+RMS_EPS = 6.25e-8  # rmsnorm.rs:28 (and :104, :159)
 SQRT_HEAD_DIM = 11.313708  # attention.rs:10
 EPS = 6.25e-8              # attention.rs:13
 NEG_INF_BITS = 0xFF800000
@@ -218,3 +221,19 @@ def mlp(ops, x, up_w, gate_w, down_w, stages=None):
     if stages is not None:
         stages.update(up=ops.get(up, BF16), gate=ops.get(gate, BF16), x=ops.get(h, BF16), down=ops.get(down, F32))
     return ops.get(ops.map(down, F32, BF16, "CAST"), BF16)
+
+
+def rmsnorm(ops, x, w, rows, axis, n):
+    """rmsnorm.rs `forward` (:9-78), `forward_q` (:80-150) and `forward_k` (:152-...): over the view
+    `rows, axis` of x (bf16 bits), with a gain w over `axis`, n = the axis length:
+    ms = sum_axis f32(x)^2 / n + EPS; rms = sqrt(ms); y = bf16(f32(x) * f32(w) / rms).
+    Returns (rms, y)."""
+    full = f"{rows}, {axis}"
+    xf = ops.map(ops.put(x), BF16, F32, "CAST")
+    ss = ops.reduce(ops.zip(xf, xf, F32, "MUL_F"), F32, full, rows, "ADD", 0)
+    ms = ops.map(ops.map(ss, F32, F32, "DIV_F", RHS_IMM, float(n)), F32, F32, "CLIP_ADD", RHS_IMM,
+                 float(np.float32(RMS_EPS)))
+    rms = ops.map(ms, F32, F32, "SQRT")
+    wf = ops.relayout(ops.map(ops.put(w), BF16, F32, "CAST"), F32, axis, full)
+    y = ops.zip(ops.zip(xf, wf, F32, "MUL_F"), ops.relayout(rms, F32, rows, full), F32, "DIV_F")
+    return rms, ops.map(y, F32, BF16, "CAST")

@@ -7,15 +7,21 @@ import numpy as np
 
 import furiosa_hip as fh
 import furiosa_hip.decode as fd
-from furiosa_hip.decode import (BF16, D, EPS, F32, G, H, L, MLP_SIZES, N, SIZES, T, decode, forward, forward_first,
-                                masked_exp, mlp, norm, qk_scaled, row_max, row_sum, weighted_sum)
+from furiosa_hip.decode import (BF16, D, EPS, F32, G, H, L, MLP_SIZES, N, RMS_EPS, RMS_SIZES, SIZES, T, decode, forward,
+                                forward_first, masked_exp, mlp, norm, qk_scaled, rmsnorm, row_max, row_sum,
+                                weighted_sum)
 from oracle import emulator as emu
 from oracle import mapping_ref as mr
 
 GpuOps = fd.SeamOps
 
-__all__ = ["BF16", "D", "EPS", "F32", "G", "H", "L", "MLP_SIZES", "N", "SIZES", "T", "decode", "forward",
-           "forward_first", "masked_exp", "mlp", "norm", "qk_scaled", "row_max", "row_sum", "weighted_sum"]
+__all__ = ["BF16", "D", "EPS", "F32", "G", "H", "L", "MLP_SIZES", "N", "RMS_EPS", "RMS_SIZES", "SIZES", "T", "decode",
+           "forward", "forward_first", "masked_exp", "mlp", "norm", "qk_scaled", "rmsnorm", "row_max", "row_sum",
+           "weighted_sum"]
+
+# The three RMSNorm forms of the decode step: (rows view, normed axis, its length, x shape)
+RMS_FORMS = {"forward": ("X", "H", H, (1, H)), "forward_q": ("N, G", "D", D, (N * G, D)),
+             "forward_k": ("N", "D", D, (N, D))}
 
 
 def _bits(v):
@@ -107,3 +113,21 @@ def mlp_inputs(seed):
     x = b(rng.standard_normal(H))
     return (x, b(rng.standard_normal(L * H) / np.sqrt(H)), b(rng.standard_normal(L * H) / np.sqrt(H)),
             b(rng.standard_normal(H * L) / np.sqrt(L)))
+
+
+def rms_inputs(seed, form):
+    """x and the gain (bf16 bits) of one RMSNorm form; gains near 1 as the model's are."""
+    rng = np.random.default_rng(seed)
+    _, _, n, shape = RMS_FORMS[form]
+    x = emu.f32_to_bf16((2.0 * rng.standard_normal(shape[0] * shape[1])).astype(np.float32))
+    w = emu.f32_to_bf16((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+    return x, w
+
+
+def rmsnorm_float(x, w, form):
+    """rmsnorm.rs in float64 with its one bf16 narrow: (rms per row, y)."""
+    _, _, n, shape = RMS_FORMS[form]
+    xf = emu.bf16_to_f32(x).astype(np.float64).reshape(shape)
+    rms = np.sqrt((xf * xf).sum(axis=1) / n + RMS_EPS)
+    y = emu.f32_to_bf16((xf * emu.bf16_to_f32(w).astype(np.float64) / rms[:, None]).astype(np.float32))
+    return rms, y.reshape(-1)

@@ -78,3 +78,18 @@ def test_mlp_matches_the_oracle(rt):
     near(y, y_want)
     ok, rate = accepted(dc.mlp_float(x, up_w, gate_w, down_w), emu.bf16_to_f32(y))
     assert ok and rate == 1.0, rate
+
+
+
+@pytest.mark.parametrize("form", list(dc.RMS_FORMS))
+def test_rmsnorm_forms_match_the_oracle(rt, form):
+    """rmsnorm.rs forward (H = 1024), forward_q ([N, G, D]) and forward_k ([N, D]): the f32 sums of
+    squares regrouped on the GPU (within 1e-6), so y = bf16(x w / rms) may move by one ulp where the
+    quotient sits at a rounding boundary."""
+    rows, axis, n, _ = dc.RMS_FORMS[form]
+    x, w = dc.rms_inputs(82, form)
+    print(f"rmsnorm {form}", flush=True)
+    rms, y = dc.rmsnorm(dc.GpuOps(rt, dc.RMS_SIZES), x, w, rows, axis, n)
+    rms_w, y_w = dc.rmsnorm(dc.CpuOps(dc.RMS_SIZES), x, w, rows, axis, n)
+    np.testing.assert_allclose(dc.GpuOps(rt).get(rms, dc.F32), rms_w, rtol=1e-6)
+    near(dc.GpuOps(rt).get(y, dc.BF16), y_w)

@@ -11,6 +11,7 @@
   * a planted mistake (alpha taken as exp(max' - max)) that the acceptance test must reject.
 """
 import numpy as np
+import pytest
 
 import decode_chain as dc
 from oracle import emulator as emu
@@ -140,3 +141,37 @@ def test_planted_silu_mistake_is_rejected():
         del MLP_OPS.zip
     ok, _ = accepted(dc.mlp_float(x, up_w, gate_w, down_w), emu.bf16_to_f32(y))
     assert not ok
+
+
+
+# ---- RMSNorm of the decode step (rmsnorm.rs forward / forward_q / forward_k) ---------------------------
+
+RMS_OPS = dc.CpuOps(dc.RMS_SIZES)
+
+
+def rms_check(rms, y, x, w, form):
+    """Against float64: rms to the f32 rounding of a serial sum of at most 1024 squares, y (one bf16
+    narrow of an f32 quotient a few f32 ulps from the exact one) within one bf16 ulp and equal on
+    at least 99% of the elements."""
+    rr, yr = dc.rmsnorm_float(x, w, form)
+    np.testing.assert_allclose(rms, rr, rtol=1e-5)
+    g, r = emu.bf16_to_f32(y).astype(np.float64), emu.bf16_to_f32(yr).astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(r), 2.0 ** -126))) - 7)
+    return float(np.mean(y == yr)), float(np.max(np.abs(g - r) / ulp))
+
+
+@pytest.mark.parametrize("form", list(dc.RMS_FORMS))
+def test_rmsnorm_forms_against_float(form):
+    rows, axis, n, _ = dc.RMS_FORMS[form]
+    x, w = dc.rms_inputs(80, form)
+    rms, y = dc.rmsnorm(RMS_OPS, x, w, rows, axis, n)
+    exact, worst = rms_check(rms, y, x, w, form)
+    assert exact >= 0.99 and worst <= 1.0, (exact, worst)
+
+
+def test_planted_rmsnorm_length_mistake_is_rejected():
+    rows, axis, n, _ = dc.RMS_FORMS["forward_q"]
+    x, w = dc.rms_inputs(81, "forward_q")
+    rms, y = dc.rmsnorm(RMS_OPS, x, w, rows, axis, n + 1)  # mean over n + 1 elements: wrong
+    with pytest.raises(AssertionError):
+        rms_check(rms, y, x, w, "forward_q")
