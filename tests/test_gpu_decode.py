@@ -93,3 +93,17 @@ def test_rmsnorm_forms_match_the_oracle(rt, form):
     rms_w, y_w = dc.rmsnorm(dc.CpuOps(dc.RMS_SIZES), x, w, rows, axis, n)
     np.testing.assert_allclose(dc.GpuOps(rt).get(rms, dc.F32), rms_w, rtol=1e-6)
     near(dc.GpuOps(rt).get(y, dc.BF16), y_w)
+
+
+
+def test_reference_running_max_persists(rt):
+    """transformer_tests.rs:252-289 through the seam ops: the max stored after the third chunk is
+    sqrt(D), as the oracle's."""
+    from test_oracle_decode import running_max_case
+    case = running_max_case()
+    mx, sm, out, _ = dc.decode(dc.GpuOps(rt), *case)
+    mx_w, sm_w, out_w, _ = dc.decode(dc.CpuOps(), *case)
+    assert np.array_equal(mx.view(np.uint32), mx_w.view(np.uint32))
+    assert np.all(np.abs(mx - np.sqrt(dc.D)) < 0.05)
+    np.testing.assert_allclose(sm, sm_w, rtol=1e-5)
+    assert np.array_equal(out, out_w)
