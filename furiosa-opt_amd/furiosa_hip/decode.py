@@ -23,6 +23,17 @@ furiosa-opt-examples/src/transformer/kernel/mlp.rs:9-150 (`forward`, the SiLU ML
   x (:94-108)             bf16(f32(up) * silu)
   down (:110-150)         widen; f32 contraction over L; narrow to bf16
 
+furiosa-opt-examples/src/transformer/mod.rs:29-131, the rest of one decode step:
+
+  projection (:29-58)     rmsnorm(x); q, k, v = the GEMVs of projection.rs (widen; f32 contraction
+                          over H; narrow); v to the V cache row; rmsnorm_q(q), rmsnorm_k(k); RoPE
+                          (rope.rs: the half swap as two 64-element tile copies, then
+                          bf16(f32(x) cos + f32(swapped) sin), the sign folded into sin); k to the
+                          K cache row. The cache rows go through dma_scatter at a byte offset.
+  decoder (:89-116)       norm(out, sum); proj_o over Q; residual (residual.rs: bf16(f32(a) +
+                          f32(b))); rmsnorm; mlp; residual
+  final_layer (:118-131)  rmsnorm; lm_head (lm_head.rs: the GEMV over Wp = 19 tiles of 8192 rows)
+
 Each chain is written once against a small adapter: `SeamOps` runs the stages on the HIP runtime;
 the tests hold them against the same stages on the CPU oracle. The views are the logical layouts ([N, G, T], [T, N, D],
 [L, H], ...); the reference's slice placements change where values sit, not the order of any fold.
@@ -40,6 +51,12 @@ MLP_SIZES = dict(H=H, L=L)
 # RMSNorm of one token: the hidden state [H] (X, a unit row axis), q [N, G, D] and k [N, D]
 RMS_SIZES = dict(N=N, G=G, D=D, H=H, X=1)
 RMS_EPS = 6.25e-8  # rmsnorm.rs:28 (and :104, :159)
+Q, P = N * G * D, N * D  # axes.rs: the query and key/value projection widths
+W, WP, WT = 151936, 155648, 8192  # axes.rs: vocabulary, padded to 19 lm_head tiles of 8192 rows
+ROW_STRIDE_ND = N * D * 2  # bytes of one [N, D] bf16 KV-cache row: dma_scatter offsets (transformer.py:44)
+ROPE_THETA = 1_000_000.0   # transformer.py:41
+# Every view of one decode step (a layer and the final layer)
+STEP_SIZES = dict(N=N, G=G, D=D, T=T, H=H, L=L, Q=Q, P=P, X=1, Wp=WP)
 SQRT_HEAD_DIM = 11.313708  # attention.rs:10
 EPS = 6.25e-8              # attention.rs:13
 NEG_INF_BITS = 0xFF800000
@@ -122,6 +139,28 @@ class SeamOps:
         self.rt.transpose(out, x, t, self.view(src), self.view(dst), allow_broadcast=True)
         return out
 
+    def gemv(self, xw, ww, rows, k):
+        """f32 [rows] = sum over k of ww[rows, k] * xw[k]: one contraction over the whole weight."""
+        return self.contraction(xw, ww, k, f"{rows}, {k}", f"{rows}, {k}", rows)
+
+    def zeros(self, view, t):
+        return self._alloc(self._size(view), t)  # DmTensor::new(): zero-filled
+
+    def window(self, dst, x, t, view, base, src_offset, dst_offset):
+        """A tile copy (Tensor::tile views, commit_view): the cells of `view` placed at src_offset in
+        x's base mapping, written at dst_offset of dst's; dst is updated in place and returned."""
+        self.calls += 1
+        v, b = self.view(view), self.view(base)
+        self.rt.transpose(dst, x, t, v, v, src_map=b, dst_map=b, src_offset=src_offset, dst_offset=dst_offset)
+        return dst
+
+    def scatter(self, dst, src, index, t, src_map, key, dst_map, scaled):
+        """dma_scatter into dst (updated in place and returned); `index` i32 over `key`."""
+        self.calls += 1
+        self.rt.scatter(dst, src, self.put(index), t, self.view(src_map), self.view(key), self.view(dst_map),
+                        self.view(key), scaled)
+        return dst
+
 
 def qk_scaled(ops, q, k):
     """bf16 logits [N, G, T] (attention.rs:37-74)."""
@@ -188,9 +227,9 @@ def norm(ops, out, sm):
     return ops.map(ops.zip(ops.map(out, BF16, F32, "CAST"), s, F32, "DIV_F"), F32, BF16, "CAST")
 
 
-def decode(ops, q, ks, vs, masks, stages=None):
-    """Every chunk in order (transformer.py:530-545), then norm; (max, sum, out, normalised out) as
-    host arrays. `stages`, when a list, receives (max, sum, out) after each chunk."""
+def attend(ops, q, ks, vs, masks, stages=None):
+    """Every chunk in order (transformer.py:530-545); the running (max, sum, out) as device values.
+    `stages`, when a list, receives (max, sum, out) after each chunk as host arrays."""
     q = ops.put(q)
     mx = sm = out = None
     for c, (k, v, mask) in enumerate(zip(ks, vs, masks)):
@@ -201,39 +240,176 @@ def decode(ops, q, ks, vs, masks, stages=None):
             mx, sm, out = forward(ops, q, k, v, mask, mx, sm, out)
         if stages is not None:
             stages.append((ops.get(mx, F32), ops.get(sm, F32), ops.get(out, BF16)))
+    return mx, sm, out
+
+
+def decode(ops, q, ks, vs, masks, stages=None):
+    """attend, then norm; (max, sum, out, normalised out) as host arrays."""
+    mx, sm, out = attend(ops, q, ks, vs, masks, stages)
     y = norm(ops, out, sm)
     return ops.get(mx, F32), ops.get(sm, F32), ops.get(out, BF16), ops.get(y, BF16)
 
 
-def mlp(ops, x, up_w, gate_w, down_w, stages=None):
+def proj(ops, xw, w, rows, k="H"):
+    """bf16 [rows] = narrow(sum over k of f32(w[r, k]) * xw[k]): the GEMVs of projection.rs (proj_q
+    :9-50, proj_p :53-93, proj_o :114-152), mlp.rs (:29-69, :110-150) and lm_head.rs (:18-49). xw is
+    the widened input; w the bf16 weight [rows, k]."""
+    return ops.map(ops.gemv(xw, ops.map(ops.put(w), BF16, F32, "CAST"), rows, k), F32, BF16, "CAST")
+
+
+def mlp_block(ops, x, up_w, gate_w, down_w, stages=None):
     """mlp.rs:9-150 for one token: x [H], up/gate weights [L, H], down weight [H, L] (bf16 bits);
-    returns the bf16 output [H]. `stages`, when a dict, receives up, gate, x and the f32 down sums."""
+    returns the bf16 output [H] on the device. `stages`, when a dict, receives up, gate, x and the
+    f32 down sums."""
     xw = ops.map(ops.put(x), BF16, F32, "CAST")
-    up = ops.map(ops.contraction(xw, ops.map(ops.put(up_w), BF16, F32, "CAST"), "H", "L, H", "L, H", "L"),
-                 F32, BF16, "CAST")
-    gate = ops.map(ops.contraction(xw, ops.map(ops.put(gate_w), BF16, F32, "CAST"), "H", "L, H", "L, H", "L"),
-                   F32, BF16, "CAST")
+    up = proj(ops, xw, up_w, "L")
+    gate = proj(ops, xw, gate_w, "L")
     g = ops.map(gate, BF16, F32, "CAST")
     silu = ops.zip(ops.map(g, F32, F32, "SIGMOID"), g, F32, "MUL_F")
     h = ops.map(ops.zip(ops.map(up, BF16, F32, "CAST"), silu, F32, "MUL_F"), F32, BF16, "CAST")
-    hw = ops.map(h, BF16, F32, "CAST")
-    down = ops.contraction(hw, ops.map(ops.put(down_w), BF16, F32, "CAST"), "L", "H, L", "H, L", "H")
+    down = ops.gemv(ops.map(h, BF16, F32, "CAST"), ops.map(ops.put(down_w), BF16, F32, "CAST"), "H", "L")
     if stages is not None:
         stages.update(up=ops.get(up, BF16), gate=ops.get(gate, BF16), x=ops.get(h, BF16), down=ops.get(down, F32))
-    return ops.get(ops.map(down, F32, BF16, "CAST"), BF16)
+    return ops.map(down, F32, BF16, "CAST")
 
 
-def rmsnorm(ops, x, w, rows, axis, n):
+def mlp(ops, x, up_w, gate_w, down_w, stages=None):
+    """mlp_block with the output as a host array."""
+    return ops.get(mlp_block(ops, x, up_w, gate_w, down_w, stages), BF16)
+
+
+def rmsnorm(ops, x, w, rows, axis, n, rms=None):
     """rmsnorm.rs `forward` (:9-78), `forward_q` (:80-150) and `forward_k` (:152-...): over the view
     `rows, axis` of x (bf16 bits), with a gain w over `axis`, n = the axis length:
     ms = sum_axis f32(x)^2 / n + EPS; rms = sqrt(ms); y = bf16(f32(x) * f32(w) / rms).
-    Returns (rms, y)."""
+    Returns (rms, y). A given `rms` (f32 per row) replaces the computed one: the sum's f32 fold
+    order is free, and a check holds y to the rounding of the quotient by that rms."""
     full = f"{rows}, {axis}"
     xf = ops.map(ops.put(x), BF16, F32, "CAST")
-    ss = ops.reduce(ops.zip(xf, xf, F32, "MUL_F"), F32, full, rows, "ADD", 0)
-    ms = ops.map(ops.map(ss, F32, F32, "DIV_F", RHS_IMM, float(n)), F32, F32, "CLIP_ADD", RHS_IMM,
-                 float(np.float32(RMS_EPS)))
-    rms = ops.map(ms, F32, F32, "SQRT")
+    if rms is None:
+        ss = ops.reduce(ops.zip(xf, xf, F32, "MUL_F"), F32, full, rows, "ADD", 0)
+        ms = ops.map(ops.map(ss, F32, F32, "DIV_F", RHS_IMM, float(n)), F32, F32, "CLIP_ADD", RHS_IMM,
+                     float(np.float32(RMS_EPS)))
+        rms = ops.map(ms, F32, F32, "SQRT")
+    rms = ops.put(rms)
     wf = ops.relayout(ops.map(ops.put(w), BF16, F32, "CAST"), F32, axis, full)
     y = ops.zip(ops.zip(xf, wf, F32, "MUL_F"), ops.relayout(rms, F32, rows, full), F32, "DIV_F")
     return rms, ops.map(y, F32, BF16, "CAST")
+
+
+def residual(ops, a, b):
+    """bf16 [H] = bf16(f32(a) + f32(b)) (residual.rs:9-31: a plus the residual stream b)."""
+    s = ops.zip(ops.map(a, BF16, F32, "CAST"), ops.map(ops.put(b), BF16, F32, "CAST"), F32, "CLIP_ADD")
+    return ops.map(s, F32, BF16, "CAST")
+
+
+def rotate_half(ops, x, rows):
+    """The half swap over D (rope.rs:37-73): the first 64 elements of every row copied to the second
+    half of a zeroed [rows, D] tensor and the second half to the first, each as a tile copy of the
+    view `rows, D = 64 # 128` at a D offset. No negation: the sign is in the sin table."""
+    half, full = f"{rows}, D = {D // 2} # {D}", f"{rows}, D"
+    out = ops.zeros(full, BF16)
+    out = ops.window(out, x, BF16, half, full, {"D": 0}, {"D": D // 2})
+    return ops.window(out, x, BF16, half, full, {"D": D // 2}, {"D": 0})
+
+
+def rope(ops, x, cos, sin, rows):
+    """rope.rs:75-173 for x [rows, D] (bf16): bf16(f32(x) * cos + f32(rotate_half(x)) * sin), each
+    product an f32 multiply, their sum CLIP_ADD; cos, sin are bf16 [D] widened and broadcast."""
+    full = f"{rows}, D"
+    c = ops.relayout(ops.map(ops.put(cos), BF16, F32, "CAST"), F32, "D", full)
+    s = ops.relayout(ops.map(ops.put(sin), BF16, F32, "CAST"), F32, "D", full)
+    tc = ops.zip(ops.map(x, BF16, F32, "CAST"), c, F32, "MUL_F")
+    ts = ops.zip(ops.map(rotate_half(ops, x, rows), BF16, F32, "CAST"), s, F32, "MUL_F")
+    return ops.map(ops.zip(tc, ts, F32, "CLIP_ADD"), F32, BF16, "CAST")
+
+
+def cache_row(ops, cache, row, offset):
+    """dma_scatter::<m![1]> of one [N, D] row into a [T, N, D] cache (projection.rs:111, rope.rs:175):
+    the key axis is the unit mapping, the indexed axis T, and `offset` the row's byte offset
+    (row index * ROW_STRIDE_ND, transformer.py:432-435). Returns the updated cache."""
+    idx = np.array([offset], np.int32)
+    return ops.scatter(ops.put(cache), row, idx, BF16, "N, D", "1", "T, N, D", scaled=True)
+
+
+def rope_row(pos):
+    """cos and sin (bf16 bits [D]) at one absolute position, as the host builds its tables
+    (transformer.py:452-472): inv_freq = 1 / theta^(2i / D) in f32, cos = cos(pos * inv_freq) on both
+    halves, sin = [-sin, sin] (the rotation's sign folded in)."""
+    inv_freq = np.float32(1.0) / (np.float32(ROPE_THETA) ** (np.arange(0, D, 2, dtype=np.float32) / np.float32(D)))
+    f = np.float32(pos) * inv_freq.astype(np.float32)
+    cos = np.concatenate([np.cos(f), np.cos(f)]).astype(np.float32)
+    sin = np.concatenate([-np.sin(f), np.sin(f)]).astype(np.float32)
+
+    def bf16(v):  # round to nearest even (finite values)
+        u = v.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return bf16(cos), bf16(sin)
+
+
+def projection(ops, x, wq, wk, wv, g_in, g_q, g_k, offset, cos, sin, k_cache, v_cache, stages=None):
+    """ops::projection (mod.rs:29-58) for one token x [H]: returns (q [N, G, D], k_cache, v_cache),
+    the caches with row `offset` (bytes) written. `stages`, when a dict, receives the device values
+    y (the normed input), q, k, v (the GEMVs), qn, kn (their norms), kr (the roped k) and the rms of
+    each norm (y_rms, qn_rms, kn_rms)."""
+    y_rms, y = rmsnorm(ops, x, g_in, "X", "H", H)
+    yw = ops.map(y, BF16, F32, "CAST")
+    q, k, v = proj(ops, yw, wq, "Q"), proj(ops, yw, wk, "P"), proj(ops, yw, wv, "P")
+    v_cache = cache_row(ops, v_cache, v, offset)
+    qn_rms, qn = rmsnorm(ops, q, g_q, "N, G", "D", D)
+    kn_rms, kn = rmsnorm(ops, k, g_k, "N", "D", D)
+    qr, kr = rope(ops, qn, cos, sin, "N, G"), rope(ops, kn, cos, sin, "N")
+    k_cache = cache_row(ops, k_cache, kr, offset)
+    if stages is not None:
+        stages.update(y=y, y_rms=y_rms, q=q, k=k, v=v, qn=qn, qn_rms=qn_rms, kn=kn, kn_rms=kn_rms, kr=kr)
+    return qr, k_cache, v_cache
+
+
+def decoder(ops, out, sm, rx, wo, g_post, up_w, gate_w, down_w, stages=None):
+    """ops::decoder (mod.rs:89-116): the attention output normalised by its sum, proj_o over Q, the
+    residual, the post-attention RMSNorm, the MLP and the second residual; returns the new residual
+    stream [H]. `stages`, when a dict, receives a (the normed attention), o, rx1 (the first residual),
+    y (its norm), y_rms and m (the MLP output)."""
+    a = norm(ops, ops.put(out), ops.put(sm))  # [N, G, D], read as [Q]
+    o = proj(ops, ops.map(a, BF16, F32, "CAST"), wo, "H", "Q")
+    rx1 = residual(ops, o, rx)
+    y_rms, y = rmsnorm(ops, rx1, g_post, "X", "H", H)
+    mo = mlp_block(ops, y, up_w, gate_w, down_w)
+    if stages is not None:
+        stages.update(a=a, o=o, rx1=rx1, y=y, y_rms=y_rms, m=mo)
+    return residual(ops, mo, rx1)
+
+
+def final_layer(ops, x, g, lm_w, stages=None):
+    """ops::final_layer (mod.rs:118-131): rmsnorm, then the lm_head GEMV over the padded vocabulary
+    (lm_w [Wp, H]); returns the bf16 logits [Wp]."""
+    y_rms, y = rmsnorm(ops, x, g, "X", "H", H)
+    if stages is not None:
+        stages.update(y=y, y_rms=y_rms)
+    return proj(ops, ops.map(y, BF16, F32, "CAST"), lm_w, "Wp")
+
+
+def causal_mask(row):
+    """The mask of the chunk holding the query (transformer.py:437-450): keys up to `row` attended."""
+    m_ = np.zeros(T, np.float32)
+    m_[:row + 1] = 1.0
+    return m_
+
+
+def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None):
+    """One layer of Pipeline.step (transformer.py:495-562) for the token at absolute position pos:
+    projection into the cache of chunk pos // T at row pos % T, attention over chunks 0..pos // T
+    (the last one causal), decoder. `lw` holds the layer's weights by the names of mod.rs; `caches`
+    a list of (k, v) per chunk, updated. Returns the new residual stream."""
+    chunk, row = divmod(pos, T)
+    kc, vc = caches[chunk]
+    q, kc, vc = projection(ops, x, lw["q"], lw["k"], lw["v"], lw["input_norm"], lw["q_norm"], lw["k_norm"],
+                           row * ROW_STRIDE_ND, cos, sin, kc, vc, stages)
+    caches[chunk] = (kc, vc)
+    full = ops.put(np.ones(T, np.float32))
+    masks = [full] * chunk + [ops.put(causal_mask(row))]
+    ks, vs = [c[0] for c in caches[:chunk + 1]], [c[1] for c in caches[:chunk + 1]]
+    _, sm, out = attend(ops, q, ks, vs, masks)
+    if stages is not None:
+        stages.update(q_out=q, sum=sm, out=out)
+    return decoder(ops, out, sm, x, lw["o"], lw["post_norm"], lw["up"], lw["gate"], lw["down"], stages)

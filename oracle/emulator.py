@@ -196,14 +196,21 @@ def reduce(src: np.ndarray, dtype: int, src_map: dict, dst_map: dict, op: int, i
     return out
 
 
-def contraction(lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int, lhs_map: dict, rhs_map: dict,
-                pre_reduce: dict, out_map: dict) -> np.ndarray:
+def contraction_plan(lhs_map: dict, rhs_map: dict, pre_reduce: dict, out_map: dict):
+    """The read plans of a contraction (buf.rs:401-447): per output cell the lhs and rhs base
+    offsets, and the residue deltas shared by every cell. A plan depends on the mappings only, so a
+    caller that contracts several buffers of one layout resolves it once."""
     contracted = mr.carve(pre_reduce, out_map)
     ol, lr, lpos = mr.read_plan(lhs_map, out_map, contracted)
     _, _, rpos = mr.read_plan(rhs_map, out_map, contracted)
     lbase, ldelta = _additive(lpos, ol)
     rbase, rdelta = _additive(rpos, ol)
-    n_out = mr.size(out_map)
+    return lbase, ldelta, rbase, rdelta, mr.size(out_map)
+
+
+def contraction_run(plan, lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int) -> np.ndarray:
+    """Contracts lhs and rhs along a plan from contraction_plan."""
+    lbase, ldelta, rbase, rdelta, n_out = plan
     acc_t = I32 if out_t == I4 else out_t
     out = np.zeros(n_out, dtype=NP[acc_t])
     L, R = np.ascontiguousarray(lhs), np.ascontiguousarray(rhs)
@@ -211,6 +218,11 @@ def contraction(lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int, lhs_map
     lib.ref_contraction(_p(L), _p(R), in_t, _p(out), acc_t, n_out, _p(lbase), _p(rbase), len(ldelta), _p(ldelta),
                         _p(rdelta), len(L) * per, len(R) * per)
     return pack_nibbles(out) if out_t == I4 else out
+
+
+def contraction(lhs: np.ndarray, rhs: np.ndarray, in_t: int, out_t: int, lhs_map: dict, rhs_map: dict,
+                pre_reduce: dict, out_map: dict) -> np.ndarray:
+    return contraction_run(contraction_plan(lhs_map, rhs_map, pre_reduce, out_map), lhs, rhs, in_t, out_t)
 
 
 def pack_nibbles(v: np.ndarray) -> np.ndarray:
