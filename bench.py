@@ -339,14 +339,41 @@ def bench_decode(fh, rt, steps, warmup, rng):
     wu, wg = (rt.upload(f32_to_bf16(rng.standard_normal(fd.L * fd.H, dtype=np.float32) / 32)) for _ in range(2))
     wd = rt.upload(f32_to_bf16(rng.standard_normal(fd.H * fd.L, dtype=np.float32) / 55))
     mlp = lambda: fd.mlp(mops, x, wu, wg, wd)
-    n = max(5, steps // 10)
-    aw, ae = timed(rt, attention, n, max(2, warmup // 10))
-    a_calls = ops.calls
-    mw, me = timed(rt, mlp, n, max(2, warmup // 10))
-    m_calls = mops.calls
-    per = lambda calls: calls / (n + max(2, warmup // 10))
-    return dict(attention_4x512_keys=dict(wall_us=aw * 1e3, gpu_us=ae * 1e3, keys=4 * fd.T, seam_calls=per(a_calls)),
-                mlp_silu_h1024_l3072=dict(wall_us=mw * 1e3, gpu_us=me * 1e3, seam_calls=per(m_calls)))
+    # One whole layer of the decode step (projection, attention over two chunks, decoder) and the
+    # final layer, at position T + 88, weights and caches resident, masks and RoPE row hoisted.
+    sops = fd.SeamOps(rt, fd.STEP_SIZES)
+    up = lambda n, s: rt.upload(f32_to_bf16(rng.uniform(-s, s, n).astype(np.float32)))
+    ones = lambda n: rt.upload(np.full(n, 0x3F80, np.uint16))
+    lw = dict(q=up(fd.Q * fd.H, 1 / 32), k=up(fd.P * fd.H, 1 / 32), v=up(fd.P * fd.H, 1 / 32),
+              o=up(fd.H * fd.Q, 1 / 45), up=up(fd.L * fd.H, 1 / 32), gate=up(fd.L * fd.H, 1 / 32),
+              down=up(fd.H * fd.L, 1 / 55), input_norm=ones(fd.H), q_norm=ones(fd.D), k_norm=ones(fd.D),
+              post_norm=ones(fd.H))
+    pos = fd.T + 88
+    caches = [(up(fd.T * fd.N * fd.D, 1.0), up(fd.T * fd.N * fd.D, 1.0)) for _ in range(2)]
+    cos, sin = (rt.upload(t) for t in fd.rope_row(pos))
+    step_masks = [masks[0], rt.upload(fd.causal_mask(pos - fd.T))]
+    xs = up(fd.H, 1.0)
+    layer = lambda: fd.layer_step(sops, xs, lw, pos, caches, cos, sin, masks=step_masks)
+    fops = fd.SeamOps(rt, fd.STEP_SIZES)
+    lm, g = up(fd.WP * fd.H, 1 / 32), ones(fd.H)
+    final = lambda: fd.final_layer(fops, xs, g, lm)
+
+    n, w = max(5, steps // 10), max(2, warmup // 10)
+    per = lambda calls: calls / (n + w)
+    res = {}
+    for name, fn, o, extra in (
+            ("attention_4x512_keys", attention, ops, dict(keys=4 * fd.T)),
+            ("mlp_silu_h1024_l3072", mlp, mops, {}),
+            # HBM floor: the layer's seven weights (15.7 M bf16) and two chunks of K and V read once
+            ("layer_step_pos600", layer, sops, dict(hbm_bytes=2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q
+                                                                   + 3 * fd.L * fd.H) + 2 * 2 * fd.T * fd.N * fd.D * 2)),
+            ("final_layer_wp155648", final, fops, dict(hbm_bytes=2 * fd.WP * fd.H))):
+        wall, gpu = timed(rt, fn, n, w)
+        r = dict(wall_us=wall * 1e3, gpu_us=gpu * 1e3, seam_calls=per(o.calls), **extra)
+        if "hbm_bytes" in extra:
+            r["hbm_floor_us"] = extra["hbm_bytes"] / (PEAK_HBM_GBS * 1e3)
+        res[name] = r
+    return res
 
 
 def cpu_baseline_gemm(target_s: float = 30.0):
@@ -522,6 +549,9 @@ def main():
     for k, r in res.get("decode", {}).items():  # latency per token through the seam ops
         configs[f"decode_seam_{k}"] = dict(value=r["wall_us"], unit="us", gpu_us=r["gpu_us"],
                                            seam_calls=r["seam_calls"], us_per_call=r["wall_us"] / r["seam_calls"])
+        if "hbm_floor_us" in r:  # the time the step's weights and caches take to stream once at HBM peak
+            configs[f"decode_seam_{k}"].update(hbm_floor_us=r["hbm_floor_us"],
+                                               roofline_frac=r["hbm_floor_us"] / r["gpu_us"])
     for group in ("relayout", "chain"):
         for k, r in res.get(group, {}).items():
             name = "switch_broadcast_256x512x64_x4_bf16" if k == "switch_broadcast" else f"relayout_{k}_8192x8192_bf16"

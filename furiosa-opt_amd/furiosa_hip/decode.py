@@ -396,18 +396,21 @@ def causal_mask(row):
     return m_
 
 
-def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None):
+def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None, masks=None):
     """One layer of Pipeline.step (transformer.py:495-562) for the token at absolute position pos:
     projection into the cache of chunk pos // T at row pos % T, attention over chunks 0..pos // T
     (the last one causal), decoder. `lw` holds the layer's weights by the names of mod.rs; `caches`
-    a list of (k, v) per chunk, updated. Returns the new residual stream."""
+    a list of (k, v) per chunk, updated. `masks`, when given, are the chunks' masks already resident
+    (the pipeline hoists them out of its layer loop, transformer.py:437-450). Returns the new
+    residual stream."""
     chunk, row = divmod(pos, T)
     kc, vc = caches[chunk]
     q, kc, vc = projection(ops, x, lw["q"], lw["k"], lw["v"], lw["input_norm"], lw["q_norm"], lw["k_norm"],
                            row * ROW_STRIDE_ND, cos, sin, kc, vc, stages)
     caches[chunk] = (kc, vc)
-    full = ops.put(np.ones(T, np.float32))
-    masks = [full] * chunk + [ops.put(causal_mask(row))]
+    if masks is None:
+        full = ops.put(np.ones(T, np.float32))
+        masks = [full] * chunk + [ops.put(causal_mask(row))]
     ks, vs = [c[0] for c in caches[:chunk + 1]], [c[1] for c in caches[:chunk + 1]]
     _, sm, out = attend(ops, q, ks, vs, masks)
     if stages is not None:
