@@ -28,6 +28,7 @@ SOURCES = [
     "k_vector.hip",
     "k_gemm.hip",
     "k_gemm_wheels.hip",
+    "k_gemv.hip",
     "k_rowops.hip",
     "k_attention.hip",
     "k_mlp.hip",

@@ -1132,6 +1132,15 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
         place *= w.size;
       }
       const bool unit_k = rw.size() == 1 && rw[0].stride[0] == 1 && rw[0].stride[1] == 1;
+      // One lhs vector against contiguous rhs rows (a token against a weight matrix): the GEMV
+      // kernel, one lane folding each cell in k order.
+      if (unit_k && mw.empty() && bw.empty() && nw.size() == 1 && !padded) {
+        const int64_t N = nw[0].w.size, K = rw[0].size, ldw = nw[0].w.stride[1];
+        if (K - 1 < lhs_len && (N - 1) * ldw + K - 1 < rhs_len && gemv_supported(ct, co, L, R, N, K, ldw)) {
+          launch_gemv(rt->stream, O, L, R, ct, co, N, K, ldw, nw[0].place);
+          return;
+        }
+      }
       if (gemm_supported(ct, co) && unit_k) {
         // The tiled kernel: one affine row, column and batch wheel each, no padding.
         if (!padded && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1) {

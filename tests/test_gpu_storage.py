@@ -682,6 +682,42 @@ def test_contraction_mfma(rt, case, types):
         close(emu.bf16_to_f32(got), emu.bf16_to_f32(want))
 
 
+# One vector against weight rows (k_gemv: a lane folds each cell in k order). Sizes cover each
+# rows-per-block choice (16, 32, 64), a ragged last block, K with a partial last stage, K = 8, rows
+# wider than K (a padded row stride) and a strided output.
+GEMV_CASES = [
+    (dict(N=1024, K=1024), "K", "N, K", "N, K", "N"),
+    (dict(N=1000, K=1000), "K", "N, K", "N, K", "N"),
+    (dict(N=3, K=8), "K", "N, K", "N, K", "N"),
+    (dict(N=20000, K=136), "K", "N, K", "N, K", "N"),
+    (dict(N=40000, K=64), "K", "N, K", "N, K", "N"),
+    (dict(N=300, K=200), "K", "N, K # 208", "N, K", "N"),
+]
+
+
+@pytest.mark.parametrize("case", GEMV_CASES, ids=lambda c: f"{c[1]}|{c[2]}->{c[4]}:{c[0]}")
+@pytest.mark.parametrize("types", [(BF16, F32, True), (BF16, BF16, False), (BF16, F32, False)])
+def test_contraction_gemv_exact(rt, case, types):
+    sizes, l_t, r_t, p_t, o_t = case
+    in_t, out_t, widened = types
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
+    rng = np.random.default_rng(21)
+    lhs = emu.f32_to_bf16(rng.standard_normal(mr.size(lo)).astype(np.float32))
+    rhs = emu.f32_to_bf16(rng.standard_normal(mr.size(ro)).astype(np.float32))
+    want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
+    print(f"gemv {sizes} {r_t} -> {o_t} out {out_t} widened {widened}", flush=True)
+    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[out_t]))
+    maps = [fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)]
+    if widened:
+        wl, wr = rt.alloc(len(lhs) * 4), rt.alloc(len(rhs) * 4)
+        rt.map(wl, F32, rt.upload(lhs), BF16, len(lhs), fh.op("CAST"))
+        rt.map(wr, F32, rt.upload(rhs), BF16, len(rhs), fh.op("CAST"))
+        rt.contraction(out, wl, wr, F32, F32, *maps)
+    else:
+        rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *maps)
+    assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
+
+
 # ---- transmute --------------------------------------------------------------------------------------
 
 
