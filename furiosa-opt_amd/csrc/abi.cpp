@@ -133,9 +133,39 @@ fm::Factors flat(const char* json_text, const char* what) {
   return fm::flatten(fm::parse_json(json_text));
 }
 
-void check_rt(fo_runtime* rt) { require(rt != nullptr, "runtime is NULL"); }
-void check_buf(const fo_buffer* b, const char* what) {
+// The runtime of the entry point running on this thread (set by check_rt, which every entry point
+// that takes buffers calls first): the stream a deferred zero fill goes on.
+thread_local fo_runtime* t_rt = nullptr;
+void check_rt(fo_runtime* rt) {
+  require(rt != nullptr, "runtime is NULL");
+  t_rt = rt;
+}
+void fill_pending(fo_runtime* rt, const fo_buffer* b) {
+  if (!b->zero_pending) return;
+  fo_buffer* m = const_cast<fo_buffer*>(b);
+  FO_HIP(hipSetDevice(rt->device));
+  launch_zero(rt->stream, m->ptr, (m->capacity + 15) & ~15ull);
+  m->zero_pending = false;
+}
+void check_ptr(const fo_buffer* b, const char* what) {
   require(b != nullptr && b->ptr != nullptr, std::string(what) + " buffer is NULL");
+}
+// A buffer an op reads, or writes in part: its deferred zero fill goes first.
+void check_buf(const fo_buffer* b, const char* what) {
+  check_ptr(b, what);
+  if (b->zero_pending) {
+    require(t_rt != nullptr, "buffer used before any runtime call on this thread");
+    fill_pending(t_rt, b);
+  }
+}
+// An op's output, just before its launch: `written` bytes from the start are overwritten; when
+// they cover the buffer the deferred zero fill is dropped, otherwise it goes first.
+void claim_out(fo_runtime* rt, fo_buffer* b, uint64_t written) {
+  if (!b->zero_pending) return;
+  if (written >= b->bytes)
+    b->zero_pending = false;
+  else
+    fill_pending(rt, b);
 }
 
 void set_device(fo_runtime* rt) { FO_HIP(hipSetDevice(rt->device)); }
@@ -485,9 +515,10 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
         throw OomError("hipMalloc(" + std::to_string(cls) + ") failed: " + hipGetErrorString(e));
       b->capacity = cls;
     }
-    // Zero-filled (Backend::zeroed): a fill kernel on the runtime's stream orders the zeros before
-    // every later op of this runtime, including a reuse's previous owner's last reads.
-    launch_zero(rt->stream, b->ptr, (cls + 15) & ~15ull);
+    // Zero-filled (Backend::zeroed), the fill deferred to the first use (check_buf / claim_out). It
+    // then runs on that op's runtime stream, after every earlier op of the runtime, including a
+    // reuse's previous owner's last reads.
+    b->zero_pending = true;
     *out = b.release();
   });
 }
@@ -522,6 +553,7 @@ int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out) {
     fo_buffer* b = nullptr;
     int32_t st = fo_buffer_alloc(rt, src->bytes, &b);
     if (st != FO_OK) throw OomError(g_last_error);
+    b->zero_pending = false;  // every byte is copied
     FO_HIP(hipMemcpyAsync(b->ptr, src->ptr, src->bytes, hipMemcpyDeviceToDevice, rt->stream));
     *out = b;
   });
@@ -532,11 +564,12 @@ uint64_t fo_buffer_bytes(const fo_buffer* buf) { return buf ? buf->bytes : 0; }
 int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst) {
   return guard([&] {
     check_rt(rt);
-    check_buf(dst, "dst");
+    check_ptr(dst, "dst");
     note_write(dst);
     require(host != nullptr || bytes == 0, "host pointer is NULL");
     require(bytes <= dst->bytes, "write of " + std::to_string(bytes) + " bytes exceeds the buffer");
     set_device(rt);
+    claim_out(rt, dst, bytes);
     TraceScope trace_span(rt, "write");
     FO_HIP(hipMemcpyAsync(dst->ptr, host, bytes, hipMemcpyHostToDevice, rt->stream));
     FO_HIP(hipStreamSynchronize(rt->stream));
@@ -631,13 +664,14 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
                const fo_op* op) {
   return guard([&] {
     check_rt(rt);
-    check_buf(dst, "dst");
+    check_ptr(dst, "dst");
     note_write(dst);
     check_buf(src, "src");
     require(op != nullptr, "op is NULL");
     require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
     if (n == 0) return;
     set_device(rt);
+    claim_out(rt, dst, span_bytes(dst_t, n));
     TraceScope trace_span(rt, "map");
     launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
     // An exact widening cast (the engine's contract_outer widen) leaves a record for the
@@ -653,7 +687,7 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
                     fo_dtype in_t, uint64_t n, const fo_op* op) {
   return guard([&] {
     check_rt(rt);
-    check_buf(dst, "dst");
+    check_ptr(dst, "dst");
     note_write(dst);
     check_buf(a, "a");
     check_buf(b, "b");
@@ -663,6 +697,7 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
             "zip_with: n exceeds a buffer");
     if (n == 0) return;
     set_device(rt);
+    claim_out(rt, dst, n * dtype_bytes(dst_t));
     TraceScope trace_span(rt, "zip_with");
     launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
   });
@@ -1004,7 +1039,7 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
                   const char* dst_map, int32_t op, uint32_t identity, int32_t allow_broadcast) {
   return guard([&] {
     check_rt(rt);
-    check_buf(dst, "dst");
+    check_ptr(dst, "dst");
     note_write(dst);
     check_buf(src, "src");
     require(t == FO_F32 || t == FO_I32 || t == FO_BF16, "reduce: dtype must be f32, i32 or bf16");
@@ -1028,6 +1063,7 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     require(out_count < (1ll << 31), "reduce: more than 2^31 output cells");
     if (out_count == 0) return;
     set_device(rt);
+    claim_out(rt, dst, (uint64_t)(out_count * eb));  // every cell is written, a dead one with the identity
     TraceScope trace_span(rt, "reduce");
     const int mem[1] = {0};
     const Wheels<1> owd = to_desc<1>(ow, mem), rwd = to_desc<1>(rw, mem);
@@ -1053,7 +1089,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
                       const char* out_map, bool noalloc) {
   {
     check_rt(rt);
-    check_buf(out, "out");
+    check_ptr(out, "out");
     note_write(out);
     check_buf(lhs, "lhs");
     check_buf(rhs, "rhs");
@@ -1218,6 +1254,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
       launch_contraction_generic(rt->stream, O, L, R, ct, co, lhs_len, rhs_len, out_count, to_desc<2>(ow, mem),
                                  to_desc<2>(rw, mem));
     };
+    claim_out(rt, out, span_bytes(out_t, (uint64_t)out_count));  // every cell is written
     run();
     if (in_t == FO_I4 && out_t == FO_I4) launch_pack_i4(rt->stream, out->ptr, (const int32_t*)O, (uint64_t)out_count);
   }

@@ -66,6 +66,9 @@ struct fo_buffer {
   uint64_t capacity = 0;  // the block's size (the pool's size class)
   int device = 0;
   std::shared_ptr<fo_pool> pool;
+  // Zero-filled as allocated (Backend::zeroed), with the fill deferred to the buffer's first use:
+  // an op that overwrites every byte drops it, any other use launches it first.
+  bool zero_pending = false;
 };
 
 namespace fo {

@@ -80,10 +80,12 @@ int32_t fo_runtime_device_info(fo_runtime* rt, int32_t* compute_units, char* arc
 
 /* Device allocation of `bytes` (zero-filled), the storage of an `HbmTensor`.
  * Replaces Backend::alloc_hbm / zeroed (backend/mod.rs:60-66, cpu.rs:31-35). Stream-ordered: the
- * zeros are written by a kernel on the runtime's stream (no host wait), and fo_buffer_free returns
- * the block to the runtime's cache without waiting for the device; the block is reused only by
- * buffers of the same runtime, whose ops all follow on the same stream. A buffer used on another
- * runtime's stream must be synchronized with its own runtime first. */
+ * zeros are written by a kernel on the stream of the first call that uses the buffer (no host
+ * wait), and not at all when that call overwrites every byte of it (a map or zip over the whole
+ * buffer, a reduce or contraction whose output covers it, a full-size fo_write); fo_buffer_free
+ * returns the block to the runtime's cache without waiting for the device; the block is reused
+ * only by buffers of the same runtime, whose ops all follow on the same stream. A buffer used on
+ * another runtime's stream must be synchronized with its own runtime first. */
 int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out);
 void fo_buffer_free(fo_buffer* buf);
 /* Device-to-device copy into a new buffer (Storage: Clone). Also Backend::reshape (backend/mod.rs:

@@ -131,6 +131,29 @@ def test_rmsnorm_softmax_nonfinite(rt, cols, gain_case):
     close_chain(got[fin], want[fin], frac_beyond=1e-4, hard=bound[fin])
 
 
+@pytest.mark.parametrize("cols", [1024, 4096])
+def test_rmsnorm_softmax_subnormal_operands(rt, cols):
+    """Subnormal inputs and gains read as zero (float/bf16.rs:16-40), also where a large gain would
+    lift a subnormal product into the normal range: a row of subnormals only (y = 0, the uniform
+    row), rows mixing them with normal values, and gains up to 2^63 with subnormal gains between."""
+    rows = 6
+    rng = np.random.default_rng(34)
+    x = bf16(rng, rows * cols).reshape(rows, cols)
+    sub = rng.integers(1, 0x80, (rows, cols)).astype(np.uint16) | (rng.integers(0, 2, (rows, cols)).astype(np.uint16) << 15)
+    x[0] = sub[0]
+    x[1:4, ::3] = sub[1:4, ::3]
+    g = emu.f32_to_bf16(rng.uniform(0.5, 2.0, cols).astype(np.float32))
+    g[::7] = emu.f32_to_bf16(np.float32(2.0 ** 63))
+    g[3::11] = rng.integers(1, 0x80, len(g[3::11])).astype(np.uint16)  # subnormal gains
+    want = emu.bf16_to_f32(emu.rmsnorm_softmax(x.ravel(), g, rows, cols, 1e-6)).reshape(rows, cols)
+    out = rt.alloc(rows * cols * 2)
+    rt.rmsnorm_softmax(out, rt.upload(x.ravel()), rt.upload(g), rows, cols, 1e-6)
+    got = emu.bf16_to_f32(out.read(np.uint16)).reshape(rows, cols)
+    assert np.all(want[0] == want[0, 0])  # the subnormal row is uniform
+    bound = rmsnorm_bound(x.ravel(), g, rows, cols, 1e-6).reshape(rows, cols)
+    close_chain(got, want, frac_beyond=1e-4, hard=bound)
+
+
 def bf16r(x):
     """f32 -> bf16 -> f32 with the reference's rounding (float/bf16.rs:28-40)."""
     return emu.bf16_to_f32(emu.f32_to_bf16(np.asarray(x, np.float32)))

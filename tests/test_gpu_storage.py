@@ -873,3 +873,64 @@ def test_trace_spans(rt):
     rt.map(x, I32, y, I32, 16, fh.op("ADD_FXP", fh.RHS_IMM, 1))
     rt.sync()
     assert len(spans) == 3
+
+
+# ---- fresh buffers read as zero (Backend::zeroed), with the fill deferred to first use ----------------
+
+
+def dirty_block(rt, nbytes):
+    """A buffer of nbytes taken from a cached block last holding 0x5A bytes: allocate, dirty, free,
+    then allocate the same size again (the runtime's cache hands the block back)."""
+    b = rt.upload(np.full(nbytes, 0x5A, np.uint8))
+    rt.sync()
+    b.free()
+    return rt.alloc(nbytes)
+
+
+@pytest.mark.parametrize("nbytes", [4096, 4000, 3 << 20])
+def test_fresh_buffer_reads_zero(rt, nbytes):
+    assert not dirty_block(rt, nbytes).read(np.uint8).any()
+
+
+def test_fresh_buffer_partial_writes_keep_zero_tails(rt):
+    """Ops that write part of a fresh buffer leave the rest zero: a map over fewer elements, a host
+    write of a prefix, a reduce and a contraction into a larger buffer, and a transpose into a
+    padded window."""
+    n = 1024
+    x = rt.upload(np.arange(n, dtype=np.float32))
+    d = dirty_block(rt, 4 * n)
+    rt.map(d, F32, x, F32, n // 2, fh.op("CAST"))
+    got = d.read(np.float32)
+    assert np.array_equal(got[: n // 2], np.arange(n // 2, dtype=np.float32)) and not got[n // 2:].any()
+    d = dirty_block(rt, 4 * n)
+    d.write(np.ones(10, np.float32))
+    got = d.read(np.float32)
+    assert np.all(got[:10] == 1) and not got[10:].any()
+    s = dict(A=8, B=128)
+    d = dirty_block(rt, 4 * n)
+    rt.reduce(d, x, F32, fh.m("A, B", **s), fh.m("A", **s), fh.RED["ADD"], 0)
+    got = d.read(np.float32)
+    assert np.array_equal(got[:8], np.arange(n, dtype=np.float32).reshape(8, 128).sum(axis=1)) and not got[8:].any()
+    s = dict(M=4, K=8, N=4)
+    d = dirty_block(rt, 4 * n)
+    a = np.ones(32, np.float32)
+    rt.contraction(d, rt.upload(a), rt.upload(a), F32, F32, *(fh.m(t, **s) for t in ("M, K", "N, K", "M, N, K", "M, N")))
+    got = d.read(np.float32)
+    assert np.all(got[:16] == 8) and not got[16:].any()
+    s = dict(A=8, B=16)
+    d = dirty_block(rt, 8 * 32 * 4)
+    rt.transpose(d, rt.upload(np.ones(8 * 16, np.int32)), I32, fh.m("A, B", **s), fh.m("A, B # 32", **s))
+    got = d.read(np.int32).reshape(8, 32)
+    assert np.all(got[:, :16] == 1) and not got[:, 16:].any()
+
+
+def test_fresh_buffer_full_overwrite(rt):
+    """A map, zip or contraction that writes every byte of a fresh buffer returns exactly its values
+    (no fill is needed there), and the buffer then keeps them."""
+    n = 1000
+    x = rt.upload(np.arange(n, dtype=np.float32))
+    d = dirty_block(rt, 4 * n)
+    rt.zip_with(d, F32, x, x, F32, n, fh.op("ADD_F"))
+    assert np.array_equal(d.read(np.float32), 2 * np.arange(n, dtype=np.float32))
+    rt.map(d, F32, d, F32, n, fh.op("CAST"))
+    assert np.array_equal(d.read(np.float32), 2 * np.arange(n, dtype=np.float32))
