@@ -55,31 +55,100 @@ thread_local std::string g_last_error;
 // Pending widens. The engine widens both contraction operands with Backend::map before
 // contraction_prewidened (contract_outer, engine/contraction/outer/mod.rs:145-163), so a
 // contraction over f32 (i32) operands usually reads buffers that are exact casts of bf16 or 8-bit
-// float (i8) data. fo_map records each such cast (dst, src, source type, element count); a
-// contraction whose two operands both have a record of the same source type reads the narrow
-// sources instead -- the MFMA kernels consume them directly, and the generic fold widens them the
-// same way the map did, so its result is unchanged. Any op that writes a buffer (or frees it)
-// drops the records naming it as either side. Records are process-wide, as buffers are.
+// float (i8) data. fo_map records each such cast (dst, src, source type, element count) and defers
+// the cast itself: a contraction whose two operands both have a record of the same source type
+// reads the narrow sources instead -- the MFMA kernels consume them directly, and the generic fold
+// widens them the same way the map would, so its result is unchanged -- and never needs the wide
+// copy. Any other use of the wide buffer (check_buf) runs the deferred cast first, on the stream of
+// the runtime that issued it; so does a write to or the freeing of its source (note_write,
+// forget_buffer), before the source changes. A write to either side drops the record. Records are
+// process-wide, as buffers are.
 struct WidenRecord {
   const fo_buffer* dst;
   const fo_buffer* src;
   fo_dtype src_t;
   uint64_t n;
+  fo_dtype dst_t;
+  fo_op op;
+  fo_runtime* rt;  // the runtime whose stream the deferred cast goes on
+  bool deferred;   // the cast has not run yet
 };
 std::mutex g_widen_mu;
 std::vector<WidenRecord> g_widen;
 
-void note_write(const fo_buffer* b) {
-  if (!b) return;
-  std::lock_guard<std::mutex> lock(g_widen_mu);
-  g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
-                               [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
-                g_widen.end());
+// Runs deferred casts, in order, outside the lock.
+void run_deferred(const std::vector<WidenRecord>& rs) {
+  for (auto& r : rs) {
+    FO_HIP(hipSetDevice(r.rt->device));
+    launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
+    const_cast<fo_buffer*>(r.dst)->widen_pending = false;
+  }
 }
 
-void record_widen(const fo_buffer* dst, const fo_buffer* src, fo_dtype src_t, uint64_t n) {
+// b is about to be written: a deferred cast from or into it runs first, then its records go.
+void note_write(const fo_buffer* b) {
+  if (!b) return;
+  std::vector<WidenRecord> todo;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    for (auto& r : g_widen)
+      if ((r.dst == b || r.src == b) && r.deferred) todo.push_back(r);
+    g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
+                                 [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
+                  g_widen.end());
+  }
+  run_deferred(todo);
+}
+
+// b is being freed: a deferred cast from it runs first (its block may be reused right after); one
+// into it is dropped.
+void forget_buffer(const fo_buffer* b) {
+  std::vector<WidenRecord> todo;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    for (auto& r : g_widen)
+      if (r.src == b && r.deferred && r.dst != b) todo.push_back(r);
+    g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
+                                 [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
+                  g_widen.end());
+  }
+  run_deferred(todo);
+}
+
+// b is about to be read: its deferred cast, if any, runs first (the record stays for contractions).
+void materialize(const fo_buffer* b) {
+  if (!b->widen_pending) return;
+  std::vector<WidenRecord> todo;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    for (auto& r : g_widen)
+      if (r.dst == b && r.deferred) {
+        todo.push_back(r);
+        r.deferred = false;
+      }
+  }
+  run_deferred(todo);
+}
+
+// A runtime going away: every cast it deferred runs now, on its stream.
+void materialize_runtime(fo_runtime* rt) {
+  std::vector<WidenRecord> todo;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    for (auto& r : g_widen)
+      if (r.rt == rt && r.deferred) {
+        todo.push_back(r);
+        r.deferred = false;
+      }
+  }
+  run_deferred(todo);
+}
+
+void record_widen(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype dst_t, fo_dtype src_t, uint64_t n,
+                  const fo_op& op) {
   std::lock_guard<std::mutex> lock(g_widen_mu);
-  g_widen.push_back({dst, src, src_t, n});
+  g_widen.push_back({dst, src, src_t, n, dst_t, op, rt, true});
+  dst->widen_pending = true;
 }
 
 bool find_widen(const fo_buffer* dst, WidenRecord* out) {
@@ -157,6 +226,7 @@ void check_buf(const fo_buffer* b, const char* what) {
     require(t_rt != nullptr, "buffer used before any runtime call on this thread");
     fill_pending(t_rt, b);
   }
+  materialize(b);
 }
 // An op's output, just before its launch: `written` bytes from the start are overwritten; when
 // they cover the buffer the deferred zero fill is dropped, otherwise it goes first.
@@ -415,6 +485,10 @@ int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
 
 void fo_runtime_free(fo_runtime* rt) {
   if (!rt) return;
+  try {
+    materialize_runtime(rt);
+  } catch (const std::exception&) {
+  }
   (void)hipSetDevice(rt->device);
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto& e : rt->events)
@@ -525,7 +599,10 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
 
 void fo_buffer_free(fo_buffer* buf) {
   if (!buf) return;
-  note_write(buf);
+  try {
+    forget_buffer(buf);
+  } catch (const std::exception&) {  // a failed launch leaves the error for the next call to report
+  }
   if (buf->ptr) {
     bool direct = true;
     if (buf->pool) {
@@ -672,14 +749,17 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, span_bytes(dst_t, n));
-    TraceScope trace_span(rt, "map");
-    launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
-    // An exact widening cast (the engine's contract_outer widen) leaves a record for the
-    // contraction that follows.
+    // An exact widening cast (the engine's contract_outer widen) is recorded for the contraction
+    // that follows and deferred until something else needs the wide copy.
     const bool widen = op->code == FO_OP_CAST && dst != src &&
                        ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
                         (dst_t == FO_I32 && src_t == FO_I8));
-    if (widen) record_widen(dst, src, src_t, n);
+    if (widen) {
+      record_widen(rt, dst, src, dst_t, src_t, n, *op);
+      return;
+    }
+    TraceScope trace_span(rt, "map");
+    launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
   });
 }
 
@@ -1091,8 +1171,10 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     check_rt(rt);
     check_ptr(out, "out");
     note_write(out);
-    check_buf(lhs, "lhs");
-    check_buf(rhs, "rhs");
+    // The operands are checked here and made current (zero fill, deferred cast) below, unless the
+    // contraction reads their narrow sources.
+    check_ptr(lhs, "lhs");
+    check_ptr(rhs, "rhs");
     bool ok_types = (in_t == FO_BF16 && (out_t == FO_BF16 || out_t == FO_F32)) ||
                     (in_t == FO_I8 && (out_t == FO_I8 || out_t == FO_I32)) || (in_t == FO_F32 && out_t == FO_F32) ||
                     (in_t == FO_I32 && out_t == FO_I32) ||
@@ -1121,6 +1203,13 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     void* O = out->ptr;
     int64_t lhs_len, rhs_len;
     WidenRecord wl{}, wr{};
+    const bool narrow = (in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) &&
+                        find_widen(rhs, &wr) && wl.src_t == wr.src_t && (int64_t)wl.n >= fm::size(l) &&
+                        (int64_t)wr.n >= fm::size(r);
+    if (!narrow) {
+      check_buf(lhs, "lhs");
+      check_buf(rhs, "rhs");
+    }
     if (in_t == FO_I4) {
       auto up = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
       const uint64_t la = up(lhs->bytes * 2), ra = up(rhs->bytes * 2), oa = out_t == FO_I4 ? (uint64_t)out_count * 4 : 0;
@@ -1137,8 +1226,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
       }
       lhs_len = (int64_t)lhs->bytes * 2;
       rhs_len = (int64_t)rhs->bytes * 2;
-    } else if ((in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) && find_widen(rhs, &wr) &&
-               wl.src_t == wr.src_t && (int64_t)wl.n >= fm::size(l) && (int64_t)wr.n >= fm::size(r)) {
+    } else if (narrow) {
       // contraction_prewidened of two widened operands: contract their narrow sources (the
       // pending-widen records above), accumulating in the same type.
       ct = wl.src_t;

@@ -69,6 +69,9 @@ struct fo_buffer {
   // Zero-filled as allocated (Backend::zeroed), with the fill deferred to the buffer's first use:
   // an op that overwrites every byte drops it, any other use launches it first.
   bool zero_pending = false;
+  // An exact widening cast into this buffer recorded but not yet run (the runtime's pending
+  // widens): a read runs it first.
+  bool widen_pending = false;
 };
 
 namespace fo {

@@ -211,7 +211,9 @@ typedef struct fo_op {
 } fo_op;
 
 /* Backend::map (backend/mod.rs:92): dst[i] = op(src[i]) for i < n (unary, cast, or binary with an
- * immediate rhs). */
+ * immediate rhs). An exact widening CAST (bf16 / f8e4m3 / f8e5m2 to f32, i8 to i32) into another
+ * buffer is recorded and run only when something other than fo_contraction on the pair of widened
+ * operands uses dst, or before src is written or freed: the results are those of running it here. */
 int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* src, fo_dtype src_t,
                uint64_t n, const fo_op* op);
 /* Backend::zip_with (backend/mod.rs:96-100): dst[i] = op(a[i], b[i]). */

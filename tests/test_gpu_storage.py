@@ -934,3 +934,63 @@ def test_fresh_buffer_full_overwrite(rt):
     assert np.array_equal(d.read(np.float32), 2 * np.arange(n, dtype=np.float32))
     rt.map(d, F32, d, F32, n, fh.op("CAST"))
     assert np.array_equal(d.read(np.float32), 2 * np.arange(n, dtype=np.float32))
+
+
+# ---- deferred widening casts (fo_map CAST to f32 / i32 recorded for the contraction after it) ----------
+
+
+def widened(rt, n, seed=40):
+    rng = np.random.default_rng(seed)
+    v = emu.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
+    src = rt.upload(v)
+    dst = rt.alloc(4 * n)
+    rt.map(dst, F32, src, BF16, n, fh.op("CAST"))
+    return v, src, dst
+
+
+def test_deferred_widen_reads_back(rt):
+    v, src, dst = widened(rt, 1000)
+    assert np.array_equal(dst.read(np.float32), emu.bf16_to_f32(v))
+
+
+def test_deferred_widen_survives_a_write_to_its_source(rt):
+    """The cast runs before its source changes (a host write, an op writing it) or is freed and its
+    block reused: the wide buffer keeps the values the source had at the map."""
+    v, src, dst = widened(rt, 4096, 41)
+    src.write(np.zeros(4096, np.uint16))
+    assert np.array_equal(dst.read(np.float32), emu.bf16_to_f32(v))
+    v, src, dst = widened(rt, 4096, 42)
+    rt.map(src, BF16, rt.upload(np.zeros(4096, np.uint16)), BF16, 4096, fh.op("CAST"))
+    assert np.array_equal(dst.read(np.float32), emu.bf16_to_f32(v))
+    v, src, dst = widened(rt, 4096, 43)
+    src.free()
+    reuse = rt.upload(np.full(4096, 0x7F00, np.uint16))  # same size class: likely the freed block
+    assert np.array_equal(dst.read(np.float32), emu.bf16_to_f32(v))
+    del reuse
+
+
+def test_deferred_widen_feeds_other_ops(rt):
+    """A zip, a partial transpose into the wide buffer, and a contraction on the narrow sources
+    followed by a read of the wide copies all see the widened values."""
+    n = 1024
+    v, src, dst = widened(rt, n, 44)
+    out = rt.alloc(4 * n)
+    rt.zip_with(out, F32, dst, dst, F32, n, fh.op("ADD_F"))
+    assert np.array_equal(out.read(np.float32), 2 * emu.bf16_to_f32(v))
+    v, src, dst = widened(rt, n, 45)
+    s = dict(A=32, B=32)
+    rt.transpose(dst, rt.upload(np.zeros(32 * 16, np.float32)), F32, fh.m("A, B = 16", **s), fh.m("A, B = 16 # 32", **s))
+    want = emu.bf16_to_f32(v).reshape(32, 32).copy()
+    want[:, :16] = 0
+    assert np.array_equal(dst.read(np.float32).reshape(32, 32), want)
+    s = dict(M=16, K=64, N=16)
+    va, sa, wa = widened(rt, 16 * 64, 46)
+    vb, sb, wb = widened(rt, 16 * 64, 47)
+    maps = [fh.m(t, **s) for t in ("M, K", "N, K", "M, N, K", "M, N")]
+    c = rt.alloc(16 * 16 * 4)
+    rt.contraction(c, wa, wb, F32, F32, *maps)
+    want = emu.contraction(emu.bf16_to_f32(va), emu.bf16_to_f32(vb), F32, F32,
+                           *(mr.parse(t, s) for t in ("M, K", "N, K", "M, N, K", "M, N")))
+    close(c.read(np.float32), want, rel=1e-5)
+    assert np.array_equal(wa.read(np.float32), emu.bf16_to_f32(va))
+    assert np.array_equal(wb.read(np.float32), emu.bf16_to_f32(vb))
