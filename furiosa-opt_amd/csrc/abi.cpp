@@ -6,6 +6,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "runtime.hpp"
@@ -197,9 +198,45 @@ int64_t write_str(const std::string& s, char* out, uint64_t cap) {
   return (int64_t)s.size();
 }
 
+// Mapping work memoised by the strings that determine it: an engine issues the same few layouts
+// over and over, so each is parsed and resolved once per process (a failing one is not kept and
+// fails again on the next call). The table is cleared when it reaches its cap.
+template <typename V>
+class Memo {
+  std::mutex mu_;
+  std::unordered_map<std::string, V> m_;
+  static constexpr size_t kCap = 4096;
+
+ public:
+  template <typename F>
+  V get(const std::string& key, F&& make) {
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      auto it = m_.find(key);
+      if (it != m_.end()) return it->second;
+    }
+    V v = make();
+    std::lock_guard<std::mutex> lock(mu_);
+    if (m_.size() >= kCap) m_.clear();
+    m_.emplace(key, v);
+    return v;
+  }
+};
+
+// The key of several strings (NUL-free C strings, NULL read as empty).
+std::string memo_key(std::initializer_list<const char*> parts) {
+  std::string k;
+  for (const char* p : parts) {
+    if (p) k += p;
+    k += '\x01';
+  }
+  return k;
+}
+
 fm::Factors flat(const char* json_text, const char* what) {
   require(json_text && *json_text, std::string(what) + ": mapping is required");
-  return fm::flatten(fm::parse_json(json_text));
+  static Memo<fm::Factors> memo;
+  return memo.get(json_text, [&] { return fm::flatten(fm::parse_json(json_text)); });
 }
 
 // The runtime of the entry point running on this thread (set by check_rt, which every entry point
@@ -837,19 +874,29 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     check_buf(dst, "dst");
     note_write(dst);
     check_buf(src, "src");
-    fm::Factors sv = flat(src_view, "src_view"), dv = flat(dst_view, "dst_view");
-    // transpose_broadcast (backend/op_prep.rs:18-28): the dst leftover after carving out src.
-    if (!allow_broadcast)
-      require(fm::is_padding(fm::carve(dv, sv)), "transpose: Dst adds axes absent from Src; pass allow_broadcast");
-    fm::Joint j = fm::sequence({sv}, {dv}, fm::Mode::Carve);
-    fm::Factors sm = src_map && *src_map ? flat(src_map, "src_map") : sv;
-    fm::Factors dm = dst_map && *dst_map ? flat(dst_map, "dst_map") : dv;
-    int64_t src_base = fm::window_base(sm, fm::parse_offset_json(src_offset ? src_offset : ""));
-    int64_t dst_base = fm::window_base(dm, fm::parse_offset_json(dst_offset ? dst_offset : ""));
+    struct Plan {
+      fm::Joint j;
+      int64_t dv_size, src_base, dst_base;
+    };
+    static Memo<Plan> memo;
+    const Plan plan = memo.get(
+        memo_key({src_view, dst_view, src_map, dst_map, src_offset, dst_offset, allow_broadcast ? "b" : "-"}), [&] {
+          fm::Factors sv = flat(src_view, "src_view"), dv = flat(dst_view, "dst_view");
+          // transpose_broadcast (backend/op_prep.rs:18-28): the dst leftover after carving out src.
+          if (!allow_broadcast)
+            require(fm::is_padding(fm::carve(dv, sv)), "transpose: Dst adds axes absent from Src; pass allow_broadcast");
+          fm::Joint j = fm::sequence({sv}, {dv}, fm::Mode::Carve);
+          fm::Factors sm = src_map && *src_map ? flat(src_map, "src_map") : sv;
+          fm::Factors dm = dst_map && *dst_map ? flat(dst_map, "dst_map") : dv;
+          return Plan{j, fm::size(dv), fm::window_base(sm, fm::parse_offset_json(src_offset ? src_offset : "")),
+                      fm::window_base(dm, fm::parse_offset_json(dst_offset ? dst_offset : ""))};
+        });
+    const fm::Joint& j = plan.j;
+    const int64_t src_base = plan.src_base, dst_base = plan.dst_base;
     int64_t eb = dtype_bytes(t);
     int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
     require(dst_base <= dst_len, "transpose: dst window starts past the buffer");
-    int64_t count = std::min<int64_t>({j.stream_size, fm::size(dv), dst_len - dst_base});
+    int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
     if (count <= 0) return;
     require(src_base + max_live_offset(j.wheels, 0) < src_len, "transpose: the src window reads past the buffer");
     require(count < (1ll << 31), "transpose: more than 2^31 positions");
@@ -1125,20 +1172,30 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     require(t == FO_F32 || t == FO_I32 || t == FO_BF16, "reduce: dtype must be f32, i32 or bf16");
     require(op >= FO_RED_ADD && op <= FO_RED_ADD_SAT, "reduce: unknown op");
     require(op != FO_RED_ADD_SAT || t == FO_I32, "reduce: saturating add is i32 only");
-    fm::Factors s = flat(src_map, "src_map"), d = flat(dst_map, "dst_map");
-    // BufStorage::reduce (buf.rs:331-376): inter = dst.carve(broadcast), residue = src.carve(inter).
-    auto bsyms = fm::broadcast_symbols(s, d);
-    require(allow_broadcast || bsyms.empty(),
-            "reduce: Dst adds axes absent from the source; pass allow_broadcast=true for reduce-then-broadcast");
-    fm::Factors bcast;
-    for (auto& x : d)
-      if (x.kind == fm::Factor::Term && std::find(bsyms.begin(), bsyms.end(), x.sym) != bsyms.end()) bcast.push_back(x);
-    fm::Factors inter = bcast.empty() ? d : fm::carve(d, bcast);
-    fm::Factors residue = fm::carve(s, inter);
-    fm::Joint j = fm::sequence({s}, {d, residue}, fm::Mode::Read);
-    auto ow = part(j, 0), rw = live_only(part(j, 1));
+    struct Plan {
+      int64_t out_count;
+      std::vector<fm::Wheel> ow, rw;
+    };
+    static Memo<Plan> memo;
+    const Plan plan = memo.get(memo_key({src_map, dst_map, allow_broadcast ? "b" : "-"}), [&] {
+      fm::Factors s = flat(src_map, "src_map"), d = flat(dst_map, "dst_map");
+      // BufStorage::reduce (buf.rs:331-376): inter = dst.carve(broadcast), residue = src.carve(inter).
+      auto bsyms = fm::broadcast_symbols(s, d);
+      require(allow_broadcast || bsyms.empty(),
+              "reduce: Dst adds axes absent from the source; pass allow_broadcast=true for reduce-then-broadcast");
+      fm::Factors bcast;
+      for (auto& x : d)
+        if (x.kind == fm::Factor::Term && std::find(bsyms.begin(), bsyms.end(), x.sym) != bsyms.end())
+          bcast.push_back(x);
+      fm::Factors inter = bcast.empty() ? d : fm::carve(d, bcast);
+      fm::Factors residue = fm::carve(s, inter);
+      fm::Joint j = fm::sequence({s}, {d, residue}, fm::Mode::Read);
+      return Plan{fm::size(d), part(j, 0), live_only(part(j, 1))};
+    });
+    const std::vector<fm::Wheel>& ow = plan.ow;
+    const std::vector<fm::Wheel>& rw = plan.rw;
     int64_t eb = dtype_bytes(t);
-    int64_t out_count = fm::size(d);
+    int64_t out_count = plan.out_count;
     require(out_count * eb <= (int64_t)dst->bytes, "reduce: dst buffer smaller than dst_map");
     require(out_count < (1ll << 31), "reduce: more than 2^31 output cells");
     if (out_count == 0) return;
@@ -1181,13 +1238,22 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
                     ((in_t == FO_F8E4M3 || in_t == FO_F8E5M2) && (out_t == in_t || out_t == FO_F32)) ||
                     (in_t == FO_I4 && (out_t == FO_I4 || out_t == FO_I32));
     require(ok_types, "contraction: unsupported operand/output dtype pair");
-    fm::Factors l = flat(lhs_map, "lhs_map"), r = flat(rhs_map, "rhs_map");
-    fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");
     // contraction_in (buf.rs:401-447): contracted = pre_reduce.carve(out); one ReadPlan per operand.
-    fm::Factors contracted = fm::carve(pre, o);
-    fm::Joint j = fm::sequence({l, r}, {o, contracted}, fm::Mode::Read);
-    auto ow = part(j, 0), rw = live_only(part(j, 1));
-    int64_t out_count = fm::size(o);
+    struct Plan {
+      int64_t l_size, r_size, out_count;
+      std::vector<fm::Wheel> ow, rw;
+    };
+    static Memo<Plan> memo;
+    const Plan plan = memo.get(memo_key({lhs_map, rhs_map, pre_reduce, out_map}), [&] {
+      fm::Factors l = flat(lhs_map, "lhs_map"), r = flat(rhs_map, "rhs_map");
+      fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");
+      fm::Factors contracted = fm::carve(pre, o);
+      fm::Joint j = fm::sequence({l, r}, {o, contracted}, fm::Mode::Read);
+      return Plan{fm::size(l), fm::size(r), fm::size(o), part(j, 0), live_only(part(j, 1))};
+    });
+    const std::vector<fm::Wheel>& ow = plan.ow;
+    const std::vector<fm::Wheel>& rw = plan.rw;
+    int64_t out_count = plan.out_count;
     require(span_bytes(out_t, (uint64_t)out_count) <= out->bytes, "contraction: out buffer smaller than out_map");
     require(out_count < (1ll << 31), "contraction: more than 2^31 output cells");
     require(out_t != FO_I4 || out_count % 2 == 0, "contraction: a 4-bit output stream needs an even cell count");
@@ -1204,8 +1270,8 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     int64_t lhs_len, rhs_len;
     WidenRecord wl{}, wr{};
     const bool narrow = (in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) &&
-                        find_widen(rhs, &wr) && wl.src_t == wr.src_t && (int64_t)wl.n >= fm::size(l) &&
-                        (int64_t)wr.n >= fm::size(r);
+                        find_widen(rhs, &wr) && wl.src_t == wr.src_t && (int64_t)wl.n >= plan.l_size &&
+                        (int64_t)wr.n >= plan.r_size;
     if (!narrow) {
       check_buf(lhs, "lhs");
       check_buf(rhs, "rhs");

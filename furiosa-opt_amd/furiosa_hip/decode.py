@@ -84,6 +84,7 @@ class SeamOps:
         self.rt = rt
         self.sizes = sizes
         self.views = {}  # view text -> MappingSerde JSON (an engine builds these once per type)
+        self.ops = {}    # (name, flags, imm) -> op descriptor, built once
         self.calls = 0   # seam calls issued (allocations excluded)
 
     def view(self, text):
@@ -106,18 +107,25 @@ class SeamOps:
     def _alloc(self, n, t):
         return self.rt.alloc(n * np.dtype(NP_DTYPE[t]).itemsize)
 
+    def _op(self, name, flags=0, imm=0):
+        key = (name, flags, imm)
+        o = self.ops.get(key)
+        if o is None:
+            o = self.ops[key] = op(name, flags, imm)
+        return o
+
     def map(self, x, src_t, dst_t, name, flags=0, imm=0):
         self.calls += 1
         n = x.nbytes // np.dtype(NP_DTYPE[src_t]).itemsize
         out = self._alloc(n, dst_t)
-        self.rt.map(out, dst_t, x, src_t, n, op(name, flags, imm))
+        self.rt.map(out, dst_t, x, src_t, n, self._op(name, flags, imm))
         return out
 
     def zip(self, a, b, t, name, flags=0):
         self.calls += 1
         n = a.nbytes // np.dtype(NP_DTYPE[t]).itemsize
         out = self._alloc(n, t)
-        self.rt.zip_with(out, t, a, b, t, n, op(name, flags))
+        self.rt.zip_with(out, t, a, b, t, n, self._op(name, flags))
         return out
 
     def reduce(self, x, t, src, dst, op, identity):
