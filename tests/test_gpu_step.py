@@ -126,21 +126,34 @@ def test_decoder_step_wires_kernel_boundaries(rt):
     assert np.array_equal(got, rx)
 
 
-def test_layer_step_matches_the_model(rt):
-    """One layer at position T + 88 (two chunks, the second causal) through the seam ops: the new
-    residual stream under the acceptance test against the float64 model, the earlier chunk's cache
-    untouched and the written rows those of the device's own projection."""
+@pytest.mark.parametrize("pos", [0, T - 1, T + 88, 2 * T])
+def test_layer_step_matches_the_oracle(rt, pos):
+    """One layer through the seam ops at the first token, the last row of a chunk, a row inside the
+    second chunk and the first row of a third, against the same layer on the oracle: the new
+    residual stream bit-exact on at least 99% of its elements and everywhere within the reference's
+    per-element tolerance max(0.01 |e|, 2^-8) of the oracle's (the device regroups f32 sums and
+    rounds exp within ulps, which a few bf16 narrows downstream can turn into ulp-sized steps); at
+    T + 88 also under the reference's acceptance test against the float64 model. The earlier
+    chunks' caches stay untouched and the written K and V rows are the device's own projection."""
     from test_oracle_step import step_model
-    pos = T + 88
-    lw, x, caches = step_case(103, pos)
-    print("layer step seed 103 pos", pos, flush=True)
+    chunk, row = divmod(pos, T)
+    lw, x, caches = step_case(103 + pos, pos)
+    print("layer step seed", 103 + pos, "pos", pos, flush=True)
     ops = fd.SeamOps(rt, fd.STEP_SIZES)
     cs = [(ops.put(k), ops.put(v)) for k, v in caches]
     st = {}
     got = ops.get(fd.layer_step(ops, x, lw, pos, cs, *fd.rope_row(pos), st), BF16)
-    ok, rate = accepted(step_model(lw, x, caches, pos), dc.f64(got))
-    assert ok, rate
-    assert np.array_equal(ops.get(cs[0][0], BF16), caches[0][0])
-    k1 = ops.get(cs[1][0], BF16).reshape(T, -1)
-    assert np.array_equal(k1[88], ops.get(st["kr"], BF16))
-    assert np.array_equal(np.delete(k1, 88, axis=0), np.delete(caches[1][0].reshape(T, -1), 88, axis=0))
+    want = CPU.get(fd.layer_step(CPU, x, lw, pos, list(caches), *fd.rope_row(pos)), BF16)
+    g, w = dc.f64(got), dc.f64(want)
+    assert np.mean(got == want) >= 0.99
+    assert np.all(np.abs(g - w) <= np.maximum(0.01 * np.abs(w), 2.0 ** -8))
+    if pos == T + 88:
+        ok, rate = accepted(step_model(lw, x, caches, pos), g)
+        assert ok, rate
+    for c in range(chunk):
+        assert np.array_equal(ops.get(cs[c][0], BF16), caches[c][0])
+        assert np.array_equal(ops.get(cs[c][1], BF16), caches[c][1])
+    for side, want_row in ((0, st["kr"]), (1, st["v"])):
+        got_cache = ops.get(cs[chunk][side], BF16).reshape(T, -1)
+        assert np.array_equal(got_cache[row], ops.get(want_row, BF16))
+        assert np.array_equal(np.delete(got_cache, row, axis=0), np.delete(caches[chunk][side].reshape(T, -1), row, axis=0))

@@ -279,11 +279,47 @@ def step_model(lw, x, caches, pos):
 
 
 def test_layer_step_matches_the_model():
-    pos = T + 88  # the second chunk, row 88
+    """One layer at position T + 88 (the second chunk, row 88) against the float64 model under the
+    reference's acceptance test. (At a chunk's first rows the reference's max, taken over the masked
+    zero keys too, and its bf16(p) numerator over an f32 sum move single-key outputs by up to about
+    1% from the model's softmax, so the model check is made where many keys are attended.)"""
+    pos = T + 88
     lw, x, caches = step_case(98, pos)
     want = step_model(lw, x, caches, pos)
     cs = list(caches)
     got = OPS.get(fd.layer_step(OPS, x, lw, pos, cs, *fd.rope_row(pos)), fd.BF16)
     ok, rate = accepted(want, dc.f64(got))
     assert ok, rate
-    assert np.array_equal(cs[0][0], caches[0][0])  # the earlier chunk's cache is not written
+    assert np.array_equal(cs[0][0], caches[0][0]) and np.array_equal(cs[0][1], caches[0][1])
+
+
+@pytest.mark.parametrize("pos", [0, T - 1, 2 * T])
+def test_layer_step_edge_positions(pos):
+    """The first token, the last row of a chunk and the first row of a third chunk: the new K and V
+    rows are the projection's, at the token's row of its chunk, every other row and every earlier
+    chunk untouched, and a chunk's first row attends to its one key: the attention output is that
+    key's value row, scaled by the reference's bf16(p) / (p + EPS) with p = exp(s - max(s, 0))
+    (the max over the masked zero keys too, attention.rs:77-134, 370-392)."""
+    chunk, row = divmod(pos, T)
+    lw, x, caches = step_case(98 + pos, pos)
+    cs = list(caches)
+    st = {}
+    fd.layer_step(OPS, x, lw, pos, cs, *fd.rope_row(pos), st)
+    for c in range(chunk):
+        assert np.array_equal(cs[c][0], caches[c][0]) and np.array_equal(cs[c][1], caches[c][1])
+    for side, new_row in ((0, st["kr"]), (1, st["v"])):
+        got = cs[chunk][side].reshape(T, -1)
+        assert np.array_equal(got[row], new_row)
+        assert np.array_equal(np.delete(got, row, axis=0), np.delete(caches[chunk][side].reshape(T, -1), row, axis=0))
+    if row == 0 and chunk == 0:
+        # s = bf16(q.k0 / sqrt(D)) per (n, g); p = exp(s - max(s, 0)); out = bf16(bf16(p) v) then
+        # bf16(out / (p + EPS)): closed form in float64 with the narrows at those points
+        q = dc.f64(st["q_out"], N, G, D)
+        k0 = dc.f64(st["kr"], N, D)
+        v0 = dc.f64(st["v"], N, D)
+        s = dc.r16(np.einsum("ngd,nd->ng", q, k0) / np.float32(fd.SQRT_HEAD_DIM))
+        p = np.exp(s - np.maximum(s, 0.0))
+        out = dc.r16(dc.r16(p)[..., None] * v0[:, None, :])
+        want = dc.r16(out / (p + np.float32(fd.EPS))[..., None])
+        got = dc.f64(st["a"], N, G, D)
+        assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 2.0 ** -20)) <= 2 ** -7
