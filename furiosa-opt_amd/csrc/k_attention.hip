@@ -129,7 +129,7 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
   // Scaled sums first, then the block max over them (the max of products is the product of the
   // max, and bf16 rounding is monotonic, so the max commutes with both). Taking it on product
   // results also spares the quieting of each operand that a max of raw MFMA outputs needs.
-  float bmax = -INFINITY;
+  float bmax = -INFINITY, bmax2 = -INFINITY;
   float xs[2][16];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
@@ -143,8 +143,12 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
       for (int r = 0; r < 16; ++r) xs[kt][r] = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : xs[kt][r];
     }
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) bmax = __builtin_fmaxf(bmax, __builtin_fmaxf(xs[kt][r], xs[kt][r + 1]));
+    for (int r = 0; r < 16; r += 4) {  // two chains of three-way maxima
+      bmax = __builtin_fmaxf(__builtin_fmaxf(bmax, xs[kt][r]), xs[kt][r + 1]);
+      bmax2 = __builtin_fmaxf(__builtin_fmaxf(bmax2, xs[kt][r + 2]), xs[kt][r + 3]);
+    }
   }
+  bmax = __builtin_fmaxf(bmax, bmax2);
   {
     const LanePair b = half_pair(bmax);  // the query's other 32 keys live in lane ^ 32
     bmax = __builtin_fmaxf(b.lo, b.hi);
