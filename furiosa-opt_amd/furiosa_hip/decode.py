@@ -77,6 +77,9 @@ def mapping_size(js):
     return size(json.loads(js))
 
 
+_ITEM = {t: np.dtype(d).itemsize for t, d in NP_DTYPE.items()}  # element bytes per dtype code
+
+
 class SeamOps:
     """The stages through the C ABI (device buffers)."""
 
@@ -85,6 +88,7 @@ class SeamOps:
         self.sizes = sizes
         self.views = {}  # view text -> MappingSerde JSON (an engine builds these once per type)
         self.ops = {}    # (name, flags, imm) -> op descriptor, built once
+        self.sizes_of = {}  # view text -> its mapping's size
         self.calls = 0   # seam calls issued (allocations excluded)
 
     def view(self, text):
@@ -94,7 +98,10 @@ class SeamOps:
         return js
 
     def _size(self, text):
-        return mapping_size(self.view(text))
+        n = self.sizes_of.get(text)
+        if n is None:
+            n = self.sizes_of[text] = mapping_size(self.view(text))
+        return n
 
     def put(self, arr):
         if isinstance(arr, Buffer):  # already resident
@@ -105,7 +112,7 @@ class SeamOps:
         return x.read(NP_DTYPE[t])
 
     def _alloc(self, n, t):
-        return self.rt.alloc(n * np.dtype(NP_DTYPE[t]).itemsize)
+        return self.rt.alloc(n * _ITEM[t])
 
     def _op(self, name, flags=0, imm=0):
         key = (name, flags, imm)
@@ -116,14 +123,14 @@ class SeamOps:
 
     def map(self, x, src_t, dst_t, name, flags=0, imm=0):
         self.calls += 1
-        n = x.nbytes // np.dtype(NP_DTYPE[src_t]).itemsize
+        n = x.nbytes // _ITEM[src_t]
         out = self._alloc(n, dst_t)
         self.rt.map(out, dst_t, x, src_t, n, self._op(name, flags, imm))
         return out
 
     def zip(self, a, b, t, name, flags=0):
         self.calls += 1
-        n = a.nbytes // np.dtype(NP_DTYPE[t]).itemsize
+        n = a.nbytes // _ITEM[t]
         out = self._alloc(n, t)
         self.rt.zip_with(out, t, a, b, t, n, self._op(name, flags))
         return out
