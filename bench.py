@@ -358,6 +358,19 @@ def bench_decode(fh, rt, steps, warmup, rng):
     lm, g = up(fd.WP * fd.H, 1 / 32), ones(fd.H)
     final = lambda: fd.final_layer(fops, xs, g, lm)
 
+    # A whole token of the Qwen3-0.6B-shaped model (28 layers, tied 151936-row embedding) through
+    # the pipeline at position T + 88, every layer's caches holding two chunks.
+    layers = 28
+    hw = {k: f32_to_bf16(rng.uniform(-1 / 32, 1 / 32, lw[k].nbytes // 2).astype(np.float32))
+          for k in ("q", "k", "v", "o", "up", "gate", "down")}
+    model = dict(embed=lm, final_norm=g, lm_head=lm,
+                 layers=[dict({k: rt.upload(v) for k, v in hw.items()}, input_norm=ones(fd.H), q_norm=ones(fd.D),
+                              k_norm=ones(fd.D), post_norm=ones(fd.H)) for _ in range(layers)])
+    pops = fd.SeamOps(rt, fd.STEP_SIZES)
+    pipe = fd.Pipeline(pops, model)
+    pipe.caches = [[(up(fd.T * fd.N * fd.D, 1.0), up(fd.T * fd.N * fd.D, 1.0)) for _ in range(2)] for _ in range(layers)]
+    token = lambda: pipe.step(7, pos)
+
     n, w = max(5, steps // 10), max(2, warmup // 10)
     per = lambda calls: calls / (n + w)
     res = {}
@@ -367,7 +380,11 @@ def bench_decode(fh, rt, steps, warmup, rng):
             # HBM floor: the layer's seven weights (15.7 M bf16) and two chunks of K and V read once
             ("layer_step_pos600", layer, sops, dict(hbm_bytes=2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q
                                                                    + 3 * fd.L * fd.H) + 2 * 2 * fd.T * fd.N * fd.D * 2)),
-            ("final_layer_wp155648", final, fops, dict(hbm_bytes=2 * fd.WP * fd.H))):
+            ("final_layer_wp155648", final, fops, dict(hbm_bytes=2 * fd.WP * fd.H)),
+            # HBM floor: 28 layers as above, the lm_head, and the embedding row
+            ("token_28_layers_pos600", token, pops,
+             dict(hbm_bytes=28 * (2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q + 3 * fd.L * fd.H)
+                                   + 2 * 2 * fd.T * fd.N * fd.D * 2) + 2 * fd.WP * fd.H + 2 * fd.H))):
         wall, gpu = timed(rt, fn, n, w)
         r = dict(wall_us=wall * 1e3, gpu_us=gpu * 1e3, seam_calls=per(o.calls), **extra)
         if "hbm_bytes" in extra:

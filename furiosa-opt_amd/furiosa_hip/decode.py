@@ -56,7 +56,7 @@ W, WP, WT = 151936, 155648, 8192  # axes.rs: vocabulary, padded to 19 lm_head ti
 ROW_STRIDE_ND = N * D * 2  # bytes of one [N, D] bf16 KV-cache row: dma_scatter offsets (transformer.py:44)
 ROPE_THETA = 1_000_000.0   # transformer.py:41
 # Every view of one decode step (a layer and the final layer)
-STEP_SIZES = dict(N=N, G=G, D=D, T=T, H=H, L=L, Q=Q, P=P, X=1, Wp=WP)
+STEP_SIZES = dict(N=N, G=G, D=D, T=T, H=H, L=L, Q=Q, P=P, X=1, Wp=WP, W=W)
 SQRT_HEAD_DIM = 11.313708  # attention.rs:10
 EPS = 6.25e-8              # attention.rs:13
 NEG_INF_BITS = 0xFF800000
@@ -168,6 +168,15 @@ class SeamOps:
         v, b = self.view(view), self.view(base)
         self.rt.transpose(dst, x, t, v, v, src_map=b, dst_map=b, src_offset=src_offset, dst_offset=dst_offset)
         return dst
+
+    def row(self, table, i, t, rows, cols):
+        """Row i of a [rows, cols] table: a gather of one index (the indexed axis `rows`, the
+        payload `cols`) into a fresh [cols]."""
+        self.calls += 1
+        out = self._alloc(self._size(cols), t)
+        self.rt.gather(out, self.put(table), self.put(np.array([i], np.int32)), t, self.view(f"{rows}, {cols}"),
+                       self.view(f"X, {cols}"), self.view("X"), False)
+        return out
 
     def scatter(self, dst, src, index, t, src_map, key, dst_map, scaled):
         """dma_scatter into dst (updated in place and returned); `index` i32 over `key`."""
@@ -431,3 +440,66 @@ def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None, masks=None):
     if stages is not None:
         stages.update(q_out=q, sum=sm, out=out)
     return decoder(ops, out, sm, x, lw["o"], lw["post_norm"], lw["up"], lw["gate"], lw["down"], stages)
+
+
+def embedding(ops, table, token):
+    """ops::embedding (mod.rs:23-27) on the token's row of the embedding table (transformer.py:507:
+    `embedding_table[token]`): row `token` of the [W, H] table, as [H]."""
+    return ops.row(table, token, BF16, "W", "H")
+
+
+class Pipeline:
+    """Pipeline.step (transformer.py:425-566) over the seam ops: per token the embedding, every
+    layer's projection (K and V into the cache of chunk pos // T at row pos % T), attention over
+    chunks 0..pos // T and decoder, then the final layer; greedy sampling of the first W logits
+    (sample_token, transformer.py:489-490: the first index of the largest). `model` holds `embed`
+    [W, H], `layers` (dicts of layer_step's weight names), `final_norm` [H] and `lm_head` [Wp, H],
+    as bf16 bits or resident buffers. The KV caches are created zeroed per (layer, chunk), the masks
+    and RoPE rows per position, as the reference's pipeline hoists them."""
+
+    def __init__(self, ops, model):
+        self.ops = ops
+        self.model = {k: (ops.put(v) if k != "layers" else [{n: ops.put(w) for n, w in lw.items()} for lw in v])
+                      for k, v in model.items()}
+        self.caches = [[] for _ in self.model["layers"]]
+        self.full = ops.put(np.ones(T, np.float32))
+
+    def _cache(self, layer, chunk):
+        cs = self.caches[layer]
+        while len(cs) <= chunk:
+            cs.append((self.ops.zeros("T, N, D", BF16), self.ops.zeros("T, N, D", BF16)))
+        return cs
+
+    def step(self, token, pos):
+        """Runs one token at absolute position pos; returns the logits [Wp] as bf16 bits."""
+        ops = self.ops
+        chunk, row = divmod(pos, T)
+        cos, sin = (ops.put(t) for t in rope_row(pos))
+        masks = [self.full] * chunk + [ops.put(causal_mask(row))]
+        x = embedding(ops, self.model["embed"], token)
+        for layer, lw in enumerate(self.model["layers"]):
+            cs = self._cache(layer, chunk)
+            x = layer_step(ops, x, lw, pos, cs, cos, sin, masks=masks)
+        logits = final_layer(ops, x, self.model["final_norm"], self.model["lm_head"])
+        return ops.get(logits, BF16)
+
+    def generate(self, prompt, n_new):
+        """Every prompt token in turn, then n_new greedy tokens; returns (new tokens, each step's
+        logits)."""
+        out, logs = [], []
+        pos = 0
+        for tok in prompt:
+            logs.append(self.step(tok, pos))
+            pos += 1
+        for _ in range(n_new):
+            nxt = sample_token(logs[-1])
+            out.append(nxt)
+            logs.append(self.step(nxt, pos))
+            pos += 1
+        return out, logs
+
+
+def sample_token(logits):
+    """The first index of the largest of the W real logits (bf16 bits; torch argmax semantics)."""
+    u = np.asarray(logits[:W], np.uint32) << 16
+    return int(np.argmax(u.view(np.float32)))

@@ -85,6 +85,14 @@ class CpuOps:
         v, b = self.view(view), self.view(base)
         return emu.transpose(dst, x, v, v, src_map=b, dst_map=b, src_offset=src_offset, dst_offset=dst_offset)
 
+    def row(self, table, i, t, rows, cols):
+        """Row i of the row-major [rows, cols] table (the gather's closed form: its index picks one
+        row, scatter_gather_tests.rs:3-11)."""
+        n = self.sizes[cols]
+        if not 0 <= i < self.sizes[rows]:
+            raise IndexError("row index past the table")
+        return np.array(table[i * n:(i + 1) * n], copy=True)
+
     def scatter(self, dst, src, index, t, src_map, key, dst_map, scaled):
         k = self.view(key)
         return emu.scatter(dst, src, index, np.dtype(fh.NP_DTYPE[t]).itemsize, self.view(src_map), k,

@@ -157,3 +157,25 @@ def test_layer_step_matches_the_oracle(rt, pos):
         got_cache = ops.get(cs[chunk][side], BF16).reshape(T, -1)
         assert np.array_equal(got_cache[row], ops.get(want_row, BF16))
         assert np.array_equal(np.delete(got_cache, row, axis=0), np.delete(caches[chunk][side].reshape(T, -1), row, axis=0))
+
+
+def test_pipeline_tokens_match_the_oracle(rt):
+    """Pipeline.step (transformer.py:495-566) through the seam ops: two layers of random weights, a
+    tied embedding, a two-token prompt and two greedy tokens, the same token sequence fed to the
+    oracle's pipeline. Each step's logits are bit-exact on at least 99% of the vocabulary and all
+    within max(0.01 |e|, 2^-8) of the oracle's; the greedy token is the oracle's wherever the
+    oracle's best logit leads the next by more than two of its ulps."""
+    from test_oracle_step import tied_model
+    model = tied_model(111, layers=2, zero_layers=False)
+    print("pipeline: 2 layers, 4 steps", flush=True)
+    cpu, gpu = fd.Pipeline(CPU, model), fd.Pipeline(fd.SeamOps(rt, fd.STEP_SIZES), model)
+    prompt, want = [5, 1234], None
+    for pos in range(4):
+        tok = prompt[pos] if pos < len(prompt) else fd.sample_token(want)
+        want, got = cpu.step(tok, pos), gpu.step(tok, pos)
+        w, g = dc.f64(want[:fd.W]), dc.f64(got[:fd.W])
+        assert np.mean(got[:fd.W] == want[:fd.W]) >= 0.99, pos
+        assert np.all(np.abs(g - w) <= np.maximum(0.01 * np.abs(w), 2.0 ** -8)), pos
+        top2 = np.sort(w)[-2:]
+        if top2[1] - top2[0] > 2 * 2.0 ** (np.floor(np.log2(abs(top2[1]))) - 7):
+            assert fd.sample_token(got) == fd.sample_token(want), pos

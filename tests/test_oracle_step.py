@@ -323,3 +323,34 @@ def test_layer_step_edge_positions(pos):
         want = dc.r16(out / (p + np.float32(fd.EPS))[..., None])
         got = dc.f64(st["a"], N, G, D)
         assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 2.0 ** -20)) <= 2 ** -7
+
+
+# ---- the token loop (Pipeline.step, transformer.py:425-566) -----------------------------------------
+
+def tied_model(seed, layers=1, zero_layers=True):
+    """An embedding table of random rows, tied to the lm_head (its first W rows, the padding zero),
+    RMSNorm gains of 1 and layers of zero weights (each then leaves the residual stream as it is)."""
+    rng = np.random.default_rng(seed)
+    embed = emu.f32_to_bf16(rng.standard_normal(fd.W * H).astype(np.float32))
+    lm = np.zeros(fd.WP * H, np.uint16)
+    lm[:fd.W * H] = embed
+    one = lambda n: np.full(n, ONE, np.uint16)
+    zero = lambda n: np.zeros(n, np.uint16)
+    lw = dict(q=zero(fd.Q * H), k=zero(fd.P * H), v=zero(fd.P * H), o=zero(H * fd.Q), up=zero(L * H),
+              gate=zero(L * H), down=zero(H * L), input_norm=one(H), q_norm=one(D), k_norm=one(D), post_norm=one(H))
+    if not zero_layers:
+        lws = [dc.layer_weights(rng) for _ in range(layers)]
+    else:
+        lws = [lw] * layers
+    return dict(embed=embed, layers=lws, final_norm=one(H), lm_head=lm)
+
+
+def test_pipeline_with_identity_layers_repeats_the_last_token():
+    """With zero layer weights every layer leaves the embedding unchanged, so the tied lm_head scores
+    each vocabulary row by its dot product with the normalised embedding of the current token: the
+    token's own row wins, and greedy decoding repeats the prompt's last token."""
+    pipe = fd.Pipeline(OPS, tied_model(110))
+    new, logits = pipe.generate([5, 1234], 2)
+    assert new == [1234, 1234]
+    assert fd.sample_token(logits[0]) == 5
+    assert len(pipe.caches[0]) == 1 and not dc.f64(pipe.caches[0][0][0]).any()  # zero K rows (q, k, v = 0)
