@@ -53,6 +53,24 @@ void* static_scratch(const fo_runtime* rt, uint64_t bytes, const char* what) {
 
 thread_local std::string g_last_error;
 
+}  // namespace
+
+void fo_pool::release(void* ptr, uint64_t capacity) {
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (!orphaned && cached_bytes + capacity <= kMaxCached) {
+      cached.emplace(capacity, ptr);
+      cached_bytes += capacity;
+      return;
+    }
+  }
+  (void)hipSetDevice(device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(ptr);
+}
+
+namespace {
+
 // Pending widens. The engine widens both contraction operands with Backend::map before
 // contraction_prewidened (contract_outer, engine/contraction/outer/mod.rs:145-163), so a
 // contraction over f32 (i32) operands usually reads buffers that are exact casts of bf16 or 8-bit
@@ -246,12 +264,20 @@ void check_rt(fo_runtime* rt) {
   require(rt != nullptr, "runtime is NULL");
   t_rt = rt;
 }
+// The buffer's zero fill has run or is no longer owed.
+void mark_filled(fo_buffer* b) {
+  b->zero_pending = false;
+  if (b->pool) {
+    std::lock_guard<std::mutex> lock(b->pool->mu);
+    b->pool->unfilled.erase(b);
+  }
+}
 void fill_pending(fo_runtime* rt, const fo_buffer* b) {
   if (!b->zero_pending) return;
   fo_buffer* m = const_cast<fo_buffer*>(b);
   FO_HIP(hipSetDevice(rt->device));
   launch_zero(rt->stream, m->ptr, (m->capacity + 15) & ~15ull);
-  m->zero_pending = false;
+  mark_filled(m);
 }
 void check_ptr(const fo_buffer* b, const char* what) {
   require(b != nullptr && b->ptr != nullptr, std::string(what) + " buffer is NULL");
@@ -270,9 +296,72 @@ void check_buf(const fo_buffer* b, const char* what) {
 void claim_out(fo_runtime* rt, fo_buffer* b, uint64_t written) {
   if (!b->zero_pending) return;
   if (written >= b->bytes)
-    b->zero_pending = false;
+    mark_filled(b);
   else
     fill_pending(rt, b);
+}
+
+// The recording open on rt's pool, if any (fo_graph_begin .. fo_graph_end).
+fo_graph_mem* recording(const fo_runtime* rt) { return rt->pool ? rt->pool->recording.get() : nullptr; }
+// Calls that wait for the device cannot be recorded into a graph.
+void not_recording(const fo_runtime* rt, const char* what) {
+  require(recording(rt) == nullptr,
+          std::string(what) + " waits for the device: not allowed while a graph is being recorded");
+}
+
+// Size classes: 512-byte multiples below 1 MiB, 2 MiB multiples above. A free block serves a
+// request of its class, or a large request up to a quarter smaller than the block.
+uint64_t size_class(uint64_t need) {
+  return need < (1ull << 20) ? (need + 511) & ~511ull : (need + (2ull << 20) - 1) & ~((2ull << 20) - 1);
+}
+bool fits(uint64_t block, uint64_t cls) { return block == cls || (cls >= (1ull << 20) && block - block / 4 <= cls); }
+
+// A device block of at least `need` bytes, as (address, capacity): while recording, first from the
+// blocks freed in the recording; then from the runtime's cache; else newly allocated. A block
+// taken while recording joins the recording's memory.
+std::pair<void*, uint64_t> take_block(fo_runtime* rt, uint64_t need) {
+  const uint64_t cls = size_class(need ? need : 1);
+  fo_graph_mem* rec = recording(rt);
+  if (rec) {
+    auto it = rec->reuse.lower_bound(cls);
+    if (it != rec->reuse.end() && fits(it->first, cls)) {
+      std::pair<void*, uint64_t> r{it->second, it->first};
+      rec->reuse.erase(it);
+      return r;  // already one of the recording's blocks
+    }
+  }
+  void* ptr = nullptr;
+  uint64_t cap = 0;
+  {
+    std::lock_guard<std::mutex> lock(rt->pool->mu);
+    auto it = rt->pool->cached.lower_bound(cls);
+    if (it != rt->pool->cached.end() && fits(it->first, cls)) {
+      ptr = it->second;
+      cap = it->first;
+      rt->pool->cached_bytes -= it->first;
+      rt->pool->cached.erase(it);
+    }
+  }
+  if (!ptr) {
+    hipError_t e = hipMalloc(&ptr, cls);
+    if (e != hipSuccess && !rec) {
+      // Release the cache (after the stream drains) and try once more.
+      (void)hipGetLastError();
+      FO_HIP(hipStreamSynchronize(rt->stream));
+      std::lock_guard<std::mutex> lock(rt->pool->mu);
+      for (auto& kv : rt->pool->cached) (void)hipFree(kv.second);
+      rt->pool->cached.clear();
+      rt->pool->cached_bytes = 0;
+      e = hipMalloc(&ptr, cls);
+    }
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      throw OomError("hipMalloc(" + std::to_string(cls) + ") failed: " + hipGetErrorString(e));
+    }
+    cap = cls;
+  }
+  if (rec) rec->blocks.emplace_back(cap, ptr);
+  return {ptr, cap};
 }
 
 void set_device(fo_runtime* rt) { FO_HIP(hipSetDevice(rt->device)); }
@@ -344,6 +433,15 @@ int64_t max_live_offset(const std::vector<fm::Wheel>& ws, int k) {
 
 // The runtime's device scratch, at least `bytes` long (grown after the stream drains).
 void* runtime_scratch(fo_runtime* rt, uint64_t bytes) {
+  if (fo_graph_mem* rec = recording(rt)) {
+    // The recording's own scratch: the eager one may be regrown (freed) while the graph lives.
+    if (rec->scratch_bytes < bytes) {
+      auto blk = take_block(rt, bytes);
+      rec->scratch = blk.first;
+      rec->scratch_bytes = blk.second;
+    }
+    return rec->scratch;
+  }
   if (rt->scratch_bytes < bytes) {
     FO_HIP(hipStreamSynchronize(rt->stream));
     if (rt->scratch) FO_HIP(hipFree(rt->scratch));
@@ -353,6 +451,18 @@ void* runtime_scratch(fo_runtime* rt, uint64_t bytes) {
     rt->scratch_bytes = bytes;
   }
   return rt->scratch;
+}
+
+// Waits for a graph's launches, then destroys it; its memory goes when its last buffer does.
+void destroy_graph(fo_graph* g) {
+  if (g->rt) {
+    (void)hipSetDevice(g->rt->device);
+    (void)hipStreamSynchronize(g->rt->stream);
+    g->rt->graphs.erase(g);
+  }
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
 }
 
 // The runtime's device-visible error word (pinned host memory, written by kernels only when an
@@ -522,11 +632,31 @@ int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
 
 void fo_runtime_free(fo_runtime* rt) {
   if (!rt) return;
+  (void)hipSetDevice(rt->device);
+  if (rt->pool && rt->pool->recording) {  // an open recording is discarded
+    hipGraph_t g = nullptr;
+    (void)hipStreamEndCapture(rt->stream, &g);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipGetLastError();
+    std::lock_guard<std::mutex> lock(rt->pool->mu);
+    rt->pool->recording.reset();
+  }
+  for (fo_graph* g : rt->graveyard) destroy_graph(g);
+  rt->graveyard.clear();
+  // Graphs still held by the caller lose their executables; fo_graph_free then only releases them.
+  for (fo_graph* g : rt->graphs) {
+    (void)hipStreamSynchronize(rt->stream);
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    g->exec = nullptr;
+    g->graph = nullptr;
+    g->rt = nullptr;
+  }
+  rt->graphs.clear();
   try {
     materialize_runtime(rt);
   } catch (const std::exception&) {
   }
-  (void)hipSetDevice(rt->device);
   if (rt->stream) (void)hipStreamSynchronize(rt->stream);
   for (auto& e : rt->events)
     if (e) (void)hipEventDestroy(e);
@@ -552,6 +682,7 @@ void fo_runtime_free(fo_runtime* rt) {
 int32_t fo_runtime_synchronize(fo_runtime* rt) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_runtime_synchronize");
     FO_HIP(hipStreamSynchronize(rt->stream));
     flush_trace(rt);
     raise_device_errors(rt);
@@ -561,6 +692,7 @@ int32_t fo_runtime_synchronize(fo_runtime* rt) {
 int32_t fo_runtime_set_trace(fo_runtime* rt, fo_trace_sink sink, fo_trace_done done, void* ctx) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_runtime_set_trace");
     set_device(rt);
     FO_HIP(hipStreamSynchronize(rt->stream));
     flush_trace(rt);  // spans of the previous sink go to it
@@ -592,44 +724,22 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
     require(out != nullptr, "out is NULL");
     *out = nullptr;
     set_device(rt);
-    // Size classes: 512-byte multiples below 1 MiB, 2 MiB multiples above. A cached block serves
-    // a request of its class, or a large request up to a quarter smaller than the block.
-    const uint64_t need = bytes ? bytes : 1;
-    const uint64_t cls = need < (1ull << 20) ? (need + 511) & ~511ull : (need + (2ull << 20) - 1) & ~((2ull << 20) - 1);
     auto b = std::make_unique<fo_buffer>();
     b->bytes = bytes;
     b->device = rt->device;
     b->pool = rt->pool;
-    {
-      std::lock_guard<std::mutex> lock(rt->pool->mu);
-      auto it = rt->pool->cached.lower_bound(cls);
-      if (it != rt->pool->cached.end() && (it->first == cls || (cls >= (1ull << 20) && it->first - it->first / 4 <= cls))) {
-        b->ptr = it->second;
-        b->capacity = it->first;
-        rt->pool->cached_bytes -= it->first;
-        rt->pool->cached.erase(it);
-      }
-    }
-    if (!b->ptr) {
-      hipError_t e = hipMalloc(&b->ptr, cls);
-      if (e != hipSuccess) {
-        // Release the cache (after the stream drains) and try once more.
-        (void)hipGetLastError();
-        FO_HIP(hipStreamSynchronize(rt->stream));
-        std::lock_guard<std::mutex> lock(rt->pool->mu);
-        for (auto& kv : rt->pool->cached) (void)hipFree(kv.second);
-        rt->pool->cached.clear();
-        rt->pool->cached_bytes = 0;
-        e = hipMalloc(&b->ptr, cls);
-      }
-      if (e != hipSuccess)
-        throw OomError("hipMalloc(" + std::to_string(cls) + ") failed: " + hipGetErrorString(e));
-      b->capacity = cls;
-    }
+    auto blk = take_block(rt, bytes);
+    b->ptr = blk.first;
+    b->capacity = blk.second;
+    b->graph_mem = rt->pool->recording;  // null unless a graph is being recorded
     // Zero-filled (Backend::zeroed), the fill deferred to the first use (check_buf / claim_out). It
     // then runs on that op's runtime stream, after every earlier op of the runtime, including a
     // reuse's previous owner's last reads.
     b->zero_pending = true;
+    {
+      std::lock_guard<std::mutex> lock(rt->pool->mu);
+      rt->pool->unfilled.insert(b.get());
+    }
     *out = b.release();
   });
 }
@@ -640,21 +750,33 @@ void fo_buffer_free(fo_buffer* buf) {
     forget_buffer(buf);
   } catch (const std::exception&) {  // a failed launch leaves the error for the next call to report
   }
+  std::shared_ptr<fo_graph_mem> rec;
+  if (buf->pool) {
+    std::lock_guard<std::mutex> lock(buf->pool->mu);
+    buf->pool->unfilled.erase(buf);
+    rec = buf->pool->recording;
+  }
   if (buf->ptr) {
-    bool direct = true;
-    if (buf->pool) {
-      std::lock_guard<std::mutex> lock(buf->pool->mu);
-      if (!buf->pool->orphaned && buf->pool->cached_bytes + buf->capacity <= fo_pool::kMaxCached) {
-        buf->pool->cached.emplace(buf->capacity, buf->ptr);
-        buf->pool->cached_bytes += buf->capacity;
-        direct = false;
+    if (rec) {
+      // Freed while recording: the graph may touch the block, so it stays with the recording's
+      // memory; later allocations of the recording reuse it unless an earlier graph owns it.
+      if (buf->graph_mem == rec) {
+        rec->reuse.emplace(buf->capacity, buf->ptr);
+      } else if (buf->graph_mem) {
+        rec->keep.push_back(buf->graph_mem);
+      } else {
+        rec->blocks.emplace_back(buf->capacity, buf->ptr);
+        rec->reuse.emplace(buf->capacity, buf->ptr);
       }
-    }
-    if (direct) {
-      (void)hipSetDevice(buf->device);
-      (void)hipDeviceSynchronize();
-      (void)hipFree(buf->ptr);
-    }
+    } else if (!buf->graph_mem) {
+      if (buf->pool) {
+        buf->pool->release(buf->ptr, buf->capacity);
+      } else {
+        (void)hipSetDevice(buf->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(buf->ptr);
+      }
+    }  // else the block is its recording's, returned when that memory's last holder goes
   }
   delete buf;
 }
@@ -667,7 +789,7 @@ int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out) {
     fo_buffer* b = nullptr;
     int32_t st = fo_buffer_alloc(rt, src->bytes, &b);
     if (st != FO_OK) throw OomError(g_last_error);
-    b->zero_pending = false;  // every byte is copied
+    mark_filled(b);  // every byte is copied
     FO_HIP(hipMemcpyAsync(b->ptr, src->ptr, src->bytes, hipMemcpyDeviceToDevice, rt->stream));
     *out = b;
   });
@@ -678,6 +800,7 @@ uint64_t fo_buffer_bytes(const fo_buffer* buf) { return buf ? buf->bytes : 0; }
 int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_write");
     check_ptr(dst, "dst");
     note_write(dst);
     require(host != nullptr || bytes == 0, "host pointer is NULL");
@@ -693,6 +816,7 @@ int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* ds
 int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_read");
     check_buf(src, "src");
     require(host != nullptr || bytes == 0, "host pointer is NULL");
     require(bytes <= src->bytes, "read of " + std::to_string(bytes) + " bytes exceeds the buffer");
@@ -707,6 +831,7 @@ int32_t fo_read(fo_runtime* rt, const fo_buffer* src, void* host, uint64_t bytes
 int32_t fo_event_record(fo_runtime* rt, int32_t slot) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_event_record");
     require(slot >= 0 && slot < 16, "event slot out of range");
     FO_HIP(hipEventRecord(rt->events[slot], rt->stream));
   });
@@ -715,11 +840,112 @@ int32_t fo_event_record(fo_runtime* rt, int32_t slot) {
 int32_t fo_event_elapsed_ms(fo_runtime* rt, int32_t start, int32_t end, float* ms) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_event_elapsed_ms");
     require(start >= 0 && start < 16 && end >= 0 && end < 16, "event slot out of range");
     require(ms != nullptr, "ms is NULL");
     FO_HIP(hipEventSynchronize(rt->events[end]));
     FO_HIP(hipEventElapsedTime(ms, rt->events[start], rt->events[end]));
   });
+}
+
+// ---- recorded op streams -----------------------------------------------------------------------
+
+int32_t fo_graph_begin(fo_runtime* rt) {
+  return guard([&] {
+    check_rt(rt);
+    require(recording(rt) == nullptr, "a graph is already being recorded on this runtime");
+    require(rt->trace_sink == nullptr, "trace spans are not recorded into graphs: clear the trace sink first");
+    set_device(rt);
+    // Everything owed to buffers that exist now runs eagerly, outside the graph: a launch must not
+    // zero a cache that earlier launches filled, or redo a cast whose source has changed since.
+    materialize_runtime(rt);
+    std::vector<fo_buffer*> unfilled;
+    {
+      std::lock_guard<std::mutex> lock(rt->pool->mu);
+      unfilled.assign(rt->pool->unfilled.begin(), rt->pool->unfilled.end());
+    }
+    for (fo_buffer* b : unfilled) fill_pending(rt, b);
+    (void)error_word(rt);
+    auto mem = std::make_shared<fo_graph_mem>();
+    mem->pool = rt->pool;
+    FO_HIP(hipStreamBeginCapture(rt->stream, hipStreamCaptureModeRelaxed));
+    rt->err_ops_saved = rt->err_ops;
+    rt->err_ops = 0;
+    std::lock_guard<std::mutex> lock(rt->pool->mu);
+    rt->pool->recording = std::move(mem);
+  });
+}
+
+int32_t fo_graph_end(fo_runtime* rt, fo_graph** out) {
+  return guard([&] {
+    check_rt(rt);
+    require(out != nullptr, "out is NULL");
+    *out = nullptr;
+    require(recording(rt) != nullptr, "no graph is being recorded on this runtime");
+    set_device(rt);
+    // Casts deferred while recording whose outputs are still alive belong to the graph.
+    std::string failure;
+    try {
+      materialize_runtime(rt);
+    } catch (const std::exception& e) {
+      failure = e.what();
+    }
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(rt->stream, &graph);
+    std::shared_ptr<fo_graph_mem> mem;
+    {
+      std::lock_guard<std::mutex> lock(rt->pool->mu);
+      mem = std::move(rt->pool->recording);
+      rt->pool->recording.reset();
+    }
+    const uint32_t err_ops = rt->err_ops;
+    rt->err_ops = rt->err_ops_saved;
+    for (fo_graph* g : rt->graveyard) destroy_graph(g);
+    rt->graveyard.clear();
+    if (e != hipSuccess || graph == nullptr || !failure.empty()) {
+      if (graph) (void)hipGraphDestroy(graph);
+      (void)hipGetLastError();
+      throw HipError(!failure.empty() ? failure
+                                      : std::string("recording failed: hipStreamEndCapture: ") + hipGetErrorString(e));
+    }
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ie = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      (void)hipGraphDestroy(graph);
+      throw HipError(std::string("hipGraphInstantiate failed: ") + hipGetErrorString(ie));
+    }
+    auto* g = new fo_graph();
+    g->rt = rt;
+    g->graph = graph;
+    g->exec = exec;
+    g->mem = std::move(mem);
+    g->err_ops = err_ops;
+    rt->graphs.insert(g);
+    *out = g;
+  });
+}
+
+int32_t fo_graph_launch(fo_runtime* rt, fo_graph* graph) {
+  return guard([&] {
+    check_rt(rt);
+    require(graph != nullptr, "graph is NULL");
+    require(graph->rt == rt && graph->exec != nullptr, "the graph was not recorded on this runtime");
+    require(recording(rt) == nullptr, "a graph cannot be launched while one is being recorded");
+    set_device(rt);
+    materialize_runtime(rt);  // casts deferred since, which the graph may read
+    TraceScope trace_span(rt, "graph");
+    FO_HIP(hipGraphLaunch(graph->exec, rt->stream));
+    rt->err_ops |= graph->err_ops;
+  });
+}
+
+void fo_graph_free(fo_graph* graph) {
+  if (!graph) return;
+  if (graph->rt && recording(graph->rt)) {  // no waiting on a stream that is recording
+    graph->rt->graveyard.push_back(graph);
+    return;
+  }
+  destroy_graph(graph);
 }
 
 // ---- mapping utilities -------------------------------------------------------------------------
@@ -1102,8 +1328,16 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     TraceScope trace_span(rt, "scatter");
     int32_t* flag = error_word(rt);
     // Winner words: grown (and zeroed) when too short, and zeroed again when the 32-bit generation
-    // wraps; otherwise each call only takes the next generation.
-    if (rt->scatter_win_slots < (uint64_t)axis_size || rt->scatter_gen == UINT32_MAX) {
+    // wraps; otherwise each call only takes the next generation. A recorded scatter has words of its
+    // own, cleared by a kernel in the graph, so every launch starts from a clean generation.
+    uint64_t* win = rt->scatter_win;
+    uint32_t gen = 0;
+    if (recording(rt)) {
+      auto blk = take_block(rt, (uint64_t)axis_size * 8);
+      launch_zero(rt->stream, blk.first, blk.second);
+      win = (uint64_t*)blk.first;
+      gen = 1;
+    } else if (rt->scatter_win_slots < (uint64_t)axis_size || rt->scatter_gen == UINT32_MAX) {
       FO_HIP(hipStreamSynchronize(rt->stream));
       if (rt->scatter_win_slots < (uint64_t)axis_size) {
         if (rt->scatter_win) FO_HIP(hipFree(rt->scatter_win));
@@ -1115,11 +1349,14 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
       FO_HIP(hipMemsetAsync(rt->scatter_win, 0, (size_t)rt->scatter_win_slots * 8, rt->stream));
       rt->scatter_gen = 0;
     }
-    const uint32_t gen = ++rt->scatter_gen;
+    if (!gen) {
+      gen = ++rt->scatter_gen;
+      win = rt->scatter_win;
+    }
     const int mem[1] = {0};
     launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,
-                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd),
-                   rt->scatter_win, gen, flag);
+                   to_desc<1>(ws, mem), to_desc<1>(wd, mem), inner_part_wheels(ws), inner_part_wheels(wd), win, gen,
+                   flag);
     rt->err_ops |= 2;
   });
 }
@@ -1553,6 +1790,7 @@ int32_t fo_safetensors_load(fo_runtime* rt, fo_buffer* dst, const char* path, co
                             const char* element_map) {
   return guard([&] {
     check_rt(rt);
+    not_recording(rt, "fo_safetensors_load");
     check_buf(dst, "dst");
     note_write(dst);
     require(path != nullptr && name != nullptr && element_map != nullptr, "safetensors: NULL argument");

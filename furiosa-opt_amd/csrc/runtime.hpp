@@ -10,6 +10,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/furiosa_hip.h"
@@ -21,6 +22,8 @@
 // work enqueued with the old owner completes before any work of the new one starts, so neither
 // the free nor the reuse waits for the device. A pool outlives its runtime while buffers of it
 // remain; those then release their blocks directly.
+struct fo_graph_mem;
+struct fo_buffer;
 struct fo_pool {
   std::mutex mu;
   int device = 0;
@@ -28,6 +31,27 @@ struct fo_pool {
   std::multimap<uint64_t, void*> cached;  // free blocks by capacity
   uint64_t cached_bytes = 0;
   static constexpr uint64_t kMaxCached = 8ull << 30;
+  std::unordered_set<fo_buffer*> unfilled;  // live buffers whose deferred zero fill has not run
+  std::shared_ptr<fo_graph_mem> recording;  // set while the runtime records a graph
+  // Returns a block to the cache, or frees it (after the device drains) when the cache is full or
+  // the runtime is gone.
+  void release(void* ptr, uint64_t capacity);
+};
+
+// The device blocks a recorded graph's kernels touch: every block handed out while recording
+// (outputs, intermediates, scratch, scatter winner words) and the blocks of buffers freed while
+// recording. They stay out of the pool's cache while the graph or any buffer born in the recording
+// lives, so a launch never writes memory that another buffer holds; the last holder returns them.
+struct fo_graph_mem {
+  std::shared_ptr<fo_pool> pool;
+  std::vector<std::pair<uint64_t, void*>> blocks;       // (capacity, address), each once
+  std::multimap<uint64_t, void*> reuse;                 // freed while recording: later allocations take them
+  std::vector<std::shared_ptr<fo_graph_mem>> keep;      // earlier recordings' blocks freed in this one
+  void* scratch = nullptr;                              // the recording's op scratch (grown by new blocks)
+  uint64_t scratch_bytes = 0;
+  ~fo_graph_mem() {
+    for (auto& b : blocks) pool->release(b.second, b.first);
+  }
 };
 
 struct fo_runtime {
@@ -58,6 +82,18 @@ struct fo_runtime {
     hipEvent_t begin, end;
   };
   std::vector<Span> spans;
+  uint32_t err_ops_saved = 0;  // err_ops of the eager stream while a graph is recorded
+  std::vector<struct fo_graph*> graveyard;  // graphs freed while recording, destroyed when it ends
+  std::unordered_set<struct fo_graph*> graphs;  // live graphs recorded on this runtime
+};
+
+// A recorded op stream (fo_graph_begin .. fo_graph_end), launched as one HIP graph.
+struct fo_graph {
+  fo_runtime* rt = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::shared_ptr<fo_graph_mem> mem;
+  uint32_t err_ops = 0;  // device error checks its launches owe the next synchronize
 };
 
 struct fo_buffer {
@@ -72,6 +108,9 @@ struct fo_buffer {
   // An exact widening cast into this buffer recorded but not yet run (the runtime's pending
   // widens): a read runs it first.
   bool widen_pending = false;
+  // Born while a graph was recorded: the block belongs to that recording's memory, not to the
+  // pool, and outlives this buffer while the graph lives.
+  std::shared_ptr<fo_graph_mem> graph_mem;
 };
 
 namespace fo {

@@ -88,6 +88,10 @@ _sig = {
     "fo_read": (C.c_int32, [_P, _P, _P, C.c_uint64]),
     "fo_event_record": (C.c_int32, [_P, C.c_int32]),
     "fo_event_elapsed_ms": (C.c_int32, [_P, C.c_int32, C.c_int32, C.POINTER(C.c_float)]),
+    "fo_graph_begin": (C.c_int32, [_P]),
+    "fo_graph_end": (C.c_int32, [_P, C.POINTER(_P)]),
+    "fo_graph_launch": (C.c_int32, [_P, _P]),
+    "fo_graph_free": (None, [_P]),
     "fo_mapping_parse": (C.c_int64, [C.c_char_p, C.c_char_p, C.c_char_p, C.c_uint64]),
     "fo_mapping_sequence": (
         C.c_int32,
@@ -228,6 +232,15 @@ class Runtime:
     def record(self, slot: int):
         _check(_lib.fo_event_record(self.h, slot))
 
+    def graph_begin(self):
+        """Ops issued from here to graph_end() are recorded into a graph instead of running."""
+        _check(_lib.fo_graph_begin(self.h))
+
+    def graph_end(self) -> "Graph":
+        h = _P()
+        _check(_lib.fo_graph_end(self.h, C.byref(h)))
+        return Graph(self, h)
+
     def elapsed_ms(self, a: int, b: int) -> float:
         ms = C.c_float()
         _check(_lib.fo_event_elapsed_ms(self.h, a, b, C.byref(ms)))
@@ -353,6 +366,28 @@ class Buffer:
         out = np.empty(n, dtype=dt)
         _check(_lib.fo_read(self.rt.h, self.h, out.ctypes.data, out.nbytes))
         return out
+
+
+class Graph:
+    """A recorded op stream (fo_graph_begin .. fo_graph_end); launch() runs it on the runtime's stream."""
+
+    def __init__(self, rt: Runtime, h):
+        self.rt = rt  # the runtime outlives its graphs
+        self.h = h
+
+    def launch(self):
+        _check(_lib.fo_graph_launch(self.rt.h, self.h))
+
+    def free(self):
+        if self.h:
+            _lib.fo_graph_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 def safetensors_info(path: str, name: str):

@@ -171,11 +171,12 @@ class SeamOps:
 
     def row(self, table, i, t, rows, cols):
         """Row i of a [rows, cols] table: a gather of one index (the indexed axis `rows`, the
-        payload `cols`) into a fresh [cols]."""
+        payload `cols`) into a fresh [cols]. `i` is an int or a resident i32 [1]."""
         self.calls += 1
         out = self._alloc(self._size(cols), t)
-        self.rt.gather(out, self.put(table), self.put(np.array([i], np.int32)), t, self.view(f"{rows}, {cols}"),
-                       self.view(f"X, {cols}"), self.view("X"), False)
+        idx = i if isinstance(i, Buffer) else self.put(np.array([i], np.int32))
+        self.rt.gather(out, self.put(table), idx, t, self.view(f"{rows}, {cols}"), self.view(f"X, {cols}"),
+                       self.view("X"), False)
         return out
 
     def scatter(self, dst, src, index, t, src_map, key, dst_map, scaled):
@@ -351,8 +352,9 @@ def rope(ops, x, cos, sin, rows):
 def cache_row(ops, cache, row, offset):
     """dma_scatter::<m![1]> of one [N, D] row into a [T, N, D] cache (projection.rs:111, rope.rs:175):
     the key axis is the unit mapping, the indexed axis T, and `offset` the row's byte offset
-    (row index * ROW_STRIDE_ND, transformer.py:432-435). Returns the updated cache."""
-    idx = np.array([offset], np.int32)
+    (row index * ROW_STRIDE_ND, transformer.py:432-435), an int or a resident i32 [1]. Returns the
+    updated cache."""
+    idx = offset if isinstance(offset, Buffer) else np.array([offset], np.int32)
     return ops.scatter(ops.put(cache), row, idx, BF16, "N, D", "1", "T, N, D", scaled=True)
 
 
@@ -420,17 +422,17 @@ def causal_mask(row):
     return m_
 
 
-def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None, masks=None):
+def layer_step(ops, x, lw, pos, caches, cos, sin, stages=None, masks=None, offset=None):
     """One layer of Pipeline.step (transformer.py:495-562) for the token at absolute position pos:
     projection into the cache of chunk pos // T at row pos % T, attention over chunks 0..pos // T
     (the last one causal), decoder. `lw` holds the layer's weights by the names of mod.rs; `caches`
     a list of (k, v) per chunk, updated. `masks`, when given, are the chunks' masks already resident
-    (the pipeline hoists them out of its layer loop, transformer.py:437-450). Returns the new
-    residual stream."""
+    (the pipeline hoists them out of its layer loop, transformer.py:437-450); `offset`, when given,
+    the cache row's byte offset already resident. Returns the new residual stream."""
     chunk, row = divmod(pos, T)
     kc, vc = caches[chunk]
     q, kc, vc = projection(ops, x, lw["q"], lw["k"], lw["v"], lw["input_norm"], lw["q_norm"], lw["k_norm"],
-                           row * ROW_STRIDE_ND, cos, sin, kc, vc, stages)
+                           row * ROW_STRIDE_ND if offset is None else offset, cos, sin, kc, vc, stages)
     caches[chunk] = (kc, vc)
     if masks is None:
         full = ops.put(np.ones(T, np.float32))
@@ -455,14 +457,26 @@ class Pipeline:
     (sample_token, transformer.py:489-490: the first index of the largest). `model` holds `embed`
     [W, H], `layers` (dicts of layer_step's weight names), `final_norm` [H] and `lm_head` [Wp, H],
     as bf16 bits or resident buffers. The KV caches are created zeroed per (layer, chunk), the masks
-    and RoPE rows per position, as the reference's pipeline hoists them."""
+    and RoPE rows per position, as the reference's pipeline hoists them.
 
-    def __init__(self, ops, model):
+    With `graphs` (SeamOps only), the first token of each chunk count records the whole step (every
+    seam call of the embedding, the layers and the final layer) into one graph, and every token of
+    that chunk count launches it: the per-token inputs (token id, cache row offset, RoPE row, causal
+    mask) sit in resident buffers that are rewritten before each launch, and everything else a
+    step reads (weights, caches, the full mask) stays where it was when recorded. This is the
+    NPU's compile-once, launch-per-call model (runtime.rs:157-177) on HIP graphs."""
+
+    def __init__(self, ops, model, graphs=False):
         self.ops = ops
         self.model = {k: (ops.put(v) if k != "layers" else [{n: ops.put(w) for n, w in lw.items()} for lw in v])
                       for k, v in model.items()}
         self.caches = [[] for _ in self.model["layers"]]
         self.full = ops.put(np.ones(T, np.float32))
+        self.graphs = {} if graphs else None  # chunk -> (graph, its logits buffer)
+        if graphs:
+            self.inputs = dict(token=ops.put(np.zeros(1, np.int32)), offset=ops.put(np.zeros(1, np.int32)),
+                               cos=ops.put(np.zeros(D, np.uint16)), sin=ops.put(np.zeros(D, np.uint16)),
+                               mask=ops.put(np.zeros(T, np.float32)))
 
     def _cache(self, layer, chunk):
         cs = self.caches[layer]
@@ -470,18 +484,45 @@ class Pipeline:
             cs.append((self.ops.zeros("T, N, D", BF16), self.ops.zeros("T, N, D", BF16)))
         return cs
 
+    def _forward(self, token, pos, cos, sin, mask, offset):
+        """The seam calls of one token; returns the logits buffer."""
+        ops = self.ops
+        chunk = pos // T
+        masks = [self.full] * chunk + [mask]
+        x = embedding(ops, self.model["embed"], token)
+        for layer, lw in enumerate(self.model["layers"]):
+            x = layer_step(ops, x, lw, pos, self._cache(layer, chunk), cos, sin, masks=masks, offset=offset)
+        return final_layer(ops, x, self.model["final_norm"], self.model["lm_head"])
+
     def step(self, token, pos):
         """Runs one token at absolute position pos; returns the logits [Wp] as bf16 bits."""
         ops = self.ops
         chunk, row = divmod(pos, T)
-        cos, sin = (ops.put(t) for t in rope_row(pos))
-        masks = [self.full] * chunk + [ops.put(causal_mask(row))]
-        x = embedding(ops, self.model["embed"], token)
-        for layer, lw in enumerate(self.model["layers"]):
-            cs = self._cache(layer, chunk)
-            x = layer_step(ops, x, lw, pos, cs, cos, sin, masks=masks)
-        logits = final_layer(ops, x, self.model["final_norm"], self.model["lm_head"])
-        return ops.get(logits, BF16)
+        cos, sin = rope_row(pos)
+        if self.graphs is None:
+            logits = self._forward(token, pos, ops.put(cos), ops.put(sin), ops.put(causal_mask(row)),
+                                   row * ROW_STRIDE_ND)
+            return ops.get(logits, BF16)
+        inp = self.inputs
+        for name, v in (("token", np.array([token], np.int32)), ("offset", np.array([row * ROW_STRIDE_ND], np.int32)),
+                        ("cos", cos), ("sin", sin), ("mask", causal_mask(row))):
+            inp[name].write(v)
+        rec = self.graphs.get(chunk)
+        if rec is None:
+            for layer in range(len(self.model["layers"])):
+                self._cache(layer, chunk)  # created, and zeroed, before the recording
+            ops.rt.graph_begin()
+            try:
+                logits = self._forward(inp["token"], pos, inp["cos"], inp["sin"], inp["mask"], inp["offset"])
+            except BaseException:
+                try:
+                    ops.rt.graph_end().free()
+                except RuntimeError:
+                    pass
+                raise
+            rec = self.graphs[chunk] = (ops.rt.graph_end(), logits)
+        rec[0].launch()
+        return ops.get(rec[1], BF16)
 
     def generate(self, prompt, n_new):
         """Every prompt token in turn, then n_new greedy tokens; returns (new tokens, each step's
