@@ -41,23 +41,37 @@ __global__ void __launch_bounds__(kBlock) k_relayout(T* __restrict__ dst, const 
       off += (int64_t)digit[i] * w.stride[0][i];
       q = nq;
     }
+    // The run's source offsets are walked first and its reads issued together after a scheduling
+    // barrier (a dead or past-the-end position reads element 0, which every non-empty buffer holds,
+    // and writes nothing), so a run costs one memory latency rather than one per element.
+    int64_t at[RUN];
+    bool st[RUN];
+#pragma unroll
     for (int r = 0; r < RUN; ++r) {
-      uint32_t p = p0 + r;
-      if (p >= count) break;
-      bool live = true;
+      const bool in = p0 + r < count;
+      bool live = in;
       for (int i = 0; i < w.n; ++i) live &= digit[i] < w.live[i];
-      if (live) dst[dst_base + p] = src[src_base + off];
-      // tick
-      for (int i = 0; i < w.n; ++i) {
-        if (digit[i] + 1 < w.size[i]) {
-          digit[i] += 1;
-          off += w.stride[0][i];
-          break;
+      st[r] = live;
+      at[r] = live ? src_base + off : 0;
+      if (in) {  // tick
+        for (int i = 0; i < w.n; ++i) {
+          if (digit[i] + 1 < w.size[i]) {
+            digit[i] += 1;
+            off += w.stride[0][i];
+            break;
+          }
+          off -= (int64_t)digit[i] * w.stride[0][i];
+          digit[i] = 0;
         }
-        off -= (int64_t)digit[i] * w.stride[0][i];
-        digit[i] = 0;
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    T v[RUN];
+#pragma unroll
+    for (int r = 0; r < RUN; ++r) v[r] = src[at[r]];
+#pragma unroll
+    for (int r = 0; r < RUN; ++r)
+      if (st[r]) dst[dst_base + p0 + r] = v[r];
   }
 }
 
@@ -700,8 +714,12 @@ constexpr int kBatch = 16;
 
 // One tick of an odometer over wheels w (innermost first): the digits and the offsets into each
 // of the NMEM memories advance to the next position.
+// The digits are indexed by a runtime wheel count, so they may live in indexed registers; an
+// indexed register access makes the compiler wait for every load in flight. Batched readers
+// therefore compute a batch's offsets first and issue its loads after a scheduling barrier.
 template <int NMEM>
-__device__ __forceinline__ void odometer_step(const Wheels<NMEM>& w, uint32_t* digit, int64_t (&off)[NMEM]) {
+__device__ __forceinline__ void odometer_step(const Wheels<NMEM>& w, uint32_t (&digit)[kMaxWheels],
+                                              int64_t (&off)[NMEM]) {
   for (int i = 0; i < w.n; ++i) {
     if (digit[i] + 1 < w.size[i]) {
       digit[i]++;
@@ -712,6 +730,21 @@ __device__ __forceinline__ void odometer_step(const Wheels<NMEM>& w, uint32_t* d
 #pragma unroll
     for (int k = 0; k < NMEM; ++k) off[k] -= (int64_t)digit[i] * w.stride[k][i];
     digit[i] = 0;
+  }
+}
+
+// The odometer at stream position pos: digits and the offsets added to `off`.
+template <int NMEM>
+__device__ __forceinline__ void odometer_seek(const Wheels<NMEM>& w, uint32_t pos, uint32_t (&digit)[kMaxWheels],
+                                              int64_t (&off)[NMEM]) {
+  for (int i = 0; i < kMaxWheels; ++i) digit[i] = 0;
+  uint32_t q = pos;
+  for (int i = 0; i < w.n; ++i) {
+    const uint32_t nq = w.div[i].div(q);
+    digit[i] = q - nq * w.size[i];
+#pragma unroll
+    for (int k = 0; k < NMEM; ++k) off[k] += (int64_t)digit[i] * w.stride[k][i];
+    q = nq;
   }
 }
 
@@ -771,13 +804,17 @@ __global__ void __launch_bounds__(kBlock) k_reduce_thread(void* dst, const void*
     for (uint32_t r0 = 0; r0 < total; r0 += kBatch) {
       decltype(R::load(src, 0)) v[kBatch];
       bool ok[kBatch];
+      int64_t at[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const bool in = r0 + u < total;
         ok[u] = in && off[0] >= 0 && off[0] < src_len;
-        v[u] = ok[u] ? R::load(src, off[0]) : R::from_bits(0);
+        at[u] = ok[u] ? off[0] : 0;
         if (in) odometer_step(rw, digit, off);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = R::load(src, at[u]);  // all reads in flight together
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
         if (ok[u]) acc = R::apply(op, acc, v[u]);
@@ -925,25 +962,23 @@ __global__ void __launch_bounds__(64 * kSeg) k_reduce_cols(void* dst, const void
   const uint32_t r_begin = min(total, (uint32_t)seg * len), r_end = min(total, r_begin + len);
   if (!dead && r_begin < r_end) {
     // the odometer at r_begin
-    uint32_t digit[kMaxWheels] = {};
+    uint32_t digit[kMaxWheels];
     int64_t off[1] = {b[0]};
-    uint32_t q = r_begin;
-    for (int i = 0; i < rw.n; ++i) {
-      const uint32_t nq = rw.div[i].div(q);
-      digit[i] = q - nq * rw.size[i];
-      off[0] += (int64_t)digit[i] * rw.stride[0][i];
-      q = nq;
-    }
+    odometer_seek(rw, r_begin, digit, off);
     for (uint32_t r0 = r_begin; r0 < r_end; r0 += kBatch) {
       V v[kBatch];
       bool ok[kBatch];
+      int64_t at[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const bool in = r0 + u < r_end;
         ok[u] = in && off[0] >= 0 && off[0] < src_len;
-        v[u] = ok[u] ? R::load(src, off[0]) : R::from_bits(0);
+        at[u] = ok[u] ? off[0] : 0;
         if (in) odometer_step(rw, digit, off);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) v[u] = R::load(src, at[u]);  // all reads in flight together
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
         if (ok[u]) acc = R::apply(op, acc, v[u]);
@@ -994,15 +1029,9 @@ __global__ void __launch_bounds__(256) k_reduce_cols4(void* __restrict__ partial
   const uint32_t wlen = (chunk_len + 3) / 4;
   const uint32_t r_begin = min(c1, c0 + wave * wlen), r_end = min(c1, r_begin + wlen);
   if (!dead && r_begin < r_end) {
-    uint32_t digit[kMaxWheels] = {};
+    uint32_t digit[kMaxWheels];
     int64_t off[1] = {b[0]};
-    uint32_t q = r_begin;
-    for (int i = 0; i < rw.n; ++i) {
-      const uint32_t nq = rw.div[i].div(q);
-      digit[i] = q - nq * rw.size[i];
-      off[0] += (int64_t)digit[i] * rw.stride[0][i];
-      q = nq;
-    }
+    odometer_seek(rw, r_begin, digit, off);
     const V4* s4 = (const V4*)src;
     uint32_t r = r_begin;
     for (; r + 8 <= r_end; r += 8) {
@@ -1320,15 +1349,20 @@ __global__ void __launch_bounds__(kBlock) k_contract_generic(Out* __restrict__ o
     for (uint32_t r0 = 0; r0 < total; r0 += kBatch) {
       In va[kBatch], vb[kBatch];
       bool ok[kBatch];
+      int64_t al[kBatch], ar[kBatch];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const bool in = r0 + u < total;
         ok[u] = in && off[0] < lhs_len && off[1] < rhs_len;
-        if (ok[u]) {
-          va[u] = lhs[off[0]];
-          vb[u] = rhs[off[1]];
-        }
+        al[u] = ok[u] ? off[0] : 0;
+        ar[u] = ok[u] ? off[1] : 0;
         if (in) odometer_step(rw, digit, off);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {  // all reads in flight together
+        va[u] = lhs[al[u]];
+        vb[u] = rhs[ar[u]];
       }
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)

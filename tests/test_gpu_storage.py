@@ -718,6 +718,47 @@ def test_contraction_gemv_exact(rt, case, types):
     assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
 
 
+def special_bf16(rng, n):
+    """bf16 bits of N(0, 1) values with a twentieth each of bf16 subnormals (which the reference widen
+    reads as zero), signed zeros, values near 2^-70 (whose products are f32 subnormals, kept by the
+    reference's f32 arithmetic) and values near 2^40."""
+    v = rng.standard_normal(n).astype(np.float32)
+    kind = rng.integers(0, 20, n)
+    v[kind == 1] *= np.float32(2.0 ** -70)
+    v[kind == 2] *= np.float32(2.0 ** 40)
+    bits = emu.f32_to_bf16(v)
+    sub = kind == 3
+    bits[sub] = (rng.integers(1, 0x80, sub.sum()) | (rng.integers(0, 2, sub.sum()) << 15)).astype(np.uint16)
+    zero = kind == 4
+    bits[zero] = (rng.integers(0, 2, zero.sum()) << 15).astype(np.uint16)
+    return bits
+
+
+@pytest.mark.parametrize("sizes", [dict(N=300, K=1000), dict(N=70, K=4104)], ids=["fold", "staged"])
+@pytest.mark.parametrize("out_t", [F32, BF16])
+def test_contraction_gemv_special_values(rt, sizes, out_t):
+    """Both GEMV kernels (K up to 4096: products in LDS; beyond: rows staged and folded together) on
+    operands holding bf16 subnormals, signed zeros and values whose products and partial sums are
+    f32 subnormals: bit-exact against the oracle's fold."""
+    rng = np.random.default_rng(23)
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in ("K", "N, K", "N, K", "N"))
+    lhs, rhs = special_bf16(rng, sizes["K"]), special_bf16(rng, sizes["N"] * sizes["K"])
+    # four rows nonzero only where x is near 2^-70, with weights near 2^-70: every product and partial
+    # sum of their folds is an f32 subnormal
+    small = np.abs(emu.bf16_to_f32(lhs)) < 2.0 ** -60
+    tiny = rhs.reshape(sizes["N"], sizes["K"])[:4]
+    tiny[:] = 0
+    tiny[:, small] = emu.f32_to_bf16(rng.standard_normal((4, int(small.sum()))).astype(np.float32) * np.float32(2.0 ** -70))
+    want = emu.contraction(lhs, rhs, BF16, out_t, lo, ro, po, oo)
+    if out_t == F32:
+        assert np.all((want[:4] != 0) & (np.abs(want[:4]) < 2.0 ** -126))  # the case is exercised
+    print(f"gemv special {sizes} out {out_t}", flush=True)
+    out = rt.alloc(mr.size(oo) * (4 if out_t == F32 else 2))
+    maps = [fh.m(t, **sizes) for t in ("K", "N, K", "N, K", "N")]
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), BF16, out_t, *maps)
+    assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
+
+
 # ---- transmute --------------------------------------------------------------------------------------
 
 
