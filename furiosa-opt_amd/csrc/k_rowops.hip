@@ -138,7 +138,9 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, ui
 constexpr int waitcnt_vm0 = (0 & 15) | (7 << 4) | (15 << 8);  // vmcnt(0); lgkmcnt, expcnt left alone
 constexpr int waitcnt_lgkm0 = 15 | (7 << 4) | (0 << 8) | (3 << 14);  // lgkmcnt(0); vmcnt left alone
 
-constexpr int kDmaWaves = 8;  // waves per block (they share the staged gain)
+// Waves per block, sharing the staged gain: one block of sixteen fills a CU (144 KiB of LDS). Two
+// blocks of eight per CU measured 4% slower on the 8192 x 4096 config.
+constexpr int kDmaWaves = 16;
 template <int NCH>
 __global__ void __launch_bounds__(64 * kDmaWaves) k_rmsnorm_softmax_dma(uint16_t* __restrict__ out, const uint16_t* __restrict__ x,
                                                              const uint16_t* __restrict__ gain, int64_t rows,
