@@ -1097,8 +1097,7 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
                      const char* dst_offset, int32_t allow_broadcast) {
   return guard([&] {
     check_rt(rt);
-    check_buf(dst, "dst");
-    note_write(dst);
+    check_ptr(dst, "dst");
     check_buf(src, "src");
     struct Plan {
       fm::Joint j;
@@ -1123,6 +1122,18 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
     require(dst_base <= dst_len, "transpose: dst window starts past the buffer");
     int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
+    // dst positions dst_base .. dst_base + count - 1 are written where every digit is live: from
+    // position 0 over the whole buffer with no dead digit, the op overwrites every byte and a
+    // pending zero fill is not needed; otherwise the fill goes first.
+    bool all_live = true;
+    for (auto& w : j.wheels) all_live &= w.live == w.size;
+    if (count > 0 && dst_base == 0 && all_live && count * eb >= (int64_t)dst->bytes) {
+      set_device(rt);
+      claim_out(rt, dst, dst->bytes);
+    } else {
+      check_buf(dst, "dst");
+    }
+    note_write(dst);
     if (count <= 0) return;
     require(src_base + max_live_offset(j.wheels, 0) < src_len, "transpose: the src window reads past the buffer");
     require(count < (1ll << 31), "transpose: more than 2^31 positions");

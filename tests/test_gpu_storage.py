@@ -977,6 +977,35 @@ def test_fresh_buffer_full_overwrite(rt):
     assert np.array_equal(d.read(np.float32), 2 * np.arange(n, dtype=np.float32))
 
 
+def test_fresh_buffer_transposes(rt):
+    """A transpose that writes every position of a fresh buffer (a genuine transpose, a broadcast)
+    returns exactly its values with no fill; one that leaves positions unwritten (a buffer longer
+    than the view, a window at an offset, a padded destination view) leaves them zero."""
+    s = dict(A=16, B=24, X=3)
+    x = np.arange(16 * 24, dtype=np.float32)
+    xb = rt.upload(x)
+    d = dirty_block(rt, 4 * 16 * 24)
+    rt.transpose(d, xb, F32, fh.m("A, B", **s), fh.m("B, A", **s))
+    assert np.array_equal(d.read(np.float32), x.reshape(16, 24).T.ravel())
+    d = dirty_block(rt, 4 * 16 * 24 * 3)
+    rt.transpose(d, xb, F32, fh.m("A, B", **s), fh.m("A, X, B", **s), allow_broadcast=True)
+    assert np.array_equal(d.read(np.float32), np.repeat(x.reshape(16, 1, 24), 3, axis=1).ravel())
+    d = dirty_block(rt, 4 * 16 * 24 + 64)
+    rt.transpose(d, xb, F32, fh.m("A, B", **s), fh.m("B, A", **s))
+    got = d.read(np.float32)
+    assert np.array_equal(got[:16 * 24], x.reshape(16, 24).T.ravel()) and not got[16 * 24:].any()
+    full, half = fh.m("A, B", **s), fh.m("A, B = 12 # 24", **s)
+    d = dirty_block(rt, 4 * 16 * 24)
+    rt.transpose(d, xb, F32, half, half, src_map=full, dst_map=full, src_offset={"B": 0}, dst_offset={"B": 12})
+    got = d.read(np.float32).reshape(16, 24)
+    assert np.array_equal(got[:, 12:], x.reshape(16, 24)[:, :12]) and not got[:, :12].any()
+    p = dict(A=16, B=24)
+    d = dirty_block(rt, 4 * 16 * 32)
+    rt.transpose(d, xb, F32, fh.m("A, B", **p), fh.m("A, B # 32", **p))
+    got = d.read(np.float32).reshape(16, 32)
+    assert np.array_equal(got[:, :24], x.reshape(16, 24)) and not got[:, 24:].any()
+
+
 # ---- deferred widening casts (fo_map CAST to f32 / i32 recorded for the contraction after it) ----------
 
 
