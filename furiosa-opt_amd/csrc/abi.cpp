@@ -170,6 +170,19 @@ void record_widen(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
   dst->widen_pending = true;
 }
 
+// b holds a widen of at least n bf16 elements into f32, recorded on rt and not yet run.
+bool deferred_bf16_widen(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenRecord* out) {
+  if (!b || !b->widen_pending) return false;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == b && r.deferred) {
+      if (r.rt != rt || r.src_t != FO_BF16 || r.dst_t != FO_F32 || r.op.code != FO_OP_CAST || r.n < n) return false;
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
 bool find_widen(const fo_buffer* dst, WidenRecord* out) {
   std::lock_guard<std::mutex> lock(g_widen_mu);
   for (auto& r : g_widen)
@@ -1032,17 +1045,26 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
     check_rt(rt);
     check_ptr(dst, "dst");
     note_write(dst);
-    check_buf(a, "a");
-    check_buf(b, "b");
     require(op != nullptr, "op is NULL");
     require(n * dtype_bytes(dst_t) <= dst->bytes && n * dtype_bytes(in_t) <= a->bytes &&
                 n * dtype_bytes(in_t) <= b->bytes,
             "zip_with: n exceeds a buffer");
+    // An f32 input that is a still-deferred exact widen of bf16 data is read from that data and
+    // widened in the kernel, so the cast need not run.
+    WidenRecord wa{}, wb{};
+    const bool na = in_t == FO_F32 && dst_t == FO_F32 && deferred_bf16_widen(rt, a, n, &wa);
+    const bool nb = in_t == FO_F32 && dst_t == FO_F32 && deferred_bf16_widen(rt, b, n, &wb);
+    check_buf(na ? wa.src : a, "a");
+    check_buf(nb ? wb.src : b, "b");
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, n * dtype_bytes(dst_t));
     TraceScope trace_span(rt, "zip_with");
-    launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
+    if (na || nb)
+      launch_zip_widened(rt->stream, dst->ptr, dst_t, na ? wa.src->ptr : a->ptr, na, nb ? wb.src->ptr : b->ptr, nb, n,
+                         *op);
+    else
+      launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
   });
 }
 

@@ -362,6 +362,38 @@ __global__ void __launch_bounds__(kBlock) k_zip_v(void* __restrict__ dst, const 
   }
 }
 
+// zip_with over f32 inputs, either of which may be given as the bf16 source of a deferred exact
+// widen (AB or BB = 2): its words are widened here by the cast's own rule (bf16_to_f32), so the
+// result is the same as zipping the materialized f32 copy, which then never needs writing.
+__device__ __forceinline__ uint32_t widened_word(uint32_t raw, int width) {
+  return width == 2 ? f32_bits(bf16_to_f32((uint16_t)raw)) : raw;
+}
+template <int AB, int BB, int OB>
+__global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const void* __restrict__ a,
+                                                  const void* __restrict__ b, uint64_t n, fo_op op) {
+  constexpr int MINB = AB < BB ? (AB < OB ? AB : OB) : (BB < OB ? BB : OB);
+  constexpr int V = 16 / MINB;
+  const uint64_t nv = (n + V - 1) / V;
+  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
+    if ((j + 1) * V <= n) {
+      Regs<V * AB> ra;
+      Regs<V * BB> rb;
+      Regs<V * OB> out;
+      ra.load((const uint8_t*)a + j * V * AB);
+      rb.load((const uint8_t*)b + j * V * BB);
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+        out.template set<OB>(e, combine(op, widened_word(ra.template get<AB>(e), AB),
+                                        widened_word(rb.template get<BB>(e), BB), op.imm1));
+      out.store((uint8_t*)dst + j * V * OB);
+    } else {
+      for (uint64_t i = j * V; i < n; ++i)
+        store_raw<OB>(dst, i, combine(op, widened_word(load_raw<AB>(a, i), AB), widened_word(load_raw<BB>(b, i), BB),
+                                      op.imm1));
+    }
+  }
+}
+
 // ---- zip3 with tag-guarded slots (apply_slots) --------------------------------------------------
 // Each cell takes the first register slot whose guard admits its execution id, else the port slot
 // if its guard admits, else passes through. A tag byte above 15 is not an execution id (the
@@ -702,6 +734,26 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
   FO_ZIP_CASE(1, 2);
 #undef FO_ZIP_CASE
   throw InvalidArg("zip_with: unsupported element widths");
+}
+
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, bool a_bf16, const void* b,
+                        bool b_bf16, uint64_t n, const fo_op& op) {
+  require(dst_t == FO_F32, "zip_with: widened inputs take f32 outputs");
+  require(aligned16(dst) && aligned16(a) && aligned16(b), "zip_with: buffers must be 16-byte aligned");
+  const int ab = a_bf16 ? 2 : 4, bb = b_bf16 ? 2 : 4, ob = width_of(dst_t);
+#define FO_ZIPW_CASE(A, B, O)                                                                                  \
+  if (ab == A && bb == B && ob == O) {                                                                         \
+    constexpr int MINB = A < B ? (A < O ? A : O) : (B < O ? B : O);                                            \
+    hipLaunchKernelGGL((k_zip_w<A, B, O>), dim3(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB)))),      \
+                       dim3(kBlock), 0, s, dst, a, b, n, op);                                                  \
+    FO_HIP(hipGetLastError());                                                                                 \
+    return;                                                                                                    \
+  }
+  FO_ZIPW_CASE(2, 4, 4);
+  FO_ZIPW_CASE(4, 2, 4);
+  FO_ZIPW_CASE(2, 2, 4);
+#undef FO_ZIPW_CASE
+  throw InvalidArg("zip_with: no widened form for these inputs");
 }
 
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

@@ -225,6 +225,9 @@ void launch_pack_i4(hipStream_t s, void* dst, const int32_t* src, uint64_t n);
 void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
                 const fo_op& op);
 // *flag = 1 when a tag byte is above 15 (not an execution id).
+// zip_with with in_t f32 where a and/or b is the bf16 source of a deferred exact widen (k_vector.hip).
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, bool a_bf16, const void* b,
+                        bool b_bf16, uint64_t n, const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,
                        uint64_t n, const fo_slots& slots, int32_t* flag);
 void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t, uint64_t n, const fo_cmp* cmps);

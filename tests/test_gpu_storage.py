@@ -1009,6 +1009,49 @@ def test_fresh_buffer_transposes(rt):
 # ---- deferred widening casts (fo_map CAST to f32 / i32 recorded for the contraction after it) ----------
 
 
+@pytest.mark.parametrize("n", [1000, 4096 + 3])
+@pytest.mark.parametrize("which", ["a", "b", "both"])
+@pytest.mark.parametrize("op", [("ADD_F", 0), ("SUB_F", fh.SWAP), ("MUL_F", 0)], ids=lambda o: f"{o[0]}{o[1]}")
+def test_zip_reads_deferred_widens(rt, n, which, op):
+    """A zip whose f32 input is a still-deferred widen of bf16 data reads that data and widens it in
+    the kernel: bit-identical to the same zip after the cast has run, on inputs with bf16 subnormals,
+    signed zeros, NaN and large values, at lengths with and without a vector tail."""
+    rng = np.random.default_rng(31)
+    va, vb = special_bf16(rng, n), special_bf16(rng, n)
+    va[::97] = 0x7FC1  # NaN payloads: the widen canonicalises them
+    sa, sb = rt.upload(va), rt.upload(vb)
+    print(f"zip widened {which} {op} n {n}", flush=True)
+
+    def wide(src):
+        w = rt.alloc(4 * n)
+        rt.map(w, F32, src, BF16, n, fh.op("CAST"))  # recorded, not run
+        return w
+    wa = wide(sa) if which in ("a", "both") else rt.upload(emu.bf16_to_f32(va))
+    wb = wide(sb) if which in ("b", "both") else rt.upload(emu.bf16_to_f32(vb))
+    o = fh.op(op[0], op[1])
+    lazy = rt.alloc(4 * n)
+    rt.zip_with(lazy, F32, wa, wb, F32, n, o)
+    got = lazy.read(np.uint32)
+    wa.read(np.uint32), wb.read(np.uint32)  # the casts run now
+    eager = rt.alloc(4 * n)
+    rt.zip_with(eager, F32, wa, wb, F32, n, o)
+    assert np.array_equal(got, eager.read(np.uint32))
+
+
+def test_zip_of_widen_whose_source_was_rewritten(rt):
+    """A write to the bf16 source after the widen was recorded runs the cast first: the zip then
+    sees the old values."""
+    n = 2048
+    old, new = np.full(n, 0x3F80, np.uint16), np.full(n, 0x4000, np.uint16)  # 1.0, then 2.0
+    src = rt.upload(old)
+    w = rt.alloc(4 * n)
+    rt.map(w, F32, src, BF16, n, fh.op("CAST"))
+    src.write(new)
+    out = rt.alloc(4 * n)
+    rt.zip_with(out, F32, w, w, F32, n, fh.op("ADD_F"))
+    assert np.all(out.read(np.float32) == 2.0)
+
+
 def widened(rt, n, seed=40):
     rng = np.random.default_rng(seed)
     v = emu.f32_to_bf16(rng.standard_normal(n).astype(np.float32))
