@@ -1120,7 +1120,7 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
   return guard([&] {
     check_rt(rt);
     check_ptr(dst, "dst");
-    check_buf(src, "src");
+    check_ptr(src, "src");
     struct Plan {
       fm::Joint j;
       int64_t dv_size, src_base, dst_base;
@@ -1142,6 +1142,12 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     const int64_t src_base = plan.src_base, dst_base = plan.dst_base;
     int64_t eb = dtype_bytes(t);
     int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
+    // An f32 source that is a still-deferred widen of bf16 data may be read from that data.
+    WidenRecord wsrc{};
+    const bool narrow = t == FO_F32 && src != dst &&
+                        deferred_bf16_widen(rt, src, (uint64_t)(src_base + max_live_offset(j.wheels, 0) + 1), &wsrc) &&
+                        wsrc.src != dst;
+    check_buf(narrow ? wsrc.src : src, "src");
     require(dst_base <= dst_len, "transpose: dst window starts past the buffer");
     int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
     // dst positions dst_base .. dst_base + count - 1 are written where every digit is live: from
@@ -1162,7 +1168,12 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     set_device(rt);
     TraceScope trace_span(rt, "transpose");
     const int mem[1] = {0};
-    launch_relayout(rt->stream, dst->ptr, src->ptr, eb, dst_base, src_base, count, to_desc<1>(j.wheels, mem));
+    const Wheels<1> w = to_desc<1>(j.wheels, mem);
+    if (narrow && launch_relayout_widen(rt->stream, (float*)dst->ptr, (const uint16_t*)wsrc.src->ptr, dst_base, src_base,
+                                        count, w))
+      return;
+    if (narrow) check_buf(src, "src");  // no widening form for this layout: the cast runs first
+    launch_relayout(rt->stream, dst->ptr, src->ptr, eb, dst_base, src_base, count, w);
   });
 }
 

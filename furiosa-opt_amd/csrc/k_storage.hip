@@ -291,6 +291,31 @@ __global__ void __launch_bounds__(kBlock) k_relayout_chunks(uint8_t* __restrict_
   }
 }
 
+// The chunked copy of f32 elements whose source is bf16 data standing for its exact widen: each
+// four-element chunk reads 8 bytes and writes the widened 16 (bf16_to_f32, the widening cast's rule).
+__global__ void __launch_bounds__(kBlock) k_relayout_chunks_widen(float* __restrict__ dst, const uint16_t* __restrict__ src,
+                                                                  int64_t dst_base, int64_t src_base, uint32_t nchunks,
+                                                                  Wheels<1> w) {
+  for (uint32_t c = blockIdx.x * kBlock + threadIdx.x; c < nchunks; c += gridDim.x * kBlock) {
+    uint32_t q = c * 4;
+    int64_t off = 0;
+    bool live = true;
+    for (int i = 0; i < w.n; ++i) {
+      uint32_t nq = w.div[i].div(q);
+      uint32_t d = q - nq * w.size[i];
+      live &= d < w.live[i];
+      off += (int64_t)d * w.stride[0][i];
+      q = nq;
+    }
+    if (live) {
+      const uint2 h = *(const uint2*)(src + src_base + off);
+      *(float4*)(dst + dst_base + (int64_t)c * 4) =
+          make_float4(bf16_to_f32((uint16_t)h.x), bf16_to_f32((uint16_t)(h.x >> 16)), bf16_to_f32((uint16_t)h.y),
+                      bf16_to_f32((uint16_t)(h.y >> 16)));
+    }
+  }
+}
+
 template <typename T>
 void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int64_t src_base, int64_t count,
                 const Wheels<1>& w) {
@@ -612,6 +637,21 @@ void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t eb, int6
       return relayout_t<uint32_t>(s, dst, src, dst_base, src_base, count, w);
   }
   throw InvalidArg("relayout: unsupported element size");
+}
+
+bool launch_relayout_widen(hipStream_t s, float* dst, const uint16_t* src, int64_t dst_base, int64_t src_base,
+                           int64_t count, const Wheels<1>& w) {
+  // The f32 chunked copy's conditions, with the source 8-byte aligned (its chunks are 4 bf16).
+  if (!(w.n >= 1 && w.stride[0][0] == 1 && w.live[0] == w.size[0] && w.size[0] % 4 == 0 && count % 4 == 0 &&
+        dst_base % 4 == 0 && src_base % 4 == 0 && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 8) == 0))
+    return false;
+  for (int i = 1; i < w.n; ++i)
+    if (w.stride[0][i] % 4 != 0) return false;
+  const int64_t nchunks = count / 4;
+  hipLaunchKernelGGL(k_relayout_chunks_widen, dim3(grid_for(nchunks)), dim3(kBlock), 0, s, dst, src, dst_base, src_base,
+                     (uint32_t)nchunks, w);
+  FO_HIP(hipGetLastError());
+  return true;
 }
 
 void launch_transmute(hipStream_t s, void* dst, const void* src, int64_t eb, int64_t dst_count,

@@ -183,6 +183,10 @@ Wheels<NMEM> to_desc(const std::vector<mapping::Wheel>& ws, const int (&mem)[NME
 // ---- launchers (one per kernel family) ----------------------------------------------------------
 
 // Transpose: dst[dst_base + p] = src[src_base + off(p)] for live p < count.
+// The f32 relayout of bf16 data standing for its exact widen, when the chunked copy applies (every
+// dst run a multiple of four elements, contiguous in src); false when it does not (k_storage.hip).
+bool launch_relayout_widen(hipStream_t s, float* dst, const uint16_t* src, int64_t dst_base, int64_t src_base,
+                           int64_t count, const Wheels<1>& w);
 void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, int64_t dst_base, int64_t src_base,
                      int64_t count, const Wheels<1>& w);
 // A chain of full-view transposes as one gather. Step k writes its positions p < count (a live

@@ -1038,6 +1038,34 @@ def test_zip_reads_deferred_widens(rt, n, which, op):
     assert np.array_equal(got, eager.read(np.uint32))
 
 
+@pytest.mark.parametrize("case", ["broadcast", "transpose", "window"])
+def test_transpose_reads_deferred_widens(rt, case):
+    """A transpose of a still-deferred bf16 -> f32 widen (the decode step's broadcast of a widened
+    gain or RoPE row; a genuine transpose, which has no widening form and runs the cast first; a
+    window at an offset) equals the transpose of the materialized f32 copy, bit for bit."""
+    rng = np.random.default_rng(33)
+    s = dict(A=16, B=32, X=4)
+    v = special_bf16(rng, 16 * 32)
+    src = rt.upload(v)
+    print(f"transpose widened {case}", flush=True)
+    views = {"broadcast": (fh.m("A, B", **s), fh.m("A, X, B", **s), {}, 16 * 4 * 32),
+             "transpose": (fh.m("A, B", **s), fh.m("B, A", **s), {}, 16 * 32),
+             "window": (fh.m("A, B = 16 # 32", **s), fh.m("A, B = 16 # 32", **s),
+                        dict(src_map=fh.m("A, B", **s), dst_map=fh.m("A, B", **s), src_offset={"B": 16},
+                             dst_offset={"B": 0}), 16 * 32)}
+    sv, dv, kw, n_out = views[case]
+    w = rt.alloc(4 * 16 * 32)
+    rt.map(w, F32, src, BF16, 16 * 32, fh.op("CAST"))  # recorded, not run
+    lazy = rt.alloc(4 * n_out)
+    rt.transpose(lazy, w, F32, sv, dv, allow_broadcast=case == "broadcast", **kw)
+    got = lazy.read(np.uint32)
+    w.read(np.uint32)  # the cast runs now
+    eager = rt.alloc(4 * n_out)
+    rt.transpose(eager, w, F32, sv, dv, allow_broadcast=case == "broadcast", **kw)
+    assert np.array_equal(got, eager.read(np.uint32))
+    assert np.array_equal(w.read(np.uint32), emu.bf16_to_f32(v).view(np.uint32))
+
+
 def test_zip_of_widen_whose_source_was_rewritten(rt):
     """A write to the bf16 source after the widen was recorded runs the cast first: the zip then
     sees the old values."""
