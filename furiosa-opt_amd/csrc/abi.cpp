@@ -1449,7 +1449,7 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     check_rt(rt);
     check_ptr(dst, "dst");
     note_write(dst);
-    check_buf(src, "src");
+    check_ptr(src, "src");
     require(t == FO_F32 || t == FO_I32 || t == FO_BF16, "reduce: dtype must be f32, i32 or bf16");
     require(op >= FO_RED_ADD && op <= FO_RED_ADD_SAT, "reduce: unknown op");
     require(op != FO_RED_ADD_SAT || t == FO_I32, "reduce: saturating add is i32 only");
@@ -1481,13 +1481,22 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     require(out_count < (1ll << 31), "reduce: more than 2^31 output cells");
     if (out_count == 0) return;
     set_device(rt);
-    claim_out(rt, dst, (uint64_t)(out_count * eb));  // every cell is written, a dead one with the identity
-    TraceScope trace_span(rt, "reduce");
     const int mem[1] = {0};
     const Wheels<1> owd = to_desc<1>(ow, mem), rwd = to_desc<1>(rw, mem);
     const int64_t src_len = (int64_t)(src->bytes / eb);
     const ReduceSplit split = plan_reduce_split(t, op, src->ptr, src_len, out_count, owd, rwd);
-    if (split.nchunks > 0)
+    // An f32 source that is a still-deferred widen of bf16 data (covering the whole buffer) is read
+    // from that data, widened on load, unless the two-pass column form is chosen.
+    WidenRecord ws{};
+    const bool narrow = t == FO_F32 && split.nchunks == 0 && src != dst &&
+                        deferred_bf16_widen(rt, src, (uint64_t)src_len, &ws) && ws.src != dst;
+    check_buf(narrow ? ws.src : src, "src");
+    claim_out(rt, dst, (uint64_t)(out_count * eb));  // every cell is written, a dead one with the identity
+    TraceScope trace_span(rt, "reduce");
+    if (narrow)
+      launch_reduce_widened(rt->stream, dst->ptr, (const uint16_t*)ws.src->ptr, src_len, out_count, owd, rwd, op,
+                            identity);
+    else if (split.nchunks > 0)
       launch_reduce_split(rt->stream, dst->ptr, src->ptr, t, out_count, owd, rwd, op, identity, split,
                           runtime_scratch(rt, split.scratch_bytes));
     else

@@ -705,6 +705,14 @@ struct RedT<float> {
     }
   }
 };
+// An f32 fold over bf16 data standing for its exact widen (a deferred widening cast): each element
+// is widened on load by the cast's own rule, then folded as f32.
+struct WidenedBf16 {};
+template <>
+struct RedT<WidenedBf16> : RedT<float> {
+  static __device__ __forceinline__ float load(const void* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
+};
+
 template <>
 struct RedT<int32_t> {
   static __device__ __forceinline__ int32_t load(const void* p, int64_t i) { return ((const int32_t*)p)[i]; }
@@ -858,6 +866,37 @@ __global__ void __launch_bounds__(kBlock) k_reduce_thread(void* dst, const void*
 #pragma unroll
       for (int u = 0; u < kBatch; ++u)
         if (ok[u]) acc = R::apply(op, acc, v[u]);
+    }
+    R::store(dst, o, acc);
+  }
+}
+
+// Thread per cell over a residue of one wheel (`total` elements `rstride` apart): the reads of a
+// batch are issued together and folded in order, the emulator's serial fold.
+template <typename Tag>
+__global__ void __launch_bounds__(kBlock) k_reduce_strided(void* dst, const void* src, int64_t src_len,
+                                                           uint32_t out_count, Wheels<1> ow, uint32_t total,
+                                                           int64_t rstride, int op, uint32_t identity) {
+  using R = RedT<Tag>;
+  constexpr int U = 16;
+  for (uint32_t o = blockIdx.x * kBlock + threadIdx.x; o < out_count; o += gridDim.x * kBlock) {
+    int64_t b[1];
+    const bool dead = cell_base(ow, o, out_count, b);
+    auto acc = R::from_bits(identity);
+    if (!dead) {
+      for (uint32_t r0 = 0; r0 < total; r0 += U) {
+        decltype(R::load(src, 0)) v[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t off = b[0] + (int64_t)(r0 + u) * rstride;
+          ok[u] = r0 + u < total && off >= 0 && off < src_len;
+          v[u] = R::load(src, ok[u] ? off : 0);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (ok[u]) acc = R::apply(op, acc, v[u]);
+      }
     }
     R::store(dst, o, acc);
   }
@@ -1142,7 +1181,7 @@ void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_
   // parallelism: a wave per cell when the residue is contiguous, 64 cells x kSeg segments per block
   // when the cells are. For f32 that reassociates the sum, which BufStorage::reduce's own contract
   // accepts (buf.rs:316-330) and the f32 tolerance covers.
-  constexpr bool is_f32 = std::is_same<Tag, float>::value;
+  constexpr bool is_f32 = std::is_same<Tag, float>::value || std::is_same<Tag, WidenedBf16>::value;
   const bool exact_only = std::is_same<Tag, Bf16Red>::value || op == FO_RED_ADD_SAT;
   const bool res_contig = rw.n > 0 && rw.stride[0][0] == 1;
   const bool cells_contig = ow.n > 0 && ow.stride[0][0] == 1;
@@ -1173,6 +1212,9 @@ void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_
     if (blocks > 65535ll * 16) blocks = 65535ll * 16;
     hipLaunchKernelGGL(k_reduce_tiled<Tag>, dim3((unsigned)blocks), dim3(256), 0, s, dst, src, src_len,
                        (uint32_t)out_count, ow, rw, op, identity, (uint32_t)total);
+  } else if (rw.n == 1) {
+    hipLaunchKernelGGL(k_reduce_strided<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
+                       (uint32_t)out_count, ow, (uint32_t)total, rw.stride[0][0], op, identity);
   } else {
     hipLaunchKernelGGL(k_reduce_thread<Tag>, dim3(grid_for(out_count)), dim3(kBlock), 0, s, dst, src, src_len,
                        (uint32_t)out_count, ow, rw, op, identity);
@@ -1262,6 +1304,11 @@ void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_
     default:
       throw InvalidArg("reduce: unsupported dtype");
   }
+}
+
+void launch_reduce_widened(hipStream_t s, void* dst, const uint16_t* src, int64_t src_len, int64_t out_count,
+                           const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity) {
+  reduce_t<WidenedBf16>(s, dst, src, src_len, out_count, ow, rw, op, identity);
 }
 
 // ---------------------------------------------------------------------------------------------

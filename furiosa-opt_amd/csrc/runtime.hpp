@@ -237,6 +237,9 @@ void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* p
 void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t, uint64_t n, const fo_cmp* cmps);
 
 // Reduce over a plan: out wheels (memory strides into src) and residue wheels.
+// An f32 reduce whose source is bf16 data standing for its exact widen (k_storage.hip).
+void launch_reduce_widened(hipStream_t s, void* dst, const uint16_t* src, int64_t src_len, int64_t out_count,
+                           const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity);
 void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,
                    const Wheels<1>& out_w, const Wheels<1>& res_w, int op, uint32_t identity);
 

@@ -1066,6 +1066,56 @@ def test_transpose_reads_deferred_widens(rt, case):
     assert np.array_equal(w.read(np.uint32), emu.bf16_to_f32(v).view(np.uint32))
 
 
+@pytest.mark.parametrize("r", [32, 40])
+@pytest.mark.parametrize("case", [(F32, "ADD", 0), (F32, "MAX", 0xFF800000), (BF16, "ADD", 0), (I32, "ADD_SAT", 0)],
+                         ids=lambda c: f"{c[0]}-{c[1]}")
+def test_reduce_over_one_strided_wheel_exact(rt, r, case):
+    """A reduce whose residue is one strided wheel (the decode step's sum of 32 partial products, 128
+    apart) folds each cell serially in the emulator's order: bit-exact against the oracle, for a
+    residue that is and is not a multiple of the read batch."""
+    t, opname, ident = case
+    s = dict(A=8, R=r, B=128)
+    so, do = mr.parse("A, R, B", s), mr.parse("A, B", s)
+    rng = np.random.default_rng(34)
+    n = 8 * r * 128
+    if t == I32:
+        src = rng.integers(-2**31, 2**31 - 1, n, dtype=np.int64).astype(np.int32)
+    else:
+        src = rng.standard_normal(n).astype(np.float32)
+        if t == BF16:
+            src = emu.f32_to_bf16(src)
+    want = emu.reduce(src, t, so, do, fh.RED[opname], ident)
+    out = rt.alloc(8 * 128 * 4)
+    rt.reduce(out, rt.upload(src), t, fh.m("A, R, B", **s), fh.m("A, B", **s), fh.RED[opname], ident)
+    assert np.array_equal(out.read(want.dtype, want.size), want)
+
+
+@pytest.mark.parametrize("case", ["rows", "strided"])
+def test_reduce_reads_deferred_widens(rt, case):
+    """A reduce of a still-deferred bf16 -> f32 widen (the decode step's row max over 512 keys; its
+    sum of 32 partials) reads the bf16 data, widening on load: equal to the reduce of the
+    materialized copy."""
+    rng = np.random.default_rng(35)
+    if case == "rows":
+        s = dict(A=16, T=512)
+        sm, dm, op, ident = "A, T", "A", fh.RED["MAX"], 0xFF800000
+    else:
+        s = dict(A=16, R=32, B=128)
+        sm, dm, op, ident = "A, R, B", "A, B", fh.RED["ADD"], 0
+    n = int(np.prod(list(s.values())))
+    v = special_bf16(rng, n)
+    w = rt.alloc(4 * n)
+    rt.map(w, F32, rt.upload(v), BF16, n, fh.op("CAST"))  # recorded, not run
+    n_out = n // (512 if case == "rows" else 32)
+    lazy = rt.alloc(4 * n_out)
+    rt.reduce(lazy, w, F32, fh.m(sm, **s), fh.m(dm, **s), op, ident)
+    got = lazy.read(np.uint32)
+    w.read(np.uint32)  # the cast runs now
+    eager = rt.alloc(4 * n_out)
+    rt.reduce(eager, w, F32, fh.m(sm, **s), fh.m(dm, **s), op, ident)
+    assert np.array_equal(got, eager.read(np.uint32))
+
+
 def test_zip_of_widen_whose_source_was_rewritten(rt):
     """A write to the bf16 source after the widen was recorded runs the cast first: the zip then
     sees the old values."""
