@@ -154,14 +154,26 @@ __global__ void __launch_bounds__(256) k_gemv_fold(Out* __restrict__ out, const 
   // Every producer issues the same loads every stage (addresses past N or K are clamped onto valid
   // data, whose products are skipped or never folded into a written cell), so the loads complete in
   // issue order and each stage waits only for its own.
+  // A producer's chunks sit at fixed (row, column) places of every stage: their row pointers,
+  // columns and product offsets are computed once.
+  const uint16_t* wrow[kFoldPer];
+  int pcol[kFoldPer], poff[kFoldPer];
+#pragma unroll
+  for (int u = 0; u < kFoldPer; ++u) {
+    const int c = p + u * kFoldProducers;
+    const int row = c / kFoldCPR;
+    pcol[u] = (c % kFoldCPR) * 8;
+    poff[u] = row * kFoldPS + pcol[u];
+    wrow[u] = w + min(n0 + row, N - 1) * ldw;
+  }
   uint4 reg[kFoldDepth][kFoldPer];
   auto load = [&](int s, uint4 (&r)[kFoldPer]) {
+    const int k0 = s * kFoldKC;
+    const bool full = k0 + kFoldKC <= K;  // uniform: no chunk of the stage reaches K
 #pragma unroll
     for (int u = 0; u < kFoldPer; ++u) {
-      const int c = p + u * kFoldProducers;
-      const int k = s * kFoldKC + (c % kFoldCPR) * 8;
-      const int64_t n = min(n0 + c / kFoldCPR, N - 1);
-      r[u] = *(const uint4*)(w + n * ldw + (k < K ? k : K - 8));
+      const int k = k0 + pcol[u];
+      r[u] = *(const uint4*)(wrow[u] + (full || k < K ? k : K - 8));
     }
   };
   if (!folder) {
@@ -205,31 +217,34 @@ __global__ void __launch_bounds__(256) k_gemv_fold(Out* __restrict__ out, const 
 #pragma unroll
       for (int j = 0; j < kFoldDepth; ++j) {
         const int s = r * kFoldDepth + j;
-        if (s < stages) {
+        // The products of stage s into P[s & 1]; FULL (a constant at each inlined use) when every
+        // chunk of the stage lies below K, else chunks past K write +0.
+        auto produce = [&](int s, const uint4 (&r)[kFoldPer], bool FULL) __attribute__((always_inline)) {
           float* dst = P[s & 1];
-          const bool full = (s + 1) * kFoldKC <= K;  // every chunk of the stage lies below K
           float4 xa[kFoldPer], xb[kFoldPer];
 #pragma unroll
           for (int u = 0; u < kFoldPer; ++u) {  // all x reads first, then the products
-            const int k = s * kFoldKC + ((p + u * kFoldProducers) % kFoldCPR) * 8;
-            const int kk = k < K ? k : K - 8;
+            const int k = s * kFoldKC + pcol[u];
+            const int kk = FULL || k < K ? k : K - 8;
             xa[u] = *(const float4*)&xs[kk];
             xb[u] = *(const float4*)&xs[kk + 4];
           }
 #pragma unroll
           for (int u = 0; u < kFoldPer; ++u) {
-            const int c = p + u * kFoldProducers;
-            const int row = c / kFoldCPR, col = (c % kFoldCPR) * 8;
-            const uint4 v = reg[j][u];
+            const uint4 v = r[u];
             float4 a = make_float4(__fmul_rn(xa[u].x, bf16_lo(v.x)), __fmul_rn(xa[u].y, bf16_hi(v.x)),
                                    __fmul_rn(xa[u].z, bf16_lo(v.y)), __fmul_rn(xa[u].w, bf16_hi(v.y)));
             float4 b = make_float4(__fmul_rn(xb[u].x, bf16_lo(v.z)), __fmul_rn(xb[u].y, bf16_hi(v.z)),
                                    __fmul_rn(xb[u].z, bf16_lo(v.w)), __fmul_rn(xb[u].w, bf16_hi(v.w)));
-            if (!full && s * kFoldKC + col >= K) a = b = make_float4(0.f, 0.f, 0.f, 0.f);  // past K: +0
-            *(float4*)&dst[row * kFoldPS + col] = a;
-            *(float4*)&dst[row * kFoldPS + col + 4] = b;
+            if (!FULL && s * kFoldKC + pcol[u] >= K) a = b = make_float4(0.f, 0.f, 0.f, 0.f);  // past K: +0
+            *(float4*)&dst[poff[u]] = a;
+            *(float4*)&dst[poff[u] + 4] = b;
           }
-        }
+        };
+        if ((s + 1) * kFoldKC <= K)
+          produce(s, reg[j], true);
+        else if (s < stages)
+          produce(s, reg[j], false);
         load(s + kFoldDepth, reg[j]);
         handover();
       }
