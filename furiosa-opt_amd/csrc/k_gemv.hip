@@ -9,10 +9,11 @@
 // reference's bf16 rule (float/bf16.rs:16-40: a subnormal reads as a signed zero); the products
 // and sums themselves are IEEE f32, subnormal results included. The parallelism is across cells,
 // and the chain of K dependent adds per cell bounds a small GEMV, HBM a large one. Two kernels:
-//   * k_gemv_fold (K <= 4096): a block of four waves owns 64 cells. Waves 1-3 stream the 64 weight
+//   * k_gemv_fold (K <= 4096): a block of seven waves owns 64 cells. Waves 1-6 stream the 64 weight
 //     rows from HBM (16-byte loads, four stages in flight) and write the exact f32 products of each
 //     96-element stage to LDS; wave 0 folds the previous stage's products, one cell per lane, so its
-//     instruction stream is one LDS read per four adds. The producer waves run with subnormal inputs
+//     instruction stream is one LDS read per four adds. (Three producer waves left the fold waiting
+//     on them; six bring a stage close to the folder's own chain of dependent adds.) The producer waves run with subnormal inputs
 //     flushed and subnormal results kept (the MODE register is per wave): the reference's widen of
 //     a subnormal weight to zero, then an IEEE product. The folding wave keeps full IEEE behaviour.
 //   * k_gemv_bf16 (any K): R cells per block, the rows staged through LDS by all waves and folded by
@@ -126,7 +127,7 @@ __global__ void __launch_bounds__(kGemvThreads) k_gemv_bf16(Out* __restrict__ ou
 constexpr int kFoldR = 64;                          // cells per block: one per lane of wave 0
 constexpr int kFoldKC = 96;                         // k elements per stage
 constexpr int kFoldCPR = kFoldKC / 8;               // 16-byte chunks per row per stage
-constexpr int kFoldProducers = 192;                 // threads of waves 1-3
+constexpr int kFoldProducers = 384;                 // threads of waves 1-6
 constexpr int kFoldPer = kFoldR * kFoldCPR / kFoldProducers;  // chunks per producer per stage (4)
 constexpr int kFoldPS = kFoldKC + 4;  // product row stride in floats: 16 lanes' b128 reads cover 64 banks once
 constexpr int kFoldMaxK = 4096;       // x is staged whole in LDS
@@ -139,7 +140,7 @@ constexpr int kModeDenormF32 = 1 | (4 << 6) | (1 << 11);  // s_setreg hwreg(HW_R
 constexpr int kDenormFlushIn = 2;
 
 template <typename Out>
-__global__ void __launch_bounds__(256) k_gemv_fold(Out* __restrict__ out, const uint16_t* __restrict__ x,
+__global__ void __launch_bounds__(64 + kFoldProducers) k_gemv_fold(Out* __restrict__ out, const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ w, int64_t N, int K, int64_t ldw,
                                                    int64_t ldo) {
   __shared__ __attribute__((aligned(16))) float P[2][kFoldR * kFoldPS];
@@ -281,7 +282,7 @@ template <typename Out>
 void gemv_fold(hipStream_t s, Out* out, const uint16_t* x, const uint16_t* w, int64_t N, int64_t K, int64_t ldw,
                int64_t ldo) {
   const int64_t blocks = (N + kFoldR - 1) / kFoldR;
-  hipLaunchKernelGGL((k_gemv_fold<Out>), dim3((unsigned)blocks), dim3(256), 0, s, out, x, w, N, (int)K, ldw, ldo);
+  hipLaunchKernelGGL((k_gemv_fold<Out>), dim3((unsigned)blocks), dim3(64 + kFoldProducers), 0, s, out, x, w, N, (int)K, ldw, ldo);
   FO_HIP(hipGetLastError());
 }
 
