@@ -77,6 +77,7 @@ constexpr int kPP = kKC + 4;     // LDS row pitch in floats (16-byte rows, confl
 constexpr int kMlpThreads = 512;
 constexpr int kUnits = 4;  // producer work units per chunk per thread (hidden * kKC / 8 <= kUnits * producers)
 constexpr int kAhead = 2;  // chunks of weights in flight ahead of the products
+constexpr int kW2Per = 4;  // fc2 weights per thread, loaded at the start (out_f * hidden <= kW2Per * threads)
 // s_waitcnt immediate (gfx9 encoding): LDS/scalar count 0, vector memory and export counts left open.
 constexpr int kWaitLgkm0 = 0xF | (0x7 << 4) | (0x3 << 14);
 
@@ -101,6 +102,12 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
   const int nprod = kMlpThreads - fw * 64;           // producer threads
   const int nchunks = (in_f + kKC - 1) / kKC;
   constexpr int G = kKC / 8;                         // 8-product groups per row per chunk
+  // fc2's weights and both biases are loaded now, so their latency hides behind fc1.
+  const int n2 = out_f * hidden;
+  uint16_t w2r[kW2Per];
+#pragma unroll
+  for (int j = 0; j < kW2Per; ++j) w2r[j] = w2[min(tid + j * kMlpThreads, n2 - 1)];
+  const uint16_t b1r = b1[min(tid, hidden - 1)], b2r = b2[min(tid, out_f - 1)];
   for (int i = tid; i < in_f; i += kMlpThreads) xs[i] = bf16_to_f32(x[b * in_f + i]);
   __syncthreads();
   // Producer p owns work units p, p + nprod, ... (at most kUnits): unit u is hidden row u / G,
@@ -108,11 +115,13 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
   // set per chunk in flight.
   const int ptid = tid - fw * 64, units = hidden * G;
   i32x4_t wv[kAhead][kUnits];
+  // Every producer issues all kUnits loads (a unit past the end reads the last group, which its
+  // produce step then skips), so the loads complete in issue order and each chunk waits for its own.
   auto load = [&](int c, int set) {
 #pragma unroll
     for (int i = 0; i < kUnits; ++i) {
-      const int u = ptid + i * nprod, h = u / G, k0 = c * kKC + (u % G) * 8;
-      if (u < units && k0 < in_f) wv[set][i] = *(const i32x4_t*)(w1 + (int64_t)h * in_f + k0);
+      const int u = min(ptid + i * nprod, units - 1), h = u / G, k0 = min(c * kKC + (u % G) * 8, in_f - 8);
+      wv[set][i] = *(const i32x4_t*)(w1 + (int64_t)h * in_f + k0);
     }
   };
   auto produce = [&](int c, int buf, int set) {
@@ -127,8 +136,11 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
       for (int e = 0; e < 4; ++e) {
         const uint32_t uw = (uint32_t)wv[set][i][e];
         const float xl = e < 2 ? xa[2 * e] : xb[2 * e - 4], xh = e < 2 ? xa[2 * e + 1] : xb[2 * e - 3];
-        const float lo = __fmul_rn(xl, bf16_to_f32((uint16_t)(uw & 0xffffu)));
-        const float hi = __fmul_rn(xh, bf16_to_f32((uint16_t)(uw >> 16)));
+        // The weight's bits as an f32; its subnormals read as zero through this wave's flush of
+        // subnormal inputs (set below), as the reference widen has them. A NaN weight keeps its
+        // payload here but makes a NaN sum, which the bf16 narrow of fc1 canonicalises.
+        const float lo = __fmul_rn(xl, __uint_as_float(uw << 16));
+        const float hi = __fmul_rn(xh, __uint_as_float(uw & 0xffff0000u));
         if (e < 2) {
           p0[2 * e] = lo;
           p0[2 * e + 1] = hi;
@@ -152,6 +164,9 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
   const bool folder = tid < fw * 64;
   float acc = 0.f;
   if (!folder) {
+    // MODE.FP_DENORM single-precision field = 2: subnormal inputs flushed, subnormal results kept
+    // (a per-wave register; the folder waves keep full IEEE behaviour).
+    __builtin_amdgcn_s_setreg(1 | (4 << 6) | (1 << 11), 2);
     load(0, 0);
     if (nchunks > 1) load(1, 1);
     produce(0, 0, 0);
@@ -163,12 +178,28 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
       if (tid < hidden) {
         const float* P = pb + (c & 1) * hidden * kPP + tid * kPP;
         const int kn = min(kKC, in_f - c * kKC);  // a multiple of 8
-        for (int k = 0; k < kn; k += 4) {
-          const f32x4_t p = *(const f32x4_t*)(P + k);
-          acc = __fadd_rn(acc, p[0]);
-          acc = __fadd_rn(acc, p[1]);
-          acc = __fadd_rn(acc, p[2]);
-          acc = __fadd_rn(acc, p[3]);
+        if (kn == kKC) {
+          // A full chunk's row is read whole before the adds: one LDS latency per chunk rather
+          // than one per four adds.
+          f32x4_t v[kKC / 4];
+#pragma unroll
+          for (int i = 0; i < kKC / 4; ++i) v[i] = *(const f32x4_t*)(P + 4 * i);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int i = 0; i < kKC / 4; ++i) {
+            acc = __fadd_rn(acc, v[i][0]);
+            acc = __fadd_rn(acc, v[i][1]);
+            acc = __fadd_rn(acc, v[i][2]);
+            acc = __fadd_rn(acc, v[i][3]);
+          }
+        } else {
+          for (int k = 0; k < kn; k += 4) {
+            const f32x4_t p = *(const f32x4_t*)(P + k);
+            acc = __fadd_rn(acc, p[0]);
+            acc = __fadd_rn(acc, p[1]);
+            acc = __fadd_rn(acc, p[2]);
+            acc = __fadd_rn(acc, p[3]);
+          }
         }
       }
     } else if (c + 1 < nchunks) {
@@ -185,22 +216,41 @@ __global__ void __launch_bounds__(kMlpThreads) k_mlp_split(int32_t* __restrict__
   }
   if (tid < hidden) {
     float hv = bf16_to_f32(f32_to_bf16(acc));                    // contract_lane + cast
-    float z = fmaxf(__fadd_rn(hv, bf16_to_f32(b1[tid])), 0.0f);  // clip Add, clip Max 0
+    float z = fmaxf(__fadd_rn(hv, bf16_to_f32(b1r)), 0.0f);  // clip Add, clip Max 0
     hs[tid] = bf16_to_f32(f32_to_bf16(z));
   }
   __syncthreads();
   // fc2: the out_f x hidden products in parallel into the (free) product buffer, then one
   // thread per output folds them in ascending k.
-  for (int i = tid; i < out_f * hidden; i += kMlpThreads) {
-    const int o = i / hidden, kk = i % hidden;
-    pb[o * hp + kk] = __fmul_rn(hs[kk], bf16_to_f32(w2[(int64_t)o * hidden + kk]));
+#pragma unroll
+  for (int j = 0; j < kW2Per; ++j) {
+    const int i = tid + j * kMlpThreads;
+    if (i < n2) {
+      const int o = i / hidden, kk = i % hidden;
+      pb[o * hp + kk] = __fmul_rn(hs[kk], bf16_to_f32(w2r[j]));
+    }
   }
   __syncthreads();
   for (int o = tid; o < out_f; o += kMlpThreads) {
     float a2 = 0.f;
-    for (int kk = 0; kk < hidden; ++kk) a2 = __fadd_rn(a2, pb[o * hp + kk]);
+    int kk = 0;
+    // Runs of 32 products read before they are added, in ascending k as before.
+    for (; kk + 32 <= hidden; kk += 32) {
+      f32x4_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = *(const f32x4_t*)(pb + o * hp + kk + 4 * i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        a2 = __fadd_rn(a2, v[i][0]);
+        a2 = __fadd_rn(a2, v[i][1]);
+        a2 = __fadd_rn(a2, v[i][2]);
+        a2 = __fadd_rn(a2, v[i][3]);
+      }
+    }
+    for (; kk < hidden; ++kk) a2 = __fadd_rn(a2, pb[o * hp + kk]);
     float yv = bf16_to_f32(f32_to_bf16(a2));
-    uint16_t y = f32_to_bf16(__fadd_rn(yv, bf16_to_f32(b2[o])));
+    uint16_t y = f32_to_bf16(__fadd_rn(yv, bf16_to_f32(o == tid ? b2r : b2[o])));
     ys[o] = bf16_to_f32(y);
     if (logits) logits[b * out_f + o] = y;
   }
@@ -229,6 +279,7 @@ void launch_mlp(hipStream_t s, int32_t* pred, uint16_t* logits, const uint16_t* 
       (size_t)(((in_f + 3) / 4 + (hidden + 3) / 4 + (out_f + 3) / 4) * 4 + 2 * hidden * kPP) * sizeof(float);
   const int64_t producers = kMlpThreads - (hidden + 63) / 64 * 64;
   if (in_f % 8 == 0 && hidden <= 256 && hidden * (kKC / 8) <= kUnits * producers && out_f * ((hidden + 3) / 4 * 4) <= 2 * hidden * kPP &&
+      out_f * hidden <= kW2Per * kMlpThreads &&
       ((uintptr_t)w1 % 16) == 0 && lds_split <= 160 * 1024) {
     static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into
     if (!attr_set) {

@@ -390,6 +390,33 @@ def test_mlp_exact(rt, shape):
     assert np.array_equal(pb.read(np.int32), pred)
 
 
+@pytest.mark.parametrize("shape", [(64, 784, 128, 10), (7, 33, 40, 3)])
+def test_mlp_special_values_exact(rt, shape):
+    """Weights and inputs holding bf16 subnormals (the reference widen reads them as zero), signed
+    zeros, and weights near 2^-70 whose products with small inputs are f32 subnormals (kept by the
+    reference's f32 arithmetic): logits and predictions bit-exact against the oracle."""
+    batch, in_f, hid, out_f = shape
+    rng = np.random.default_rng(38)
+
+    def special(n, scale):
+        v = (rng.standard_normal(n) * scale).astype(np.float32)
+        kind = rng.integers(0, 12, n)
+        v[kind == 1] *= np.float32(2.0 ** -70)
+        bits = emu.f32_to_bf16(v)
+        sub = kind == 2
+        bits[sub] = (rng.integers(1, 0x80, int(sub.sum())) | (rng.integers(0, 2, int(sub.sum())) << 15)).astype(np.uint16)
+        bits[kind == 3] = 0x8000
+        return bits
+    x = special(batch * in_f, 1.0)
+    w1, b1 = special(hid * in_f, 0.05), special(hid, 0.05)
+    w2, b2 = special(out_f * hid, 0.05), special(out_f, 0.05)
+    pred, logits = emu.mlp(x, w1, b1, w2, b2, batch, in_f, hid, out_f)
+    pb, lb = rt.alloc(batch * 4), rt.alloc(batch * out_f * 2)
+    rt.mlp(pb, lb, *(rt.upload(t) for t in (x, w1, b1, w2, b2)), batch, in_f, hid, out_f)
+    assert np.array_equal(lb.read(np.uint16), logits)
+    assert np.array_equal(pb.read(np.int32), pred)
+
+
 def test_mnist_answer_key(rt):
     """furiosa-opt-examples/tests/mnist_tests.rs:7-53: the reference's weights and ten images, loaded
     through the safetensors entry point, one forward per image (batch 1, 800 -> 256 -> 16); the argmax
