@@ -79,8 +79,10 @@ namespace {
 // reads the narrow sources instead -- the MFMA kernels consume them directly, and the generic fold
 // widens them the same way the map would, so its result is unchanged -- and never needs the wide
 // copy. Any other use of the wide buffer (check_buf) runs the deferred cast first, on the stream of
-// the runtime that issued it; so does a write to or the freeing of its source (note_write,
-// forget_buffer), before the source changes. A write to either side drops the record. Records are
+// the runtime that issued it; so does a write to its source (note_write), before the source
+// changes. A write to either side drops the record. A source freed by its owner while a record reads
+// it is kept until the last such record goes (retire_source), so an engine that narrows into a
+// temporary, widens it and drops the temporary still has the cast deferred. Records are
 // process-wide, as buffers are.
 struct WidenRecord {
   const fo_buffer* dst;
@@ -104,34 +106,119 @@ void run_deferred(const std::vector<WidenRecord>& rs) {
   }
 }
 
+// A buffer's block leaves it (the buffer is being freed, rec the recording open at that moment or
+// none), then the buffer goes. A block freed while recording stays with the recording's memory,
+// since the graph may touch it; later allocations of the recording reuse it unless an earlier graph
+// owns it.
+void free_block(fo_buffer* buf, const std::shared_ptr<fo_graph_mem>& rec) {
+  if (buf->pool) {
+    std::lock_guard<std::mutex> lock(buf->pool->mu);
+    buf->pool->unfilled.erase(buf);
+  }
+  if (buf->ptr) {
+    if (rec) {
+      if (buf->graph_mem == rec) {
+        rec->reuse.emplace(buf->capacity, buf->ptr);
+      } else if (buf->graph_mem) {
+        rec->keep.push_back(buf->graph_mem);
+      } else {
+        rec->blocks.emplace_back(buf->capacity, buf->ptr);
+        rec->reuse.emplace(buf->capacity, buf->ptr);
+      }
+    } else if (!buf->graph_mem) {
+      if (buf->pool) {
+        buf->pool->release(buf->ptr, buf->capacity);
+      } else {
+        (void)hipSetDevice(buf->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(buf->ptr);
+      }
+    }  // else the block is its recording's, returned when that memory's last holder goes
+  }
+  delete buf;
+}
+
+// Erases the records that match; returns the retired sources no remaining record names (the
+// caller frees them after any cast that reads them has been launched). Called with the lock held.
+template <typename Pred>
+std::vector<fo_buffer*> erase_records(Pred drop) {
+  std::vector<fo_buffer*> gone;
+  for (auto& r : g_widen)
+    if (drop(r) && r.src->retired &&
+        std::find(gone.begin(), gone.end(), r.src) == gone.end())
+      gone.push_back(const_cast<fo_buffer*>(r.src));
+  g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(), drop), g_widen.end());
+  gone.erase(std::remove_if(gone.begin(), gone.end(),
+                            [](const fo_buffer* s) {
+                              return std::any_of(g_widen.begin(), g_widen.end(),
+                                                 [s](const WidenRecord& r) { return r.src == s; });
+                            }),
+             gone.end());
+  return gone;
+}
+
+void free_retired(const std::vector<fo_buffer*>& gone) {
+  for (fo_buffer* s : gone) {
+    std::shared_ptr<fo_graph_mem> rec = std::move(s->retired_in);
+    free_block(s, rec);
+  }
+}
+
 // b is about to be written: a deferred cast from or into it runs first, then its records go.
 void note_write(const fo_buffer* b) {
   if (!b) return;
   std::vector<WidenRecord> todo;
+  std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
     for (auto& r : g_widen)
       if ((r.dst == b || r.src == b) && r.deferred) todo.push_back(r);
-    g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
-                                 [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
-                  g_widen.end());
+    gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
   }
   run_deferred(todo);
+  free_retired(gone);
 }
 
 // b is being freed: a deferred cast from it runs first (its block may be reused right after); one
 // into it is dropped.
 void forget_buffer(const fo_buffer* b) {
   std::vector<WidenRecord> todo;
+  std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
     for (auto& r : g_widen)
       if (r.src == b && r.deferred && r.dst != b) todo.push_back(r);
-    g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(),
-                                 [b](const WidenRecord& r) { return r.dst == b || r.src == b; }),
-                  g_widen.end());
+    gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
   }
   run_deferred(todo);
+  free_retired(gone);
+}
+
+// b is being freed while a widen record reads it as its source: it is kept (retired), so the cast
+// can stay deferred and a contraction can still read the narrow data; the block is freed when the
+// last such record goes. Returns false (nothing kept) when no record reads b.
+bool retire_source(fo_buffer* b) {
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  if (!std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.src == b && r.dst != b; }) ||
+      std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.dst == b; }))
+    return false;
+  b->retired = true;
+  if (b->pool) {
+    std::lock_guard<std::mutex> plock(b->pool->mu);
+    b->retired_in = b->pool->recording;
+  }
+  return true;
+}
+
+// Before a recording: retired sources whose casts have run are let go, so that no recorded kernel
+// reads a block the recording does not own.
+void free_run_retired() {
+  std::vector<fo_buffer*> gone;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    gone = erase_records([](const WidenRecord& r) { return r.src->retired && !r.deferred; });
+  }
+  free_retired(gone);
 }
 
 // b is about to be read: its deferred cast, if any, runs first (the record stays for contractions).
@@ -759,6 +846,7 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
 
 void fo_buffer_free(fo_buffer* buf) {
   if (!buf) return;
+  if (retire_source(buf)) return;
   try {
     forget_buffer(buf);
   } catch (const std::exception&) {  // a failed launch leaves the error for the next call to report
@@ -766,32 +854,9 @@ void fo_buffer_free(fo_buffer* buf) {
   std::shared_ptr<fo_graph_mem> rec;
   if (buf->pool) {
     std::lock_guard<std::mutex> lock(buf->pool->mu);
-    buf->pool->unfilled.erase(buf);
     rec = buf->pool->recording;
   }
-  if (buf->ptr) {
-    if (rec) {
-      // Freed while recording: the graph may touch the block, so it stays with the recording's
-      // memory; later allocations of the recording reuse it unless an earlier graph owns it.
-      if (buf->graph_mem == rec) {
-        rec->reuse.emplace(buf->capacity, buf->ptr);
-      } else if (buf->graph_mem) {
-        rec->keep.push_back(buf->graph_mem);
-      } else {
-        rec->blocks.emplace_back(buf->capacity, buf->ptr);
-        rec->reuse.emplace(buf->capacity, buf->ptr);
-      }
-    } else if (!buf->graph_mem) {
-      if (buf->pool) {
-        buf->pool->release(buf->ptr, buf->capacity);
-      } else {
-        (void)hipSetDevice(buf->device);
-        (void)hipDeviceSynchronize();
-        (void)hipFree(buf->ptr);
-      }
-    }  // else the block is its recording's, returned when that memory's last holder goes
-  }
-  delete buf;
+  free_block(buf, rec);
 }
 
 int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out) {
@@ -872,6 +937,7 @@ int32_t fo_graph_begin(fo_runtime* rt) {
     // Everything owed to buffers that exist now runs eagerly, outside the graph: a launch must not
     // zero a cache that earlier launches filled, or redo a cast whose source has changed since.
     materialize_runtime(rt);
+    free_run_retired();
     std::vector<fo_buffer*> unfilled;
     {
       std::lock_guard<std::mutex> lock(rt->pool->mu);
@@ -1019,9 +1085,15 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     check_rt(rt);
     check_ptr(dst, "dst");
     note_write(dst);
-    check_buf(src, "src");
     require(op != nullptr, "op is NULL");
+    check_ptr(src, "src");
     require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
+    // An f32 input that is a still-deferred exact widen of bf16 data is read from that data and
+    // widened in the kernel, so the cast need not run.
+    WidenRecord ws{};
+    const bool narrow = src_t == FO_F32 && (dst_t == FO_F32 || dst_t == FO_BF16) &&
+                        deferred_bf16_widen(rt, src, n, &ws) && ws.src != dst;
+    check_buf(narrow ? ws.src : src, "src");
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, span_bytes(dst_t, n));
@@ -1035,7 +1107,10 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
       return;
     }
     TraceScope trace_span(rt, "map");
-    launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
+    if (narrow)
+      launch_map_widened(rt->stream, dst->ptr, dst_t, ws.src->ptr, n, *op);
+    else
+      launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
   });
 }
 

@@ -394,6 +394,32 @@ __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const 
   }
 }
 
+// map over an f32 input given as the bf16 source of a deferred exact widen: each word is widened by
+// the cast's own rule, then mapped as the f32 word it stands for.
+template <int DB>
+__global__ void __launch_bounds__(kBlock) k_map_w(void* __restrict__ dst, const void* __restrict__ src, uint64_t n,
+                                                  fo_dtype dst_t, fo_op op) {
+  constexpr int V = lanes_for<2, DB>();
+  const uint64_t nv = (n + V - 1) / V;
+  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
+    if ((j + 1) * V <= n) {
+      Regs<V * 2> in;
+      Regs<V * DB> out;
+      in.load((const uint8_t*)src + j * V * 2);
+      uint32_t w[V], r[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) w[e] = widened_word(in.template get<2>(e), 2);
+      map_words<V>(w, r, FO_F32, dst_t, op);
+#pragma unroll
+      for (int e = 0; e < V; ++e) out.template set<DB>(e, r[e]);
+      out.store((uint8_t*)dst + j * V * DB);
+    } else {
+      for (uint64_t i = j * V; i < n; ++i)
+        store_raw<DB>(dst, i, map_word(widened_word(load_raw<2>(src, i), 2), FO_F32, dst_t, op));
+    }
+  }
+}
+
 // ---- zip3 with tag-guarded slots (apply_slots) --------------------------------------------------
 // Each cell takes the first register slot whose guard admits its execution id, else the port slot
 // if its guard admits, else passes through. A tag byte above 15 is not an execution id (the
@@ -754,6 +780,21 @@ void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a,
   FO_ZIPW_CASE(2, 2, 4);
 #undef FO_ZIPW_CASE
   throw InvalidArg("zip_with: no widened form for these inputs");
+}
+
+void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src_bf16, uint64_t n, const fo_op& op) {
+  require(aligned16(dst) && aligned16(src_bf16), "map: buffers must be 16-byte aligned");
+  if (dst_t == FO_F32) {
+    constexpr int V = lanes_for<2, 4>();
+    hipLaunchKernelGGL((k_map_w<4>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, src_bf16,
+                       n, dst_t, op);
+  } else {
+    require(dst_t == FO_BF16, "map: a widened input takes f32 or bf16 outputs");
+    constexpr int V = lanes_for<2, 2>();
+    hipLaunchKernelGGL((k_map_w<2>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, src_bf16,
+                       n, dst_t, op);
+  }
+  FO_HIP(hipGetLastError());
 }
 
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

@@ -108,6 +108,11 @@ struct fo_buffer {
   // An exact widening cast into this buffer recorded but not yet run (the runtime's pending
   // widens): a read runs it first.
   bool widen_pending = false;
+  // Freed by its owner while a pending widen still reads it (the source of that widen): the block
+  // stays until no widen record names it, then goes the way a free at retirement time would have
+  // sent it (retired_in: the recording open then, if any).
+  bool retired = false;
+  std::shared_ptr<fo_graph_mem> retired_in;
   // Born while a graph was recorded: the block belongs to that recording's memory, not to the
   // pool, and outlives this buffer while the graph lives.
   std::shared_ptr<fo_graph_mem> graph_mem;
@@ -230,6 +235,8 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
                 const fo_op& op);
 // *flag = 1 when a tag byte is above 15 (not an execution id).
 // zip_with with in_t f32 where a and/or b is the bf16 source of a deferred exact widen (k_vector.hip).
+// map over an f32 input that is a deferred widen of bf16 data, read from that data (f32 or bf16 out).
+void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src_bf16, uint64_t n, const fo_op& op);
 void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, bool a_bf16, const void* b,
                         bool b_bf16, uint64_t n, const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

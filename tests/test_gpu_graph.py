@@ -11,6 +11,7 @@ import pytest
 import decode_chain as dc
 import furiosa_hip as fh
 import furiosa_hip.decode as fd
+from oracle import emulator as emu
 from test_oracle_step import step_case, tied_model
 
 pytestmark = pytest.mark.gpu
@@ -151,3 +152,46 @@ def test_recording_rejects_calls_that_wait(rt):
     assert np.allclose(y.read(F32), np.e, rtol=1e-6)
     graph.free()
     other.free()
+
+
+def test_recorded_widen_of_a_dropped_narrow(rt):
+    """Narrow into a temporary, widen it, drop the temporary, read the widen: once inside the
+    recording, and once with the temporary dropped before fo_graph_begin and its widen read inside
+    the recording. Launches for three inputs, each followed by buffers of both sizes allocated and
+    written, equal the numpy result of the chain; the later buffers keep their contents."""
+    n = 4096
+    rng = np.random.default_rng(41)
+    x = rt.upload(rng.standard_normal(n).astype(np.float32))
+    b = rt.upload(rng.standard_normal(n).astype(np.float32))
+
+    def narrow_widen(src):
+        t = rt.alloc(2 * n)
+        rt.map(t, BF16, src, F32, n, fh.op("CAST"))
+        w = rt.alloc(4 * n)
+        rt.map(w, F32, t, BF16, n, fh.op("CAST"))
+        return w  # t dropped here
+
+    x0 = rt.upload(rng.standard_normal(n).astype(np.float32))
+    w0 = narrow_widen(x0)
+    rt.graph_begin()
+    w = narrow_widen(x)
+    out = rt.alloc(4 * n)
+    rt.zip_with(out, F32, w, b, F32, n, fh.op("MUL_F"))
+    del w
+    out0 = rt.alloc(4 * n)
+    rt.zip_with(out0, F32, w0, b, F32, n, fh.op("ADD_F"))
+    graph = rt.graph_end()  # w0 is an input of the graph: it stays alive while the graph does
+    bv = b.read(F32)
+    want0 = emu.bf16_to_f32(emu.f32_to_bf16(x0.read(F32))) + bv
+    for step in range(3):
+        v = rng.standard_normal(n).astype(np.float32) * (step + 1)
+        x.write(v)
+        print("launch", step, flush=True)
+        graph.launch()
+        others = [rt.upload(np.full(m, 0x3F80 + i, np.uint16)) for i, m in enumerate((n, 2 * n, n, 2 * n))]
+        want = emu.bf16_to_f32(emu.f32_to_bf16(v)) * bv
+        assert np.array_equal(out.read(F32), want), step
+        assert np.array_equal(out0.read(F32), want0), step
+        for i, o in enumerate(others):
+            assert np.all(o.read(np.uint16) == 0x3F80 + i), (step, i)
+    graph.free()

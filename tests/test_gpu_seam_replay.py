@@ -155,13 +155,15 @@ def test_widen_record_dropped_when_the_source_is_rewritten(rt):
 
 
 def test_widened_contraction_matches_the_f32_fold(rt):
-    """contraction_prewidened over two widened bf16 operands: through the narrow sources, the generic
-    fold is bit-exact with the f32 fold (M = 4 < 8 keeps it off the MFMA kernels)."""
+    """contraction_prewidened over two widened bf16 operands whose k axis is not contiguous in lhs
+    (lhs stored K-major), so no GEMM or GEMV kernel takes it: the generic fold reads the narrow
+    sources (kept alive here, so the widens stay pending) and is bit-exact with the f32 fold."""
     s = dict(M=4, N=96, K=160)
     rng = np.random.default_rng(43)
     a = emu.f32_to_bf16(rng.standard_normal(4 * 160).astype(np.float32))
     b = emu.f32_to_bf16(rng.standard_normal(96 * 160).astype(np.float32))
-    la, lb = widen(rt, rt.upload(a), 4 * 160), widen(rt, rt.upload(b), 96 * 160)
+    sa, sb = rt.upload(np.ascontiguousarray(a.reshape(4, 160).T).ravel()), rt.upload(b)
+    la, lb = widen(rt, sa, 4 * 160), widen(rt, sb, 96 * 160)
     out = rt.alloc(4 * 96 * 4)
-    rt.contraction(out, la, lb, F32, F32, *(fh.m(t, **s) for t in ("M, K", "N, K", "M, N, K", "M, N")))
+    rt.contraction(out, la, lb, F32, F32, *(fh.m(t, **s) for t in ("K, M", "N, K", "M, N, K", "M, N")))
     assert np.array_equal(out.read(np.float32), emu.gemm_rows(a, b, 4, 96, 160, 0, 4, out_t=F32))

@@ -1038,6 +1038,80 @@ def test_zip_reads_deferred_widens(rt, n, which, op):
     assert np.array_equal(got, eager.read(np.uint32))
 
 
+@pytest.mark.parametrize("n", [4096, 1003])
+@pytest.mark.parametrize("case", [(F32, "SIGMOID", 0, 0.0), (F32, "EXP", 0, 0.0), (F32, "SQRT", 0, 0.0),
+                                  (F32, "DIV_F", fh.RHS_IMM, 3.0), (BF16, "CAST", 0, 0.0), (BF16, "TANH", 0, 0.0)],
+                         ids=lambda c: f"{c[1]}->{'f32' if c[0] == F32 else 'bf16'}")
+def test_map_reads_deferred_widens(rt, n, case):
+    """A map whose f32 input is a still-deferred widen of bf16 data reads that data and widens it in
+    the kernel: bit-identical to the same map after the cast has run (f32 and bf16 outputs, an
+    immediate operand), on bf16 subnormals, signed zeros, NaN and large values, with and without a
+    vector tail."""
+    dst_t, name, flags, imm = case
+    rng = np.random.default_rng(39)
+    v = special_bf16(rng, n)
+    v[::89] = 0x7FC1
+    src = rt.upload(v)
+    print(f"map widened {name} n {n}", flush=True)
+    w = rt.alloc(4 * n)
+    rt.map(w, F32, src, BF16, n, fh.op("CAST"))  # recorded, not run
+    o = fh.op(name, flags, imm)
+    lazy = rt.alloc((4 if dst_t == F32 else 2) * n)
+    rt.map(lazy, dst_t, w, F32, n, o)
+    got = lazy.read(np.uint32 if dst_t == F32 else np.uint16)
+    w.read(np.uint32)  # the cast runs now
+    eager = rt.alloc((4 if dst_t == F32 else 2) * n)
+    rt.map(eager, dst_t, w, F32, n, o)
+    assert np.array_equal(got, eager.read(np.uint32 if dst_t == F32 else np.uint16))
+
+
+def test_widen_of_a_dropped_narrow(rt):
+    """The engine's narrow-then-widen idiom (map f32 -> bf16 into a temporary, widen it back, drop the
+    temporary): the dropped temporary is kept while its widen is pending, so buffers allocated and
+    written after the drop (same sizes, so the same pool blocks if the temporary's had been freed)
+    leave it alone. A zip and a GEMV contraction over such widens, and a zip after the widen was
+    read whole, equal the same calls with the temporaries kept alive, bit for bit; the later buffers
+    keep their contents."""
+    rng = np.random.default_rng(37)
+    n, k = 300, 200
+    xs = rt.upload((rng.standard_normal(k) * 3).astype(np.float32))
+    ws = rt.upload(rng.standard_normal(n * k).astype(np.float32))
+    ys = rt.upload(rng.standard_normal(k).astype(np.float32))
+    maps = [fh.m(t, N=n, K=k) for t in ("K", "N, K", "N, K", "N")]
+
+    def narrow_widen(src, m, keep):
+        t = rt.alloc(2 * m)
+        rt.map(t, BF16, src, F32, m, fh.op("CAST"))
+        w = rt.alloc(4 * m)
+        rt.map(w, F32, t, BF16, m, fh.op("CAST"))
+        keep.append(t)
+        return w
+
+    def chain(drop):
+        keep = []
+        xw, ww = narrow_widen(xs, k, keep), narrow_widen(ws, n * k, keep)
+        yw = narrow_widen(xs, k, keep)
+        if drop:
+            keep.clear()
+        others = [rt.upload(np.full(m, 0x3F80 + i, np.uint16)) for i, m in enumerate((k, n * k, k))]
+        z = rt.alloc(4 * k)
+        rt.zip_with(z, F32, xw, ys, F32, k, fh.op("MUL_F"))
+        g = rt.alloc(4 * n)
+        rt.contraction(g, xw, ww, F32, F32, *maps)
+        first = yw.read(np.uint32)  # the widen runs here; the record stays
+        z2 = rt.alloc(4 * k)
+        rt.zip_with(z2, F32, yw, ys, F32, k, fh.op("ADD_F"))
+        for i, o in enumerate(others):
+            assert np.all(o.read(np.uint16) == 0x3F80 + i), (drop, i)
+        return z.read(np.uint32), g.read(np.uint32), first, z2.read(np.uint32)
+
+    print("widen of a dropped narrow", flush=True)
+    got, want = chain(True), chain(False)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
+    assert np.array_equal(got[2], emu.bf16_to_f32(emu.f32_to_bf16(xs.read(F32))).view(np.uint32))
+
+
 @pytest.mark.parametrize("case", ["broadcast", "transpose", "window"])
 def test_transpose_reads_deferred_widens(rt, case):
     """A transpose of a still-deferred bf16 -> f32 widen (the decode step's broadcast of a widened
