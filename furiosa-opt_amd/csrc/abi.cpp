@@ -71,19 +71,22 @@ void fo_pool::release(void* ptr, uint64_t capacity) {
 
 namespace {
 
-// Pending widens. The engine widens both contraction operands with Backend::map before
+// Pending casts. The engine widens both contraction operands with Backend::map before
 // contraction_prewidened (contract_outer, engine/contraction/outer/mod.rs:145-163), so a
 // contraction over f32 (i32) operands usually reads buffers that are exact casts of bf16 or 8-bit
 // float (i8) data. fo_map records each such cast (dst, src, source type, element count) and defers
 // the cast itself: a contraction whose two operands both have a record of the same source type
 // reads the narrow sources instead -- the MFMA kernels consume them directly, and the generic fold
 // widens them the same way the map would, so its result is unchanged -- and never needs the wide
-// copy. Any other use of the wide buffer (check_buf) runs the deferred cast first, on the stream of
-// the runtime that issued it; so does a write to its source (note_write), before the source
-// changes. A write to either side drops the record. A source freed by its owner while a record reads
-// it is kept until the last such record goes (retire_source), so an engine that narrows into a
-// temporary, widens it and drops the temporary still has the cast deferred. Records are
-// process-wide, as buffers are.
+// copy. The engine's kernels also round f32 results to bf16 and widen them back before the next
+// f32 step (a narrow, then a widen); the f32 -> bf16 cast is deferred the same way, and a zip, map
+// or reduce that reads such a widen reads the f32 data and rounds it on load. Any other use of a
+// buffer with a deferred cast into it (check_buf) runs the cast first (and the cast into its source
+// before it), on the stream of the runtime that issued it; so does a write to its source
+// (note_write), before the source changes. A write to either side drops the record. A source freed
+// by its owner while a record reads it is kept (retired) until no record reads it, so an engine
+// that narrows into a temporary, widens it and drops the temporary still has both casts deferred.
+// Records are process-wide, as buffers are.
 struct WidenRecord {
   const fo_buffer* dst;
   const fo_buffer* src;
@@ -96,15 +99,9 @@ struct WidenRecord {
 };
 std::mutex g_widen_mu;
 std::vector<WidenRecord> g_widen;
+std::vector<fo_buffer*> g_retired;  // freed by their owners, kept while a record reads them
 
-// Runs deferred casts, in order, outside the lock.
-void run_deferred(const std::vector<WidenRecord>& rs) {
-  for (auto& r : rs) {
-    FO_HIP(hipSetDevice(r.rt->device));
-    launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
-    const_cast<fo_buffer*>(r.dst)->widen_pending = false;
-  }
-}
+bool is_narrow(const WidenRecord& r) { return r.src_t == FO_F32 && r.dst_t == FO_BF16; }
 
 // A buffer's block leaves it (the buffer is being freed, rec the recording open at that moment or
 // none), then the buffer goes. A block freed while recording stays with the recording's memory,
@@ -138,75 +135,102 @@ void free_block(fo_buffer* buf, const std::shared_ptr<fo_graph_mem>& rec) {
   delete buf;
 }
 
-// Erases the records that match; returns the retired sources no remaining record names (the
-// caller frees them after any cast that reads them has been launched). Called with the lock held.
+// Erases the records that match, then lets go of retired buffers that no record reads any more
+// (dropping the records that cast into them, which nothing can read now, and so on); returns those
+// buffers, for the caller to free once any cast that reads them has been launched. Lock held.
 template <typename Pred>
 std::vector<fo_buffer*> erase_records(Pred drop) {
-  std::vector<fo_buffer*> gone;
-  for (auto& r : g_widen)
-    if (drop(r) && r.src->retired &&
-        std::find(gone.begin(), gone.end(), r.src) == gone.end())
-      gone.push_back(const_cast<fo_buffer*>(r.src));
   g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(), drop), g_widen.end());
-  gone.erase(std::remove_if(gone.begin(), gone.end(),
-                            [](const fo_buffer* s) {
-                              return std::any_of(g_widen.begin(), g_widen.end(),
-                                                 [s](const WidenRecord& r) { return r.src == s; });
-                            }),
-             gone.end());
+  std::vector<fo_buffer*> gone;
+  for (bool changed = true; changed;) {
+    changed = false;
+    for (size_t i = 0; i < g_retired.size(); ++i) {
+      fo_buffer* b = g_retired[i];
+      if (std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.src == b; })) continue;
+      g_widen.erase(std::remove_if(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.dst == b; }),
+                    g_widen.end());
+      gone.push_back(b);
+      g_retired.erase(g_retired.begin() + (std::ptrdiff_t)i);
+      changed = true;
+      break;
+    }
+  }
   return gone;
 }
 
 void free_retired(const std::vector<fo_buffer*>& gone) {
-  for (fo_buffer* s : gone) {
-    std::shared_ptr<fo_graph_mem> rec = std::move(s->retired_in);
-    free_block(s, rec);
+  for (fo_buffer* b : gone) {
+    std::shared_ptr<fo_graph_mem> rec = std::move(b->retired_in);
+    free_block(b, rec);
   }
 }
 
-// b is about to be written: a deferred cast from or into it runs first, then its records go.
+void materialize(const fo_buffer* b);
+
+// Runs deferred casts, in order, outside the lock; a cast whose source has a deferred cast into it
+// runs that one first.
+void run_deferred(const std::vector<WidenRecord>& rs) {
+  for (auto& r : rs) {
+    materialize(r.src);
+    FO_HIP(hipSetDevice(r.rt->device));
+    launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
+    const_cast<fo_buffer*>(r.dst)->widen_pending = false;
+  }
+}
+
+// Narrow records whose casts have run serve nothing (only deferred ones are read through).
+void drop_run_narrows() {
+  std::vector<fo_buffer*> gone;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    gone = erase_records([](const WidenRecord& r) { return is_narrow(r) && !r.deferred; });
+  }
+  free_retired(gone);
+}
+
+// b is about to be written: a deferred cast into it (the write may be partial) and the deferred
+// casts that read it run first, each after the casts its own source waits for; then b's records go.
 void note_write(const fo_buffer* b) {
   if (!b) return;
-  std::vector<WidenRecord> todo;
-  std::vector<fo_buffer*> gone;
+  std::vector<const fo_buffer*> readers;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
     for (auto& r : g_widen)
-      if ((r.dst == b || r.src == b) && r.deferred) todo.push_back(r);
+      if (r.src == b && r.deferred && r.dst != b) readers.push_back(r.dst);
+  }
+  materialize(b);
+  for (const fo_buffer* d : readers) materialize(d);
+  std::vector<fo_buffer*> gone;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
     gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
   }
-  run_deferred(todo);
   free_retired(gone);
 }
 
-// b is being freed: a deferred cast from it runs first (its block may be reused right after); one
-// into it is dropped.
+// b is being freed and no record reads it (retire_source keeps it otherwise): a cast into it is
+// dropped.
 void forget_buffer(const fo_buffer* b) {
-  std::vector<WidenRecord> todo;
   std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
-    for (auto& r : g_widen)
-      if (r.src == b && r.deferred && r.dst != b) todo.push_back(r);
     gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
   }
-  run_deferred(todo);
   free_retired(gone);
 }
 
-// b is being freed while a widen record reads it as its source: it is kept (retired), so the cast
-// can stay deferred and a contraction can still read the narrow data; the block is freed when the
-// last such record goes. Returns false (nothing kept) when no record reads b.
+// b is being freed while a record reads it as its source: it is kept (retired), so the cast can stay
+// deferred and a contraction can still read the narrow data; the block is freed when the last such
+// record goes. Returns false (nothing kept) when no record reads b.
 bool retire_source(fo_buffer* b) {
   std::lock_guard<std::mutex> lock(g_widen_mu);
-  if (!std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.src == b && r.dst != b; }) ||
-      std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.dst == b; }))
-    return false;
+  if (!std::any_of(g_widen.begin(), g_widen.end(), [b](const WidenRecord& r) { return r.src == b; })) return false;
   b->retired = true;
   if (b->pool) {
     std::lock_guard<std::mutex> plock(b->pool->mu);
     b->retired_in = b->pool->recording;
   }
+  g_retired.push_back(b);
   return true;
 }
 
@@ -221,7 +245,8 @@ void free_run_retired() {
   free_retired(gone);
 }
 
-// b is about to be read: its deferred cast, if any, runs first (the record stays for contractions).
+// b is about to be read: its deferred cast, if any, runs first (a widen record stays for
+// contractions).
 void materialize(const fo_buffer* b) {
   if (!b->widen_pending) return;
   std::vector<WidenRecord> todo;
@@ -234,9 +259,11 @@ void materialize(const fo_buffer* b) {
       }
   }
   run_deferred(todo);
+  drop_run_narrows();
 }
 
-// A runtime going away: every cast it deferred runs now, on its stream.
+// A runtime going away, or a recording starting or ending: every cast it deferred runs now, on its
+// stream.
 void materialize_runtime(fo_runtime* rt) {
   std::vector<WidenRecord> todo;
   {
@@ -248,6 +275,7 @@ void materialize_runtime(fo_runtime* rt) {
       }
   }
   run_deferred(todo);
+  drop_run_narrows();
 }
 
 void record_widen(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype dst_t, fo_dtype src_t, uint64_t n,
@@ -270,10 +298,38 @@ bool deferred_bf16_widen(const fo_runtime* rt, const fo_buffer* b, uint64_t n, W
   return false;
 }
 
+// b holds a narrow of at least n f32 elements into bf16, recorded on rt and not yet run.
+bool deferred_bf16_narrow(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenRecord* out) {
+  if (!b || !b->widen_pending) return false;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == b && r.deferred) {
+      if (r.rt != rt || !is_narrow(r) || r.op.code != FO_OP_CAST || r.n < n) return false;
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
+// How a zip, map or reduce reads an f32 input b of n elements (dst: the op's output, which the read
+// must not alias): the buffer itself (code 4), the bf16 source of its deferred widen (2), or the f32
+// source of that bf16's deferred narrow (kReadViaBf16). `buf` is what the kernel reads and what the
+// caller checks.
+struct F32Read {
+  const fo_buffer* buf;
+  int code;
+};
+F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_buffer* dst) {
+  WidenRecord w{}, nr{};
+  if (!deferred_bf16_widen(rt, b, n, &w) || w.src == dst) return {b, 4};
+  if (deferred_bf16_narrow(rt, w.src, n, &nr) && nr.src != dst) return {nr.src, kReadViaBf16};
+  return {w.src, 2};
+}
+
 bool find_widen(const fo_buffer* dst, WidenRecord* out) {
   std::lock_guard<std::mutex> lock(g_widen_mu);
   for (auto& r : g_widen)
-    if (r.dst == dst) {
+    if (r.dst == dst && !is_narrow(r)) {
       *out = r;
       return true;
     }
@@ -382,13 +438,18 @@ void fill_pending(fo_runtime* rt, const fo_buffer* b) {
 void check_ptr(const fo_buffer* b, const char* what) {
   require(b != nullptr && b->ptr != nullptr, std::string(what) + " buffer is NULL");
 }
-// A buffer an op reads, or writes in part: its deferred zero fill goes first.
-void check_buf(const fo_buffer* b, const char* what) {
+// A buffer whose zero fill, if deferred, must run now (a deferred cast into it may stay deferred).
+void check_filled(const fo_buffer* b, const char* what) {
   check_ptr(b, what);
   if (b->zero_pending) {
     require(t_rt != nullptr, "buffer used before any runtime call on this thread");
     fill_pending(t_rt, b);
   }
+}
+// A buffer an op reads, or writes in part: its deferred zero fill and any deferred cast into it go
+// first.
+void check_buf(const fo_buffer* b, const char* what) {
+  check_filled(b, what);
   materialize(b);
 }
 // An op's output, just before its launch: `written` bytes from the start are overwritten; when
@@ -1088,27 +1149,31 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     require(op != nullptr, "op is NULL");
     check_ptr(src, "src");
     require(span_bytes(dst_t, n) <= dst->bytes && span_bytes(src_t, n) <= src->bytes, "map: n exceeds a buffer");
-    // An f32 input that is a still-deferred exact widen of bf16 data is read from that data and
-    // widened in the kernel, so the cast need not run.
-    WidenRecord ws{};
-    const bool narrow = src_t == FO_F32 && (dst_t == FO_F32 || dst_t == FO_BF16) &&
-                        deferred_bf16_widen(rt, src, n, &ws) && ws.src != dst;
-    check_buf(narrow ? ws.src : src, "src");
+    // An f32 input that stands for a deferred cast (a widen of bf16 data, maybe of a deferred
+    // narrow) is read from the data it stands for, and the casts need not run.
+    const F32Read rs = src_t == FO_F32 && (dst_t == FO_F32 || dst_t == FO_BF16) ? f32_read(rt, src, n, dst)
+                                                                               : F32Read{src, 4};
+    // An exact widening cast (the engine's contract_outer widen), or a narrowing cast of f32 data to
+    // bf16, is recorded and deferred until something reads its output other than through it. Its
+    // source gets its zero fill now; a deferred cast into the source stays deferred (running this
+    // one runs that one first).
+    const bool widen = op->code == FO_OP_CAST && dst != src &&
+                       ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
+                        (dst_t == FO_I32 && src_t == FO_I8) || (dst_t == FO_BF16 && src_t == FO_F32 && rs.code == 4));
+    if (widen)
+      check_filled(src, "src");
+    else
+      check_buf(rs.buf, "src");
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, span_bytes(dst_t, n));
-    // An exact widening cast (the engine's contract_outer widen) is recorded for the contraction
-    // that follows and deferred until something else needs the wide copy.
-    const bool widen = op->code == FO_OP_CAST && dst != src &&
-                       ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
-                        (dst_t == FO_I32 && src_t == FO_I8));
     if (widen) {
       record_widen(rt, dst, src, dst_t, src_t, n, *op);
       return;
     }
     TraceScope trace_span(rt, "map");
-    if (narrow)
-      launch_map_widened(rt->stream, dst->ptr, dst_t, ws.src->ptr, n, *op);
+    if (rs.code != 4)
+      launch_map_widened(rt->stream, dst->ptr, dst_t, rs.buf->ptr, rs.code, n, *op);
     else
       launch_map(rt->stream, dst->ptr, dst_t, src->ptr, src_t, n, *op);
   });
@@ -1124,20 +1189,19 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
     require(n * dtype_bytes(dst_t) <= dst->bytes && n * dtype_bytes(in_t) <= a->bytes &&
                 n * dtype_bytes(in_t) <= b->bytes,
             "zip_with: n exceeds a buffer");
-    // An f32 input that is a still-deferred exact widen of bf16 data is read from that data and
-    // widened in the kernel, so the cast need not run.
-    WidenRecord wa{}, wb{};
-    const bool na = in_t == FO_F32 && dst_t == FO_F32 && deferred_bf16_widen(rt, a, n, &wa);
-    const bool nb = in_t == FO_F32 && dst_t == FO_F32 && deferred_bf16_widen(rt, b, n, &wb);
-    check_buf(na ? wa.src : a, "a");
-    check_buf(nb ? wb.src : b, "b");
+    // An f32 input that stands for a deferred cast (a widen of bf16 data, maybe of a deferred
+    // narrow) is read from the data it stands for, and the casts need not run.
+    const bool wide_ok = in_t == FO_F32 && dst_t == FO_F32;
+    const F32Read ra = wide_ok ? f32_read(rt, a, n, dst) : F32Read{a, 4};
+    const F32Read rb = wide_ok ? f32_read(rt, b, n, dst) : F32Read{b, 4};
+    check_buf(ra.buf, "a");
+    check_buf(rb.buf, "b");
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, n * dtype_bytes(dst_t));
     TraceScope trace_span(rt, "zip_with");
-    if (na || nb)
-      launch_zip_widened(rt->stream, dst->ptr, dst_t, na ? wa.src->ptr : a->ptr, na, nb ? wb.src->ptr : b->ptr, nb, n,
-                         *op);
+    if (ra.code != 4 || rb.code != 4)
+      launch_zip_widened(rt->stream, dst->ptr, dst_t, ra.buf->ptr, ra.code, rb.buf->ptr, rb.code, n, *op);
     else
       launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
   });
@@ -1560,17 +1624,17 @@ int32_t fo_reduce(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype
     const Wheels<1> owd = to_desc<1>(ow, mem), rwd = to_desc<1>(rw, mem);
     const int64_t src_len = (int64_t)(src->bytes / eb);
     const ReduceSplit split = plan_reduce_split(t, op, src->ptr, src_len, out_count, owd, rwd);
-    // An f32 source that is a still-deferred widen of bf16 data (covering the whole buffer) is read
-    // from that data, widened on load, unless the two-pass column form is chosen.
-    WidenRecord ws{};
-    const bool narrow = t == FO_F32 && split.nchunks == 0 && src != dst &&
-                        deferred_bf16_widen(rt, src, (uint64_t)src_len, &ws) && ws.src != dst;
-    check_buf(narrow ? ws.src : src, "src");
+    // An f32 source that stands for a deferred widen of bf16 data (covering the whole buffer), maybe
+    // of a deferred narrow, is read from the data it stands for, unless the two-pass column form is
+    // chosen.
+    const F32Read rs = t == FO_F32 && split.nchunks == 0 && src != dst ? f32_read(rt, src, (uint64_t)src_len, dst)
+                                                                        : F32Read{src, 4};
+    check_buf(rs.buf, "src");
     claim_out(rt, dst, (uint64_t)(out_count * eb));  // every cell is written, a dead one with the identity
     TraceScope trace_span(rt, "reduce");
-    if (narrow)
-      launch_reduce_widened(rt->stream, dst->ptr, (const uint16_t*)ws.src->ptr, src_len, out_count, owd, rwd, op,
-                            identity);
+    if (rs.code != 4)
+      launch_reduce_widened(rt->stream, dst->ptr, rs.buf->ptr, rs.code == kReadViaBf16, src_len, out_count, owd, rwd,
+                            op, identity);
     else if (split.nchunks > 0)
       launch_reduce_split(rt->stream, dst->ptr, src->ptr, t, out_count, owd, rwd, op, identity, split,
                           runtime_scratch(rt, split.scratch_bytes));
@@ -1640,6 +1704,9 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     if (!narrow) {
       check_buf(lhs, "lhs");
       check_buf(rhs, "rhs");
+    } else {  // the narrow sources, made current (a deferred narrow into one runs here)
+      check_buf(wl.src, "lhs");
+      check_buf(wr.src, "rhs");
     }
     if (in_t == FO_I4) {
       auto up = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };

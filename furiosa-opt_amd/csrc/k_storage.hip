@@ -712,6 +712,15 @@ template <>
 struct RedT<WidenedBf16> : RedT<float> {
   static __device__ __forceinline__ float load(const void* p, int64_t i) { return bf16_to_f32(((const uint16_t*)p)[i]); }
 };
+// An f32 fold over f32 data standing for the widen of its bf16 narrow (a deferred narrow read
+// through a deferred widen): each element is rounded on load by the narrow's rule, then widened.
+struct RoundedBf16 {};
+template <>
+struct RedT<RoundedBf16> : RedT<float> {
+  static __device__ __forceinline__ float load(const void* p, int64_t i) {
+    return bf16_to_f32(f32_to_bf16(((const float*)p)[i]));
+  }
+};
 
 template <>
 struct RedT<int32_t> {
@@ -1181,7 +1190,8 @@ void reduce_t(hipStream_t s, void* dst, const void* src, int64_t src_len, int64_
   // parallelism: a wave per cell when the residue is contiguous, 64 cells x kSeg segments per block
   // when the cells are. For f32 that reassociates the sum, which BufStorage::reduce's own contract
   // accepts (buf.rs:316-330) and the f32 tolerance covers.
-  constexpr bool is_f32 = std::is_same<Tag, float>::value || std::is_same<Tag, WidenedBf16>::value;
+  constexpr bool is_f32 = std::is_same<Tag, float>::value || std::is_same<Tag, WidenedBf16>::value ||
+                         std::is_same<Tag, RoundedBf16>::value;
   const bool exact_only = std::is_same<Tag, Bf16Red>::value || op == FO_RED_ADD_SAT;
   const bool res_contig = rw.n > 0 && rw.stride[0][0] == 1;
   const bool cells_contig = ow.n > 0 && ow.stride[0][0] == 1;
@@ -1306,9 +1316,12 @@ void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_
   }
 }
 
-void launch_reduce_widened(hipStream_t s, void* dst, const uint16_t* src, int64_t src_len, int64_t out_count,
-                           const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity) {
-  reduce_t<WidenedBf16>(s, dst, src, src_len, out_count, ow, rw, op, identity);
+void launch_reduce_widened(hipStream_t s, void* dst, const void* src, bool via_bf16, int64_t src_len,
+                           int64_t out_count, const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity) {
+  if (via_bf16)
+    reduce_t<RoundedBf16>(s, dst, src, src_len, out_count, ow, rw, op, identity);
+  else
+    reduce_t<WidenedBf16>(s, dst, src, src_len, out_count, ow, rw, op, identity);
 }
 
 // ---------------------------------------------------------------------------------------------

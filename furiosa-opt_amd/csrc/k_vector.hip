@@ -362,15 +362,23 @@ __global__ void __launch_bounds__(kBlock) k_zip_v(void* __restrict__ dst, const 
   }
 }
 
-// zip_with over f32 inputs, either of which may be given as the bf16 source of a deferred exact
-// widen (AB or BB = 2): its words are widened here by the cast's own rule (bf16_to_f32), so the
-// result is the same as zipping the materialized f32 copy, which then never needs writing.
-__device__ __forceinline__ uint32_t widened_word(uint32_t raw, int width) {
-  return width == 2 ? f32_bits(bf16_to_f32((uint16_t)raw)) : raw;
+// zip_with and map over f32 inputs that may stand for a deferred cast. An input's read code: 4 =
+// f32 data, read as is; 2 = bf16 data standing for its exact widen (a deferred widening cast),
+// widened on load by the cast's own rule (bf16_to_f32); kViaBf16 = f32 data standing for the widen
+// of its deferred bf16 narrow, rounded on load by the narrow's rule (f32_to_bf16) and widened. The
+// result is the same as that of the kernel over the materialized f32 copy, which then never needs
+// writing.
+constexpr int kViaBf16 = kReadViaBf16;
+constexpr int code_bytes(int code) { return code == kViaBf16 ? 4 : code; }
+__device__ __forceinline__ uint32_t widened_word(uint32_t raw, int code) {
+  if (code == 2) return f32_bits(bf16_to_f32((uint16_t)raw));
+  if (code == kViaBf16) return f32_bits(bf16_to_f32(f32_to_bf16(bits_f32(raw))));
+  return raw;
 }
-template <int AB, int BB, int OB>
+template <int AC, int BC, int OB>
 __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const void* __restrict__ a,
                                                   const void* __restrict__ b, uint64_t n, fo_op op) {
+  constexpr int AB = code_bytes(AC), BB = code_bytes(BC);
   constexpr int MINB = AB < BB ? (AB < OB ? AB : OB) : (BB < OB ? BB : OB);
   constexpr int V = 16 / MINB;
   const uint64_t nv = (n + V - 1) / V;
@@ -383,39 +391,41 @@ __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const 
       rb.load((const uint8_t*)b + j * V * BB);
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        out.template set<OB>(e, combine(op, widened_word(ra.template get<AB>(e), AB),
-                                        widened_word(rb.template get<BB>(e), BB), op.imm1));
+        out.template set<OB>(e, combine(op, widened_word(ra.template get<AB>(e), AC),
+                                        widened_word(rb.template get<BB>(e), BC), op.imm1));
       out.store((uint8_t*)dst + j * V * OB);
     } else {
       for (uint64_t i = j * V; i < n; ++i)
-        store_raw<OB>(dst, i, combine(op, widened_word(load_raw<AB>(a, i), AB), widened_word(load_raw<BB>(b, i), BB),
+        store_raw<OB>(dst, i, combine(op, widened_word(load_raw<AB>(a, i), AC), widened_word(load_raw<BB>(b, i), BC),
                                       op.imm1));
     }
   }
 }
 
-// map over an f32 input given as the bf16 source of a deferred exact widen: each word is widened by
-// the cast's own rule, then mapped as the f32 word it stands for.
-template <int DB>
+// map over such an input (read code SC, 2 or kViaBf16): each word is widened on load as above, then
+// mapped as the f32 word it stands for. Lanes carry 16 bytes of the wider side: at the small sizes
+// these casts come in, a lane's serial chain of slow ops (sigmoid, exp) sets the time.
+template <int SC, int DB>
 __global__ void __launch_bounds__(kBlock) k_map_w(void* __restrict__ dst, const void* __restrict__ src, uint64_t n,
                                                   fo_dtype dst_t, fo_op op) {
-  constexpr int V = lanes_for<2, DB>();
+  constexpr int SB = code_bytes(SC);
+  constexpr int V = 16 / (SB > DB ? SB : DB);
   const uint64_t nv = (n + V - 1) / V;
   for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
     if ((j + 1) * V <= n) {
-      Regs<V * 2> in;
+      Regs<V * SB> in;
       Regs<V * DB> out;
-      in.load((const uint8_t*)src + j * V * 2);
+      in.load((const uint8_t*)src + j * V * SB);
       uint32_t w[V], r[V];
 #pragma unroll
-      for (int e = 0; e < V; ++e) w[e] = widened_word(in.template get<2>(e), 2);
+      for (int e = 0; e < V; ++e) w[e] = widened_word(in.template get<SB>(e), SC);
       map_words<V>(w, r, FO_F32, dst_t, op);
 #pragma unroll
       for (int e = 0; e < V; ++e) out.template set<DB>(e, r[e]);
       out.store((uint8_t*)dst + j * V * DB);
     } else {
       for (uint64_t i = j * V; i < n; ++i)
-        store_raw<DB>(dst, i, map_word(widened_word(load_raw<2>(src, i), 2), FO_F32, dst_t, op));
+        store_raw<DB>(dst, i, map_word(widened_word(load_raw<SB>(src, i), SC), FO_F32, dst_t, op));
     }
   }
 }
@@ -762,39 +772,49 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
   throw InvalidArg("zip_with: unsupported element widths");
 }
 
-void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, bool a_bf16, const void* b,
-                        bool b_bf16, uint64_t n, const fo_op& op) {
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const void* b,
+                        int b_code, uint64_t n, const fo_op& op) {
   require(dst_t == FO_F32, "zip_with: widened inputs take f32 outputs");
   require(aligned16(dst) && aligned16(a) && aligned16(b), "zip_with: buffers must be 16-byte aligned");
-  const int ab = a_bf16 ? 2 : 4, bb = b_bf16 ? 2 : 4, ob = width_of(dst_t);
-#define FO_ZIPW_CASE(A, B, O)                                                                                  \
-  if (ab == A && bb == B && ob == O) {                                                                         \
-    constexpr int MINB = A < B ? (A < O ? A : O) : (B < O ? B : O);                                            \
-    hipLaunchKernelGGL((k_zip_w<A, B, O>), dim3(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB)))),      \
+#define FO_ZIPW_CASE(A, B)                                                                                     \
+  if (a_code == A && b_code == B) {                                                                            \
+    constexpr int MINB = code_bytes(A) < code_bytes(B) ? code_bytes(A) : code_bytes(B);                        \
+    hipLaunchKernelGGL((k_zip_w<A, B, 4>), dim3(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB)))),      \
                        dim3(kBlock), 0, s, dst, a, b, n, op);                                                  \
     FO_HIP(hipGetLastError());                                                                                 \
     return;                                                                                                    \
   }
-  FO_ZIPW_CASE(2, 4, 4);
-  FO_ZIPW_CASE(4, 2, 4);
-  FO_ZIPW_CASE(2, 2, 4);
+  FO_ZIPW_CASE(2, 4);
+  FO_ZIPW_CASE(4, 2);
+  FO_ZIPW_CASE(2, 2);
+  FO_ZIPW_CASE(kViaBf16, 4);
+  FO_ZIPW_CASE(4, kViaBf16);
+  FO_ZIPW_CASE(kViaBf16, kViaBf16);
+  FO_ZIPW_CASE(kViaBf16, 2);
+  FO_ZIPW_CASE(2, kViaBf16);
 #undef FO_ZIPW_CASE
   throw InvalidArg("zip_with: no widened form for these inputs");
 }
 
-void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src_bf16, uint64_t n, const fo_op& op) {
-  require(aligned16(dst) && aligned16(src_bf16), "map: buffers must be 16-byte aligned");
-  if (dst_t == FO_F32) {
-    constexpr int V = lanes_for<2, 4>();
-    hipLaunchKernelGGL((k_map_w<4>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, src_bf16,
-                       n, dst_t, op);
-  } else {
-    require(dst_t == FO_BF16, "map: a widened input takes f32 or bf16 outputs");
-    constexpr int V = lanes_for<2, 2>();
-    hipLaunchKernelGGL((k_map_w<2>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, src_bf16,
-                       n, dst_t, op);
+void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, int src_code, uint64_t n,
+                        const fo_op& op) {
+  require(aligned16(dst) && aligned16(src), "map: buffers must be 16-byte aligned");
+  require(dst_t == FO_F32 || dst_t == FO_BF16, "map: a widened input takes f32 or bf16 outputs");
+  require(src_code == 2 || src_code == kViaBf16, "map: unknown widened input code");
+#define FO_MAPW_CASE(SC, DB)                                                                                   \
+  if (src_code == SC && (int)dtype_bytes(dst_t) == DB) {                                                       \
+    constexpr int V = 16 / (code_bytes(SC) > DB ? code_bytes(SC) : DB);                                        \
+    hipLaunchKernelGGL((k_map_w<SC, DB>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, \
+                       src, n, dst_t, op);                                                                     \
+    FO_HIP(hipGetLastError());                                                                                 \
+    return;                                                                                                    \
   }
-  FO_HIP(hipGetLastError());
+  FO_MAPW_CASE(2, 4);
+  FO_MAPW_CASE(2, 2);
+  FO_MAPW_CASE(kViaBf16, 4);
+  FO_MAPW_CASE(kViaBf16, 2);
+#undef FO_MAPW_CASE
+  throw InvalidArg("map: no widened form for this output");
 }
 
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

@@ -234,19 +234,24 @@ void launch_pack_i4(hipStream_t s, void* dst, const int32_t* src, uint64_t n);
 void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const void* b, fo_dtype in_t, uint64_t n,
                 const fo_op& op);
 // *flag = 1 when a tag byte is above 15 (not an execution id).
-// zip_with with in_t f32 where a and/or b is the bf16 source of a deferred exact widen (k_vector.hip).
-// map over an f32 input that is a deferred widen of bf16 data, read from that data (f32 or bf16 out).
-void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src_bf16, uint64_t n, const fo_op& op);
-void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, bool a_bf16, const void* b,
-                        bool b_bf16, uint64_t n, const fo_op& op);
+// zip_with (f32 out) and map (f32 or bf16 out) over f32 inputs that stand for deferred casts
+// (k_vector.hip). An input's read code: 4 = f32 data as is; 2 = the bf16 source of a deferred exact
+// widen; kReadViaBf16 = the f32 source of a deferred bf16 narrow that a deferred widen reads,
+// rounded through bf16 on load.
+constexpr int kReadViaBf16 = 5;
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const void* b,
+                        int b_code, uint64_t n, const fo_op& op);
+void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, int src_code, uint64_t n,
+                        const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,
                        uint64_t n, const fo_slots& slots, int32_t* flag);
 void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t, uint64_t n, const fo_cmp* cmps);
 
 // Reduce over a plan: out wheels (memory strides into src) and residue wheels.
-// An f32 reduce whose source is bf16 data standing for its exact widen (k_storage.hip).
-void launch_reduce_widened(hipStream_t s, void* dst, const uint16_t* src, int64_t src_len, int64_t out_count,
-                           const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity);
+// An f32 reduce whose source is bf16 data standing for its exact widen, or (via_bf16) f32 data
+// standing for the widen of its deferred bf16 narrow (k_storage.hip).
+void launch_reduce_widened(hipStream_t s, void* dst, const void* src, bool via_bf16, int64_t src_len,
+                           int64_t out_count, const Wheels<1>& ow, const Wheels<1>& rw, int op, uint32_t identity);
 void launch_reduce(hipStream_t s, void* dst, const void* src, fo_dtype t, int64_t src_len, int64_t out_count,
                    const Wheels<1>& out_w, const Wheels<1>& res_w, int op, uint32_t identity);
 

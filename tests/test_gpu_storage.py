@@ -1065,6 +1065,80 @@ def test_map_reads_deferred_widens(rt, n, case):
     assert np.array_equal(got, eager.read(np.uint32 if dst_t == F32 else np.uint16))
 
 
+def special_f32(rng, n):
+    """f32 values that exercise the bf16 narrow's rules: normals at several scales, exact rounding
+    ties (low half 0x8000, even and odd), f32 subnormals, signed zeros, NaN, infinities and values
+    that round past the bf16 range."""
+    v = (rng.standard_normal(n) * np.float32(10.0) ** rng.integers(-3, 4, n)).astype(np.float32)
+    u = v.view(np.uint32)
+    u[::7] = (u[::7] & 0xFFFF0000) | 0x8000  # ties
+    specials = np.array([0x00000001, 0x807FFFFF, 0x00400000, 0x80000000, 0x00000000, 0x7FC00001, 0xFFC00000,
+                         0x7F800000, 0xFF800000, 0x7F7FFFFF, 0x7F7F8000, 0x3F808000, 0x3F818000], np.uint32)
+    u[3::29][:len(specials)] = specials[:len(u[3::29])]
+    return u.view(np.float32)
+
+
+@pytest.mark.parametrize("drop", [False, True], ids=["kept", "dropped"])
+@pytest.mark.parametrize("consumer", ["zip", "zip_both", "zip_bf16", "map", "map_bf16", "reduce_rows",
+                                      "reduce_cols", "rewrite"])
+def test_narrow_read_through_its_widen(rt, consumer, drop):
+    """f32 data narrowed to bf16 and widened back (both casts deferred) and read by a zip, map or
+    reduce: the kernel reads the f32 data and rounds it on load. Bit-identical to the same op over the
+    narrowed-and-widened values uploaded as f32, with the bf16 temporary kept or dropped; `rewrite`
+    writes the f32 source after the casts were recorded, which runs the narrow first, so the read
+    still sees the old values."""
+    rng = np.random.default_rng(45)
+    r, c = 64, 96
+    n = r * c
+    xv, x2v = special_f32(rng, n), special_f32(rng, n)
+    yv = rng.standard_normal(n).astype(np.float32)
+    x, x2, y = rt.upload(xv), rt.upload(x2v), rt.upload(yv)
+    keep = []
+
+    def through(src):
+        t = rt.alloc(2 * n)
+        rt.map(t, BF16, src, F32, n, fh.op("CAST"))
+        w = rt.alloc(4 * n)
+        rt.map(w, F32, t, BF16, n, fh.op("CAST"))
+        if not drop:
+            keep.append(t)
+        return w
+
+    def rounded(v):
+        return rt.upload(emu.bf16_to_f32(emu.f32_to_bf16(v)))
+
+    def run(a, b, out_t=F32):
+        if consumer in ("zip", "zip_both", "zip_bf16", "rewrite"):
+            out = rt.alloc(4 * n)
+            rt.zip_with(out, F32, a, b, F32, n, fh.op("MUL_F" if consumer == "zip_both" else "ADD_F"))
+            return out.read(np.uint32)
+        if consumer in ("map", "map_bf16"):
+            dt = F32 if consumer == "map" else BF16
+            out = rt.alloc((4 if dt == F32 else 2) * n)
+            rt.map(out, dt, a, F32, n, fh.op("SIGMOID" if dt == F32 else "CAST"))
+            return out.read(np.uint32 if dt == F32 else np.uint16)
+        rows = consumer == "reduce_rows"
+        out = rt.alloc(4 * (r if rows else c))
+        rt.reduce(out, a, F32, fh.m("R, C", R=r, C=c), fh.m("R" if rows else "C", R=r, C=c), fh.RED["ADD"], 0)
+        return out.read(np.uint32)
+
+    print(f"narrow through widen {consumer} drop {drop}", flush=True)
+    if consumer == "zip_both":
+        got, want = run(through(x), through(x2)), run(rounded(xv), rounded(x2v))
+    elif consumer == "zip_bf16":
+        b16 = rt.upload(emu.f32_to_bf16(x2v))
+        bw = rt.alloc(4 * n)
+        rt.map(bw, F32, b16, BF16, n, fh.op("CAST"))
+        got, want = run(bw, through(x)), run(rt.upload(emu.bf16_to_f32(emu.f32_to_bf16(x2v))), rounded(xv))
+    elif consumer == "rewrite":
+        w = through(x)
+        x.write(yv)
+        got, want = run(w, y), run(rounded(xv), y)
+    else:
+        got, want = run(through(x), y), run(rounded(xv), y)
+    assert np.array_equal(got, want)
+
+
 def test_widen_of_a_dropped_narrow(rt):
     """The engine's narrow-then-widen idiom (map f32 -> bf16 into a temporary, widen it back, drop the
     temporary): the dropped temporary is kept while its widen is pending, so buffers allocated and
