@@ -96,12 +96,18 @@ struct WidenRecord {
   fo_op op;
   fo_runtime* rt;  // the runtime whose stream the deferred cast goes on
   bool deferred;   // the cast has not run yet
+  // A broadcast (kind 1) instead of a cast: a transpose over the whole of the f32 dst whose src
+  // digits form one contiguous run, dst[i] = src[(i / div) % mod] for i < n; `wheels` launch it.
+  int kind = 0;
+  uint32_t div = 1, mod = 1;
+  Wheels<1> wheels{};
 };
 std::mutex g_widen_mu;
 std::vector<WidenRecord> g_widen;
 std::vector<fo_buffer*> g_retired;  // freed by their owners, kept while a record reads them
 
-bool is_narrow(const WidenRecord& r) { return r.src_t == FO_F32 && r.dst_t == FO_BF16; }
+bool is_narrow(const WidenRecord& r) { return r.kind == 0 && r.src_t == FO_F32 && r.dst_t == FO_BF16; }
+bool is_bcast(const WidenRecord& r) { return r.kind == 1; }
 
 // A buffer's block leaves it (the buffer is being freed, rec the recording open at that moment or
 // none), then the buffer goes. A block freed while recording stays with the recording's memory,
@@ -173,17 +179,20 @@ void run_deferred(const std::vector<WidenRecord>& rs) {
   for (auto& r : rs) {
     materialize(r.src);
     FO_HIP(hipSetDevice(r.rt->device));
-    launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
+    if (is_bcast(r))
+      launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, 4, 0, 0, (int64_t)r.n, r.wheels);
+    else
+      launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
     const_cast<fo_buffer*>(r.dst)->widen_pending = false;
   }
 }
 
-// Narrow records whose casts have run serve nothing (only deferred ones are read through).
+// Narrow and broadcast records that have run serve nothing (only deferred ones are read through).
 void drop_run_narrows() {
   std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
-    gone = erase_records([](const WidenRecord& r) { return is_narrow(r) && !r.deferred; });
+    gone = erase_records([](const WidenRecord& r) { return (is_narrow(r) || is_bcast(r)) && !r.deferred; });
   }
   free_retired(gone);
 }
@@ -291,7 +300,8 @@ bool deferred_bf16_widen(const fo_runtime* rt, const fo_buffer* b, uint64_t n, W
   std::lock_guard<std::mutex> lock(g_widen_mu);
   for (auto& r : g_widen)
     if (r.dst == b && r.deferred) {
-      if (r.rt != rt || r.src_t != FO_BF16 || r.dst_t != FO_F32 || r.op.code != FO_OP_CAST || r.n < n) return false;
+      if (r.rt != rt || r.kind != 0 || r.src_t != FO_BF16 || r.dst_t != FO_F32 || r.op.code != FO_OP_CAST || r.n < n)
+        return false;
       *out = r;
       return true;
     }
@@ -311,15 +321,37 @@ bool deferred_bf16_narrow(const fo_runtime* rt, const fo_buffer* b, uint64_t n, 
   return false;
 }
 
+// b holds a broadcast of at least n elements, recorded on rt and not yet run.
+bool deferred_bcast(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenRecord* out) {
+  if (!b || !b->widen_pending) return false;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == b && r.deferred) {
+      if (r.rt != rt || !is_bcast(r) || r.n < n) return false;
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
 // How a zip, map or reduce reads an f32 input b of n elements (dst: the op's output, which the read
 // must not alias): the buffer itself (code 4), the bf16 source of its deferred widen (2), or the f32
-// source of that bf16's deferred narrow (kReadViaBf16). `buf` is what the kernel reads and what the
-// caller checks.
+// source of that bf16's deferred narrow (kReadViaBf16); for a zip (bcast_ok) b may also be a
+// deferred broadcast, read through its index map (div, mod) from its source, itself read as above.
+// `buf` is what the kernel reads and what the caller checks.
 struct F32Read {
   const fo_buffer* buf;
   int code;
+  uint32_t div = 1, mod = 0;
 };
-F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_buffer* dst) {
+F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_buffer* dst, bool bcast_ok = false) {
+  WidenRecord br{};
+  if (bcast_ok && deferred_bcast(rt, b, n, &br) && br.src != dst) {
+    F32Read s = f32_read(rt, br.src, br.mod, dst);
+    s.div = br.div;
+    s.mod = br.mod;
+    return s;
+  }
   WidenRecord w{}, nr{};
   if (!deferred_bf16_widen(rt, b, n, &w) || w.src == dst) return {b, 4};
   if (deferred_bf16_narrow(rt, w.src, n, &nr) && nr.src != dst) return {nr.src, kReadViaBf16};
@@ -329,7 +361,7 @@ F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_
 bool find_widen(const fo_buffer* dst, WidenRecord* out) {
   std::lock_guard<std::mutex> lock(g_widen_mu);
   for (auto& r : g_widen)
-    if (r.dst == dst && !is_narrow(r)) {
+    if (r.dst == dst && r.kind == 0 && !is_narrow(r)) {
       *out = r;
       return true;
     }
@@ -1192,15 +1224,18 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
     // An f32 input that stands for a deferred cast (a widen of bf16 data, maybe of a deferred
     // narrow) is read from the data it stands for, and the casts need not run.
     const bool wide_ok = in_t == FO_F32 && dst_t == FO_F32;
-    const F32Read ra = wide_ok ? f32_read(rt, a, n, dst) : F32Read{a, 4};
-    const F32Read rb = wide_ok ? f32_read(rt, b, n, dst) : F32Read{b, 4};
+    const F32Read ra = wide_ok ? f32_read(rt, a, n, dst, true) : F32Read{a, 4};
+    const F32Read rb = wide_ok ? f32_read(rt, b, n, dst, true) : F32Read{b, 4};
     check_buf(ra.buf, "a");
     check_buf(rb.buf, "b");
     if (n == 0) return;
     set_device(rt);
     claim_out(rt, dst, n * dtype_bytes(dst_t));
     TraceScope trace_span(rt, "zip_with");
-    if (ra.code != 4 || rb.code != 4)
+    if (ra.div != 1 || ra.mod != 0 || rb.div != 1 || rb.mod != 0)
+      launch_zip_bcast(rt->stream, dst->ptr, ra.buf->ptr, ra.code, ra.div, ra.mod, rb.buf->ptr, rb.code, rb.div,
+                       rb.mod, n, *op);
+    else if (ra.code != 4 || rb.code != 4)
       launch_zip_widened(rt->stream, dst->ptr, dst_t, ra.buf->ptr, ra.code, rb.buf->ptr, rb.code, n, *op);
     else
       launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
@@ -1281,6 +1316,54 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     const int64_t src_base = plan.src_base, dst_base = plan.dst_base;
     int64_t eb = dtype_bytes(t);
     int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
+    // A broadcast of f32 data over the whole of dst (every digit live, the src digits one contiguous
+    // run from src position 0: dst[i] = src[(i / div) % mod]) is recorded instead of run; a zip
+    // reads it through that index map, anything else runs it first (the engine's to_vrf broadcasts
+    // of a gain, a RoPE row or a per-row scalar, each read by one zip).
+    {
+      bool all_live = true;
+      for (auto& w : j.wheels) all_live &= w.live == w.size;
+      // Innermost first: broadcast digits (stride 0), then one run of consecutive digits whose
+      // strides continue each other from 1, then broadcast digits again.
+      int64_t place = 1, div = 1, mod = 1;
+      int state = 0;  // 0 before the run, 1 in it, 2 after it
+      bool pure = all_live;
+      for (auto& w : j.wheels) {
+        if (w.size > 1) {
+          if (w.stride[0] == 0) {
+            if (state == 1) state = 2;
+          } else if (state == 0 && w.stride[0] == 1) {
+            state = 1;
+            div = place;
+            mod = w.size;
+          } else if (state == 1 && w.stride[0] == mod) {
+            mod *= w.size;
+          } else {
+            pure = false;
+          }
+        }
+        place *= w.size;
+      }
+      const int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
+      if (t == FO_F32 && src != dst && pure && src_base == 0 && dst_base == 0 && count > 0 &&
+          count * eb >= (int64_t)dst->bytes && count < (1ll << 31) && mod <= src_len && div < (1ll << 31) &&
+          mod < (1ll << 31)) {
+        check_filled(src, "src");
+        set_device(rt);
+        claim_out(rt, dst, dst->bytes);
+        note_write(dst);
+        const int mem[1] = {0};
+        std::lock_guard<std::mutex> lock(g_widen_mu);
+        WidenRecord r{dst, src, FO_F32, (uint64_t)count, FO_F32, fo_op{}, rt, true};
+        r.kind = 1;
+        r.div = (uint32_t)div;
+        r.mod = (uint32_t)mod;
+        r.wheels = to_desc<1>(j.wheels, mem);
+        g_widen.push_back(r);
+        dst->widen_pending = true;
+        return;
+      }
+    }
     // An f32 source that is a still-deferred widen of bf16 data may be read from that data.
     WidenRecord wsrc{};
     const bool narrow = t == FO_F32 && src != dst &&

@@ -402,6 +402,26 @@ __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const 
   }
 }
 
+// zip_with (f32 out) whose inputs may be broadcasts recorded by a transpose and never written: an
+// input's element i is element (i / div) % mod of the data it reads (div 1, mod 0: element i), by its
+// read code as above. The decode step's broadcasts are a few thousand elements, so a lane takes one
+// element and the index arithmetic stays off any bandwidth bound.
+struct ZipIn {
+  const void* p;
+  int32_t code;
+  uint32_t div, mod;
+};
+__device__ __forceinline__ uint32_t zip_in(const ZipIn& in, uint64_t i) {
+  if (in.div != 1) i /= in.div;
+  if (in.mod != 0) i %= in.mod;
+  const uint32_t raw = in.code == 2 ? (uint32_t)((const uint16_t*)in.p)[i] : ((const uint32_t*)in.p)[i];
+  return widened_word(raw, in.code);
+}
+__global__ void __launch_bounds__(kBlock) k_zip_b(uint32_t* __restrict__ dst, ZipIn a, ZipIn b, uint64_t n, fo_op op) {
+  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+    dst[i] = combine(op, zip_in(a, i), zip_in(b, i), op.imm1);
+}
+
 // map over such an input (read code SC, 2 or kViaBf16): each word is widened on load as above, then
 // mapped as the f32 word it stands for. Lanes carry 16 bytes of the wider side: at the small sizes
 // these casts come in, a lane's serial chain of slow ops (sigmoid, exp) sets the time.
@@ -794,6 +814,15 @@ void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a,
   FO_ZIPW_CASE(2, kViaBf16);
 #undef FO_ZIPW_CASE
   throw InvalidArg("zip_with: no widened form for these inputs");
+}
+
+void launch_zip_bcast(hipStream_t s, void* dst, const void* a, int a_code, uint32_t a_div, uint32_t a_mod,
+                      const void* b, int b_code, uint32_t b_div, uint32_t b_mod, uint64_t n, const fo_op& op) {
+  for (int c : {a_code, b_code}) require(c == 4 || c == 2 || c == kViaBf16, "zip_with: unknown input read code");
+  require(a_div >= 1 && b_div >= 1, "zip_with: broadcast divisor must be positive");
+  hipLaunchKernelGGL(k_zip_b, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, (uint32_t*)dst,
+                     ZipIn{a, a_code, a_div, a_mod}, ZipIn{b, b_code, b_div, b_mod}, n, op);
+  FO_HIP(hipGetLastError());
 }
 
 void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, int src_code, uint64_t n,

@@ -241,6 +241,10 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
 constexpr int kReadViaBf16 = 5;
 void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const void* b,
                         int b_code, uint64_t n, const fo_op& op);
+// zip_with over f32 inputs (f32 out) given as (data, read code, div, mod): element i of an input is
+// element (i / div) % mod of its data (mod 0: no wrap), a broadcast recorded by a transpose.
+void launch_zip_bcast(hipStream_t s, void* dst, const void* a, int a_code, uint32_t a_div, uint32_t a_mod,
+                      const void* b, int b_code, uint32_t b_div, uint32_t b_mod, uint64_t n, const fo_op& op);
 void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, int src_code, uint64_t n,
                         const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

@@ -1139,6 +1139,49 @@ def test_narrow_read_through_its_widen(rt, consumer, drop):
     assert np.array_equal(got, want)
 
 
+@pytest.mark.parametrize("case", ["inner", "rows", "mask", "copy", "not_pure"])
+@pytest.mark.parametrize("source", ["f32", "widened", "narrowed"])
+def test_zip_reads_recorded_broadcasts(rt, case, source):
+    """A transpose that broadcasts f32 data over the whole of a fresh buffer (a gain over rows, a
+    per-row scalar over its row, a mask over heads, a plain copy) is recorded, and a zip reads it
+    through its index map from the source, itself maybe a pending widen of bf16 data or of a pending
+    narrow: equal to numpy's broadcast and product, bit for bit. A transpose that is not such a
+    broadcast runs as before. Reading the broadcast itself afterwards runs it."""
+    s = dict(N=4, G=3, D=40, T=24, X=1, H=72, A=6, B=10)
+    views = {"inner": ("D", "N, G, D", lambda v: np.broadcast_to(v, (4, 3, 40))),
+             "rows": ("N, G", "N, G, D", lambda v: np.broadcast_to(v.reshape(4, 3, 1), (4, 3, 40))),
+             "mask": ("T", "N, G, T", lambda v: np.broadcast_to(v, (4, 3, 24))),
+             "copy": ("H", "X, H", lambda v: v.reshape(1, 72)),
+             "not_pure": ("A, B", "A, G, B", lambda v: np.broadcast_to(v.reshape(6, 1, 10), (6, 3, 10)))}
+    sv, dv, bcast = views[case]
+    rng = np.random.default_rng(47)
+    m, n = mr.size(mr.parse(sv, s)), mr.size(mr.parse(dv, s))
+    base = rng.standard_normal(m).astype(np.float32) * 4
+    if source == "f32":
+        src, vals = rt.upload(base), base
+    else:
+        vals = emu.bf16_to_f32(emu.f32_to_bf16(base))
+        if source == "widened":
+            t = rt.upload(emu.f32_to_bf16(base))
+        else:
+            t = rt.alloc(2 * m)
+            rt.map(t, BF16, rt.upload(base), F32, m, fh.op("CAST"))
+        src = rt.alloc(4 * m)
+        rt.map(src, F32, t, BF16, m, fh.op("CAST"))
+    y = rng.standard_normal(n).astype(np.float32)
+    print(f"zip of broadcast {case} from {source}", flush=True)
+    b = rt.alloc(4 * n)
+    rt.transpose(b, src, F32, fh.m(sv, **s), fh.m(dv, **s), allow_broadcast=True)
+    out = rt.alloc(4 * n)
+    rt.zip_with(out, F32, b, rt.upload(y), F32, n, fh.op("MUL_F"))
+    want = np.ascontiguousarray(bcast(vals)).ravel()
+    assert np.array_equal(out.read(F32), want * y)
+    out2 = rt.alloc(4 * n)
+    rt.zip_with(out2, F32, rt.upload(y), b, F32, n, fh.op("DIV_F"))
+    assert np.array_equal(out2.read(F32), y / want)
+    assert np.array_equal(b.read(F32), want)
+
+
 def test_widen_of_a_dropped_narrow(rt):
     """The engine's narrow-then-widen idiom (map f32 -> bf16 into a temporary, widen it back, drop the
     temporary): the dropped temporary is kept while its widen is pending, so buffers allocated and
