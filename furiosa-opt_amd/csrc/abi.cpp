@@ -101,6 +101,8 @@ struct WidenRecord {
   int kind = 0;
   uint32_t div = 1, mod = 1;
   Wheels<1> wheels{};
+  // A chain of f32 -> f32 maps (kind 2) instead of a cast: dst = pre.op[pre.n - 1](... pre.op[0](src)).
+  PreOps pre{};
 };
 std::mutex g_widen_mu;
 std::vector<WidenRecord> g_widen;
@@ -108,6 +110,7 @@ std::vector<fo_buffer*> g_retired;  // freed by their owners, kept while a recor
 
 bool is_narrow(const WidenRecord& r) { return r.kind == 0 && r.src_t == FO_F32 && r.dst_t == FO_BF16; }
 bool is_bcast(const WidenRecord& r) { return r.kind == 1; }
+bool is_chain(const WidenRecord& r) { return r.kind == 2; }
 
 // A buffer's block leaves it (the buffer is being freed, rec the recording open at that moment or
 // none), then the buffer goes. A block freed while recording stays with the recording's memory,
@@ -179,9 +182,12 @@ void run_deferred(const std::vector<WidenRecord>& rs) {
   for (auto& r : rs) {
     materialize(r.src);
     FO_HIP(hipSetDevice(r.rt->device));
-    if (is_bcast(r))
+    if (is_bcast(r)) {
       launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, 4, 0, 0, (int64_t)r.n, r.wheels);
-    else
+    } else if (is_chain(r)) {
+      for (int k = 0; k < r.pre.n; ++k)
+        launch_map(r.rt->stream, r.dst->ptr, FO_F32, k == 0 ? r.src->ptr : r.dst->ptr, FO_F32, r.n, r.pre.op[k]);
+    } else
       launch_map(r.rt->stream, r.dst->ptr, r.dst_t, r.src->ptr, r.src_t, r.n, r.op);
     const_cast<fo_buffer*>(r.dst)->widen_pending = false;
   }
@@ -192,7 +198,7 @@ void drop_run_narrows() {
   std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
-    gone = erase_records([](const WidenRecord& r) { return (is_narrow(r) || is_bcast(r)) && !r.deferred; });
+    gone = erase_records([](const WidenRecord& r) { return (is_narrow(r) || r.kind != 0) && !r.deferred; });
   }
   free_retired(gone);
 }
@@ -334,27 +340,48 @@ bool deferred_bcast(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenR
   return false;
 }
 
+// b holds a chain of f32 maps over at least n elements, recorded on rt and not yet run.
+bool deferred_chain(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenRecord* out) {
+  if (!b || !b->widen_pending) return false;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == b && r.deferred) {
+      if (r.rt != rt || !is_chain(r) || r.n < n) return false;
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
 // How a zip, map or reduce reads an f32 input b of n elements (dst: the op's output, which the read
 // must not alias): the buffer itself (code 4), the bf16 source of its deferred widen (2), or the f32
 // source of that bf16's deferred narrow (kReadViaBf16); for a zip (bcast_ok) b may also be a
-// deferred broadcast, read through its index map (div, mod) from its source, itself read as above.
-// `buf` is what the kernel reads and what the caller checks.
+// deferred broadcast, read through its index map (div, mod) from its source, itself read as above;
+// and (zip: chain_ok) the f32 data read, or narrowed, may be a deferred chain of f32 maps, applied
+// on load (pre) to its source. `buf` is what the kernel reads and what the caller checks (which runs
+// whatever is still deferred into it).
 struct F32Read {
   const fo_buffer* buf;
   int code;
   uint32_t div = 1, mod = 0;
+  PreOps pre{};
 };
-F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_buffer* dst, bool bcast_ok = false) {
-  WidenRecord br{};
+F32Read f32_read(const fo_runtime* rt, const fo_buffer* b, uint64_t n, const fo_buffer* dst, bool bcast_ok = false,
+                 bool chain_ok = false) {
+  WidenRecord br{}, ch{};
   if (bcast_ok && deferred_bcast(rt, b, n, &br) && br.src != dst) {
-    F32Read s = f32_read(rt, br.src, br.mod, dst);
+    F32Read s = f32_read(rt, br.src, br.mod, dst, false, chain_ok);
     s.div = br.div;
     s.mod = br.mod;
     return s;
   }
+  if (chain_ok && deferred_chain(rt, b, n, &ch) && ch.src != dst) return {ch.src, 4, 1, 0, ch.pre};
   WidenRecord w{}, nr{};
   if (!deferred_bf16_widen(rt, b, n, &w) || w.src == dst) return {b, 4};
-  if (deferred_bf16_narrow(rt, w.src, n, &nr) && nr.src != dst) return {nr.src, kReadViaBf16};
+  if (deferred_bf16_narrow(rt, w.src, n, &nr) && nr.src != dst) {
+    if (chain_ok && deferred_chain(rt, nr.src, n, &ch) && ch.src != dst) return {ch.src, kReadViaBf16, 1, 0, ch.pre};
+    return {nr.src, kReadViaBf16};
+  }
   return {w.src, 2};
 }
 
@@ -1192,6 +1219,34 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     const bool widen = op->code == FO_OP_CAST && dst != src &&
                        ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
                         (dst_t == FO_I32 && src_t == FO_I8) || (dst_t == FO_BF16 && src_t == FO_F32 && rs.code == 4));
+    // An f32 -> f32 map of f32 data with nothing deferred into it, or of a deferred chain of fewer
+    // than three such maps, is recorded as a chain (extended by this op) that a zip applies on load.
+    WidenRecord ch{};
+    bool chain = false;
+    if (src_t == FO_F32 && dst_t == FO_F32 && dst != src && op->code != FO_OP_CAST && op->code != FO_OP_CAST_RELU &&
+        op->code != FO_OP_TABLE_LOOKUP && op->code != FO_OP_ZERO_POINT_SUB && op->code != FO_OP_FXP_TO_FP &&
+        op->code != FO_OP_FP_TO_FXP) {
+      if (!src->widen_pending) {
+        ch.src = src;
+        chain = true;
+      } else if (deferred_chain(rt, src, n, &ch) && ch.pre.n < 3 && ch.src != dst) {
+        chain = true;
+      }
+    }
+    if (chain) {
+      check_filled(ch.src, "src");
+      if (n == 0) return;
+      set_device(rt);
+      claim_out(rt, dst, span_bytes(dst_t, n));
+      std::lock_guard<std::mutex> lock(g_widen_mu);
+      WidenRecord r{dst, ch.src, FO_F32, n, FO_F32, *op, rt, true};
+      r.kind = 2;
+      r.pre = ch.pre;
+      r.pre.op[r.pre.n++] = *op;
+      g_widen.push_back(r);
+      dst->widen_pending = true;
+      return;
+    }
     if (widen)
       check_filled(src, "src");
     else
@@ -1224,8 +1279,8 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
     // An f32 input that stands for a deferred cast (a widen of bf16 data, maybe of a deferred
     // narrow) is read from the data it stands for, and the casts need not run.
     const bool wide_ok = in_t == FO_F32 && dst_t == FO_F32;
-    const F32Read ra = wide_ok ? f32_read(rt, a, n, dst, true) : F32Read{a, 4};
-    const F32Read rb = wide_ok ? f32_read(rt, b, n, dst, true) : F32Read{b, 4};
+    const F32Read ra = wide_ok ? f32_read(rt, a, n, dst, true, true) : F32Read{a, 4};
+    const F32Read rb = wide_ok ? f32_read(rt, b, n, dst, true, true) : F32Read{b, 4};
     check_buf(ra.buf, "a");
     check_buf(rb.buf, "b");
     if (n == 0) return;
@@ -1233,10 +1288,11 @@ int32_t fo_zip_with(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buf
     claim_out(rt, dst, n * dtype_bytes(dst_t));
     TraceScope trace_span(rt, "zip_with");
     if (ra.div != 1 || ra.mod != 0 || rb.div != 1 || rb.mod != 0)
-      launch_zip_bcast(rt->stream, dst->ptr, ra.buf->ptr, ra.code, ra.div, ra.mod, rb.buf->ptr, rb.code, rb.div,
-                       rb.mod, n, *op);
-    else if (ra.code != 4 || rb.code != 4)
-      launch_zip_widened(rt->stream, dst->ptr, dst_t, ra.buf->ptr, ra.code, rb.buf->ptr, rb.code, n, *op);
+      launch_zip_bcast(rt->stream, dst->ptr, ra.buf->ptr, ra.code, ra.div, ra.mod, ra.pre, rb.buf->ptr, rb.code, rb.div,
+                       rb.mod, rb.pre, n, *op);
+    else if (ra.code != 4 || rb.code != 4 || ra.pre.n != 0 || rb.pre.n != 0)
+      launch_zip_widened(rt->stream, dst->ptr, dst_t, ra.buf->ptr, ra.code, ra.pre, rb.buf->ptr, rb.code, rb.pre, n,
+                         *op);
     else
       launch_zip(rt->stream, dst->ptr, dst_t, a->ptr, b->ptr, in_t, n, *op);
   });

@@ -375,9 +375,26 @@ __device__ __forceinline__ uint32_t widened_word(uint32_t raw, int code) {
   if (code == kViaBf16) return f32_bits(bf16_to_f32(f32_to_bf16(bits_f32(raw))));
   return raw;
 }
-template <int AC, int BC, int OB>
+// A zip input's word: loaded (and widened, code 2), taken through its deferred f32 maps, then (code
+// kViaBf16) rounded through bf16 and widened.
+// Kernels whose inputs have no chain are built without it (PRE false): the op dispatch inlined per
+// element slows every zip down, chain or not.
+template <bool PRE>
+__device__ __forceinline__ uint32_t read_word(uint32_t raw, int code, const PreOps& pre) {
+  uint32_t w = code == 2 ? f32_bits(bf16_to_f32((uint16_t)raw)) : raw;
+  if constexpr (PRE) {
+    for (int k = 0; k < pre.n; ++k) {
+      uint32_t r;
+      map_words<1>(&w, &r, FO_F32, FO_F32, pre.op[k]);
+      w = r;
+    }
+  }
+  return code == kViaBf16 ? f32_bits(bf16_to_f32(f32_to_bf16(bits_f32(w)))) : w;
+}
+template <int AC, int BC, int OB, bool PRE>
 __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const void* __restrict__ a,
-                                                  const void* __restrict__ b, uint64_t n, fo_op op) {
+                                                  const void* __restrict__ b, uint64_t n, fo_op op, PreOps pa,
+                                                  PreOps pb) {
   constexpr int AB = code_bytes(AC), BB = code_bytes(BC);
   constexpr int MINB = AB < BB ? (AB < OB ? AB : OB) : (BB < OB ? BB : OB);
   constexpr int V = 16 / MINB;
@@ -391,13 +408,13 @@ __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const 
       rb.load((const uint8_t*)b + j * V * BB);
 #pragma unroll
       for (int e = 0; e < V; ++e)
-        out.template set<OB>(e, combine(op, widened_word(ra.template get<AB>(e), AC),
-                                        widened_word(rb.template get<BB>(e), BC), op.imm1));
+        out.template set<OB>(e, combine(op, read_word<PRE>(ra.template get<AB>(e), AC, pa),
+                                        read_word<PRE>(rb.template get<BB>(e), BC, pb), op.imm1));
       out.store((uint8_t*)dst + j * V * OB);
     } else {
       for (uint64_t i = j * V; i < n; ++i)
-        store_raw<OB>(dst, i, combine(op, widened_word(load_raw<AB>(a, i), AC), widened_word(load_raw<BB>(b, i), BC),
-                                      op.imm1));
+        store_raw<OB>(dst, i, combine(op, read_word<PRE>(load_raw<AB>(a, i), AC, pa),
+                                      read_word<PRE>(load_raw<BB>(b, i), BC, pb), op.imm1));
     }
   }
 }
@@ -410,16 +427,19 @@ struct ZipIn {
   const void* p;
   int32_t code;
   uint32_t div, mod;
+  PreOps pre;
 };
+template <bool PRE>
 __device__ __forceinline__ uint32_t zip_in(const ZipIn& in, uint64_t i) {
   if (in.div != 1) i /= in.div;
   if (in.mod != 0) i %= in.mod;
   const uint32_t raw = in.code == 2 ? (uint32_t)((const uint16_t*)in.p)[i] : ((const uint32_t*)in.p)[i];
-  return widened_word(raw, in.code);
+  return read_word<PRE>(raw, in.code, in.pre);
 }
+template <bool PRE>
 __global__ void __launch_bounds__(kBlock) k_zip_b(uint32_t* __restrict__ dst, ZipIn a, ZipIn b, uint64_t n, fo_op op) {
   for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
-    dst[i] = combine(op, zip_in(a, i), zip_in(b, i), op.imm1);
+    dst[i] = combine(op, zip_in<PRE>(a, i), zip_in<PRE>(b, i), op.imm1);
 }
 
 // map over such an input (read code SC, 2 or kViaBf16): each word is widened on load as above, then
@@ -792,15 +812,19 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
   throw InvalidArg("zip_with: unsupported element widths");
 }
 
-void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const void* b,
-                        int b_code, uint64_t n, const fo_op& op) {
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const PreOps& a_pre,
+                        const void* b, int b_code, const PreOps& b_pre, uint64_t n, const fo_op& op) {
   require(dst_t == FO_F32, "zip_with: widened inputs take f32 outputs");
+  require(a_pre.n >= 0 && a_pre.n <= 3 && b_pre.n >= 0 && b_pre.n <= 3, "zip_with: at most three deferred maps");
   require(aligned16(dst) && aligned16(a) && aligned16(b), "zip_with: buffers must be 16-byte aligned");
 #define FO_ZIPW_CASE(A, B)                                                                                     \
   if (a_code == A && b_code == B) {                                                                            \
     constexpr int MINB = code_bytes(A) < code_bytes(B) ? code_bytes(A) : code_bytes(B);                        \
-    hipLaunchKernelGGL((k_zip_w<A, B, 4>), dim3(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB)))),      \
-                       dim3(kBlock), 0, s, dst, a, b, n, op);                                                  \
+    const dim3 grid(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB))));                                  \
+    if (a_pre.n != 0 || b_pre.n != 0)                                                                          \
+      hipLaunchKernelGGL((k_zip_w<A, B, 4, true>), grid, dim3(kBlock), 0, s, dst, a, b, n, op, a_pre, b_pre);  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((k_zip_w<A, B, 4, false>), grid, dim3(kBlock), 0, s, dst, a, b, n, op, a_pre, b_pre); \
     FO_HIP(hipGetLastError());                                                                                 \
     return;                                                                                                    \
   }
@@ -812,16 +836,23 @@ void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a,
   FO_ZIPW_CASE(kViaBf16, kViaBf16);
   FO_ZIPW_CASE(kViaBf16, 2);
   FO_ZIPW_CASE(2, kViaBf16);
+  FO_ZIPW_CASE(4, 4);  // inputs read through deferred maps only
 #undef FO_ZIPW_CASE
   throw InvalidArg("zip_with: no widened form for these inputs");
 }
 
 void launch_zip_bcast(hipStream_t s, void* dst, const void* a, int a_code, uint32_t a_div, uint32_t a_mod,
-                      const void* b, int b_code, uint32_t b_div, uint32_t b_mod, uint64_t n, const fo_op& op) {
+                      const PreOps& a_pre, const void* b, int b_code, uint32_t b_div, uint32_t b_mod,
+                      const PreOps& b_pre, uint64_t n, const fo_op& op) {
   for (int c : {a_code, b_code}) require(c == 4 || c == 2 || c == kViaBf16, "zip_with: unknown input read code");
   require(a_div >= 1 && b_div >= 1, "zip_with: broadcast divisor must be positive");
-  hipLaunchKernelGGL(k_zip_b, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, (uint32_t*)dst,
-                     ZipIn{a, a_code, a_div, a_mod}, ZipIn{b, b_code, b_div, b_mod}, n, op);
+  require(a_pre.n >= 0 && a_pre.n <= 3 && b_pre.n >= 0 && b_pre.n <= 3, "zip_with: at most three deferred maps");
+  if (a_pre.n != 0 || b_pre.n != 0)
+    hipLaunchKernelGGL(k_zip_b<true>, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, (uint32_t*)dst,
+                       ZipIn{a, a_code, a_div, a_mod, a_pre}, ZipIn{b, b_code, b_div, b_mod, b_pre}, n, op);
+  else
+    hipLaunchKernelGGL(k_zip_b<false>, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, (uint32_t*)dst,
+                       ZipIn{a, a_code, a_div, a_mod, a_pre}, ZipIn{b, b_code, b_div, b_mod, b_pre}, n, op);
   FO_HIP(hipGetLastError());
 }
 

@@ -239,12 +239,19 @@ void launch_zip(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, const v
 // widen; kReadViaBf16 = the f32 source of a deferred bf16 narrow that a deferred widen reads,
 // rounded through bf16 on load.
 constexpr int kReadViaBf16 = 5;
-void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const void* b,
-                        int b_code, uint64_t n, const fo_op& op);
+// Deferred f32 -> f32 maps a zip input is read through, applied in order after the load (and the
+// widen of bf16 data) and before the bf16 round trip of kReadViaBf16.
+struct PreOps {
+  int32_t n = 0;
+  fo_op op[3] = {};
+};
+void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a, int a_code, const PreOps& a_pre,
+                        const void* b, int b_code, const PreOps& b_pre, uint64_t n, const fo_op& op);
 // zip_with over f32 inputs (f32 out) given as (data, read code, div, mod): element i of an input is
 // element (i / div) % mod of its data (mod 0: no wrap), a broadcast recorded by a transpose.
 void launch_zip_bcast(hipStream_t s, void* dst, const void* a, int a_code, uint32_t a_div, uint32_t a_mod,
-                      const void* b, int b_code, uint32_t b_div, uint32_t b_mod, uint64_t n, const fo_op& op);
+                      const PreOps& a_pre, const void* b, int b_code, uint32_t b_div, uint32_t b_mod,
+                      const PreOps& b_pre, uint64_t n, const fo_op& op);
 void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* src, int src_code, uint64_t n,
                         const fo_op& op);
 void launch_zip3_slots(hipStream_t s, void* dst, const void* data, const void* port, const uint8_t* tag, fo_dtype t,

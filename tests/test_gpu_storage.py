@@ -1182,6 +1182,73 @@ def test_zip_reads_recorded_broadcasts(rt, case, source):
     assert np.array_equal(b.read(F32), want)
 
 
+@pytest.mark.parametrize("case", ["one", "three", "four", "bcast", "narrow", "reduce", "map_of_three",
+                                  "src_rewritten"])
+def test_zip_reads_deferred_map_chains(rt, case):
+    """f32 -> f32 maps (a divide and an add by immediates, sqrt, exp) are recorded as a chain of up to
+    three over their source, and a zip applies the chain on load, after a broadcast's index map and
+    before a narrow's bf16 round trip; a fourth map, a reduce, or a map after three runs the chain
+    first. Every case equals the same calls with each intermediate read back (which runs whatever is
+    deferred into it) before the next call, bit for bit; `src_rewritten` writes the chain's source
+    after recording it, which runs the chain first."""
+    rng = np.random.default_rng(49)
+    r, c = 16, 40
+    n = r * c
+    xv = rng.uniform(0.5, 4.0, n).astype(np.float32)
+    yv = rng.standard_normal(n).astype(np.float32)
+    ops = [("DIV_F", fh.RHS_IMM, 3.0), ("CLIP_ADD", fh.RHS_IMM, 1e-6), ("SQRT", 0, 0.0), ("EXP", 0, 0.0)]
+    print(f"map chain {case}", flush=True)
+
+    def run(force):
+        def chain(src, k, m):
+            cur = src
+            for name, fl, imm in ops[:k]:
+                nxt = rt.alloc(4 * m)
+                rt.map(nxt, F32, cur, F32, m, fh.op(name, fl, imm))
+                if force:
+                    nxt.read(F32)
+                cur = nxt
+            return cur
+
+        def narrowed(a, m):
+            t = rt.alloc(2 * m)
+            rt.map(t, BF16, a, F32, m, fh.op("CAST"))
+            if force:
+                t.read(np.uint16)
+            w = rt.alloc(4 * m)
+            rt.map(w, F32, t, BF16, m, fh.op("CAST"))
+            if force:
+                w.read(F32)
+            return w
+
+        x, y = rt.upload(xv), rt.upload(yv)
+        out = rt.alloc(4 * n)
+        if case in ("one", "three", "four"):
+            a = chain(x, {"one": 1, "three": 3, "four": 4}[case], n)
+        elif case == "bcast":
+            rows = chain(rt.upload(xv[:r]), 3, r)
+            a = rt.alloc(4 * n)
+            rt.transpose(a, rows, F32, fh.m("R", R=r, C=c), fh.m("R, C", R=r, C=c), allow_broadcast=True)
+            if force:
+                a.read(F32)
+        elif case == "narrow":
+            a = narrowed(chain(x, 2, n), n)
+        elif case == "reduce":
+            a = narrowed(chain(x, 2, n), n)
+            red = rt.alloc(4 * r)
+            rt.reduce(red, a, F32, fh.m("R, C", R=r, C=c), fh.m("R", R=r, C=c), fh.RED["ADD"], 0)
+            return red.read(np.uint32)
+        elif case == "map_of_three":
+            a = chain(chain(x, 3, n), 1, n)
+        else:
+            a = chain(x, 2, n)
+            x.write(yv)
+        rt.zip_with(out, F32, a, y, F32, n, fh.op("MUL_F"))
+        return out.read(np.uint32)
+
+    assert np.array_equal(run(False), run(True))
+
+
 def test_widen_of_a_dropped_narrow(rt):
     """The engine's narrow-then-widen idiom (map f32 -> bf16 into a temporary, widen it back, drop the
     temporary): the dropped temporary is kept while its widen is pending, so buffers allocated and
