@@ -320,8 +320,10 @@ template <typename T>
 void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int64_t src_base, int64_t count,
                 const Wheels<1>& w) {
   // Chunked copy when the innermost dst wheel is src-contiguous and everything is 16-byte aligned.
+  // A padded innermost wheel qualifies when its live digits are whole chunks (a window such as
+  // `D = 64 # 128`): the kernel skips a chunk with a dead digit, as the element path skips it.
   constexpr int VEC = 16 / sizeof(T);
-  if (w.n >= 1 && w.stride[0][0] == 1 && w.live[0] == w.size[0] && w.size[0] % VEC == 0 && count % VEC == 0 &&
+  if (w.n >= 1 && w.stride[0][0] == 1 && w.live[0] % VEC == 0 && w.size[0] % VEC == 0 && count % VEC == 0 &&
       dst_base % VEC == 0 && src_base % VEC == 0 && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0) {
     bool ok = true;
     for (int i = 1; i < w.n; ++i) ok &= (w.stride[0][i] % VEC) == 0;
@@ -642,7 +644,7 @@ void launch_relayout(hipStream_t s, void* dst, const void* src, int64_t eb, int6
 bool launch_relayout_widen(hipStream_t s, float* dst, const uint16_t* src, int64_t dst_base, int64_t src_base,
                            int64_t count, const Wheels<1>& w) {
   // The f32 chunked copy's conditions, with the source 8-byte aligned (its chunks are 4 bf16).
-  if (!(w.n >= 1 && w.stride[0][0] == 1 && w.live[0] == w.size[0] && w.size[0] % 4 == 0 && count % 4 == 0 &&
+  if (!(w.n >= 1 && w.stride[0][0] == 1 && w.live[0] % 4 == 0 && w.size[0] % 4 == 0 && count % 4 == 0 &&
         dst_base % 4 == 0 && src_base % 4 == 0 && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 8) == 0))
     return false;
   for (int i = 1; i < w.n; ++i)
