@@ -429,8 +429,10 @@ struct ZipIn {
   uint32_t div, mod;
   PreOps pre;
 };
+// Indices in 32 bits (64-bit division is a long software sequence): a broadcast is recorded only
+// below 2^31 elements, and the launcher takes such zips only below 2^31.
 template <bool PRE>
-__device__ __forceinline__ uint32_t zip_in(const ZipIn& in, uint64_t i) {
+__device__ __forceinline__ uint32_t zip_in(const ZipIn& in, uint32_t i) {
   if (in.div != 1) i /= in.div;
   if (in.mod != 0) i %= in.mod;
   const uint32_t raw = in.code == 2 ? (uint32_t)((const uint16_t*)in.p)[i] : ((const uint32_t*)in.p)[i];
@@ -438,7 +440,7 @@ __device__ __forceinline__ uint32_t zip_in(const ZipIn& in, uint64_t i) {
 }
 template <bool PRE>
 __global__ void __launch_bounds__(kBlock) k_zip_b(uint32_t* __restrict__ dst, ZipIn a, ZipIn b, uint64_t n, fo_op op) {
-  for (uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (uint64_t)gridDim.x * kBlock)
+  for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < (uint32_t)n; i += gridDim.x * kBlock)
     dst[i] = combine(op, zip_in<PRE>(a, i), zip_in<PRE>(b, i), op.imm1);
 }
 
@@ -846,6 +848,7 @@ void launch_zip_bcast(hipStream_t s, void* dst, const void* a, int a_code, uint3
                       const PreOps& b_pre, uint64_t n, const fo_op& op) {
   for (int c : {a_code, b_code}) require(c == 4 || c == 2 || c == kViaBf16, "zip_with: unknown input read code");
   require(a_div >= 1 && b_div >= 1, "zip_with: broadcast divisor must be positive");
+  require(n < (1ull << 31), "zip_with: a broadcast input takes fewer than 2^31 elements");
   require(a_pre.n >= 0 && a_pre.n <= 3 && b_pre.n >= 0 && b_pre.n <= 3, "zip_with: at most three deferred maps");
   if (a_pre.n != 0 || b_pre.n != 0)
     hipLaunchKernelGGL(k_zip_b<true>, dim3(grid_for((int64_t)n)), dim3(kBlock), 0, s, (uint32_t*)dst,
