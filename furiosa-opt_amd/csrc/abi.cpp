@@ -1843,8 +1843,13 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     if (!narrow) {
       check_buf(lhs, "lhs");
       check_buf(rhs, "rhs");
-    } else {  // the narrow sources, made current (a deferred narrow into one runs here)
-      check_buf(wl.src, "lhs");
+    }
+    // A GEMV's x given as a deferred narrow of f32 data is read from that data (rounded as it is
+    // staged); any other kernel below runs the narrow first.
+    WidenRecord xr{};
+    const bool x_narrowed = narrow && deferred_bf16_narrow(rt, wl.src, wl.n, &xr) && xr.src != out;
+    if (narrow) {  // the narrow sources, made current (a deferred narrow into one runs here)
+      check_buf(x_narrowed ? xr.src : wl.src, "lhs");
       check_buf(wr.src, "rhs");
     }
     if (in_t == FO_I4) {
@@ -1898,10 +1903,13 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
       if (unit_k && mw.empty() && bw.empty() && nw.size() == 1 && !padded) {
         const int64_t N = nw[0].w.size, K = rw[0].size, ldw = nw[0].w.stride[1];
         if (K - 1 < lhs_len && (N - 1) * ldw + K - 1 < rhs_len && gemv_supported(ct, co, L, R, N, K, ldw)) {
-          launch_gemv(rt->stream, O, L, R, ct, co, N, K, ldw, nw[0].place);
+          const bool xf = x_narrowed && gemv_takes_f32_x(K);
+          if (x_narrowed && !xf) check_buf(wl.src, "lhs");
+          launch_gemv(rt->stream, O, xf ? xr.src->ptr : L, R, ct, co, N, K, ldw, nw[0].place, xf);
           return;
         }
       }
+      if (x_narrowed) check_buf(wl.src, "lhs");
       if (gemm_supported(ct, co) && unit_k) {
         // The tiled kernel: one affine row, column and batch wheel each, no padding.
         if (!padded && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1) {

@@ -139,8 +139,10 @@ constexpr int kWaitLds = 15 | (7 << 4) | (0 << 8) | (3 << 14);
 constexpr int kModeDenormF32 = 1 | (4 << 6) | (1 << 11);  // s_setreg hwreg(HW_REG_MODE, 4, 2)
 constexpr int kDenormFlushIn = 2;
 
-template <typename Out>
-__global__ void __launch_bounds__(64 + kFoldProducers) k_gemv_fold(Out* __restrict__ out, const uint16_t* __restrict__ x,
+// XF32: x is f32 data standing for the widen of its deferred bf16 narrow (the runtime's deferred
+// casts); each element is rounded to bf16 by the narrow's rule and widened as it is staged.
+template <typename Out, bool XF32>
+__global__ void __launch_bounds__(64 + kFoldProducers) k_gemv_fold(Out* __restrict__ out, const void* __restrict__ x,
                                                    const uint16_t* __restrict__ w, int64_t N, int K, int64_t ldw,
                                                    int64_t ldo) {
   __shared__ __attribute__((aligned(16))) float P[2][kFoldR * kFoldPS];
@@ -180,16 +182,32 @@ __global__ void __launch_bounds__(64 + kFoldProducers) k_gemv_fold(Out* __restri
   if (!folder) {
     __builtin_amdgcn_s_setreg(kModeDenormF32, kDenormFlushIn);
     constexpr int kXPer = kFoldMaxK / 8 / kFoldProducers + 1;  // x chunks per producer (3)
-    uint4 xv[kXPer];
+    uint4 xv[kXPer][XF32 ? 2 : 1];
 #pragma unroll
-    for (int u = 0; u < kXPer; ++u) xv[u] = *(const uint4*)(x + 8 * min(p + u * kFoldProducers, xchunks - 1));
+    for (int u = 0; u < kXPer; ++u) {
+      const int c = min(p + u * kFoldProducers, xchunks - 1);
+      if constexpr (XF32) {
+        xv[u][0] = *((const uint4*)((const float*)x + 8 * c));
+        xv[u][1] = *((const uint4*)((const float*)x + 8 * c) + 1);
+      } else {
+        xv[u][0] = *(const uint4*)((const uint16_t*)x + 8 * c);
+      }
+    }
 #pragma unroll
     for (int j = 0; j < kFoldDepth; ++j) load(j, reg[j]);
 #pragma unroll
     for (int u = 0; u < kXPer; ++u) {  // the reference widen of x
       const int c = p + u * kFoldProducers;
       if (c < xchunks) {
-        const uint16_t* h = (const uint16_t*)&xv[u];
+        uint16_t h[8];
+        if constexpr (XF32) {
+          const uint32_t* f = (const uint32_t*)&xv[u][0];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(bits_f32(f[e]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = ((const uint16_t*)&xv[u][0])[e];
+        }
         float4 a = make_float4(bf16_to_f32(h[0]), bf16_to_f32(h[1]), bf16_to_f32(h[2]), bf16_to_f32(h[3]));
         float4 b = make_float4(bf16_to_f32(h[4]), bf16_to_f32(h[5]), bf16_to_f32(h[6]), bf16_to_f32(h[7]));
         *(float4*)&xs[8 * c] = a;
@@ -279,10 +297,15 @@ __global__ void __launch_bounds__(64 + kFoldProducers) k_gemv_fold(Out* __restri
 }
 
 template <typename Out>
-void gemv_fold(hipStream_t s, Out* out, const uint16_t* x, const uint16_t* w, int64_t N, int64_t K, int64_t ldw,
-               int64_t ldo) {
+void gemv_fold(hipStream_t s, Out* out, const void* x, bool x_f32, const uint16_t* w, int64_t N, int64_t K,
+               int64_t ldw, int64_t ldo) {
   const int64_t blocks = (N + kFoldR - 1) / kFoldR;
-  hipLaunchKernelGGL((k_gemv_fold<Out>), dim3((unsigned)blocks), dim3(64 + kFoldProducers), 0, s, out, x, w, N, (int)K, ldw, ldo);
+  if (x_f32)
+    hipLaunchKernelGGL((k_gemv_fold<Out, true>), dim3((unsigned)blocks), dim3(64 + kFoldProducers), 0, s, out, x, w,
+                       N, (int)K, ldw, ldo);
+  else
+    hipLaunchKernelGGL((k_gemv_fold<Out, false>), dim3((unsigned)blocks), dim3(64 + kFoldProducers), 0, s, out, x, w,
+                       N, (int)K, ldw, ldo);
   FO_HIP(hipGetLastError());
 }
 
@@ -308,15 +331,18 @@ bool gemv_supported(fo_dtype in_t, fo_dtype out_t, const void* x, const void* w,
          (N + 15) / 16 < (1ll << 31);
 }
 
+bool gemv_takes_f32_x(int64_t K) { return K <= kFoldMaxK; }
+
 void launch_gemv(hipStream_t s, void* out, const void* x, const void* w, fo_dtype in_t, fo_dtype out_t, int64_t N,
-                 int64_t K, int64_t ldw, int64_t ldo) {
+                 int64_t K, int64_t ldw, int64_t ldo, bool x_f32) {
   require(gemv_supported(in_t, out_t, x, w, N, K, ldw), "gemv: unsupported operands");
+  require(!x_f32 || gemv_takes_f32_x(K), "gemv: an f32 x through its bf16 narrow takes K <= 4096");
   const uint16_t *xp = (const uint16_t*)x, *wp = (const uint16_t*)w;
   if (K <= kFoldMaxK) {
     if (out_t == FO_F32)
-      gemv_fold<float>(s, (float*)out, xp, wp, N, K, ldw, ldo);
+      gemv_fold<float>(s, (float*)out, x, x_f32, wp, N, K, ldw, ldo);
     else
-      gemv_fold<uint16_t>(s, (uint16_t*)out, xp, wp, N, K, ldw, ldo);
+      gemv_fold<uint16_t>(s, (uint16_t*)out, x, x_f32, wp, N, K, ldw, ldo);
     return;
   }
   // Rows per block: 64 where that still gives 512 blocks, else fewer so a small N spreads out.

@@ -297,8 +297,11 @@ struct GemmDesc {
 // serial fold of each cell in k order (the emulator's contraction_in, bit-exact).
 bool gemv_supported(fo_dtype in_t, fo_dtype out_t, const void* x, const void* w, int64_t N, int64_t K,
                     int64_t ldw);
+// x_f32: x is f32 data standing for the widen of its deferred bf16 narrow, rounded as it is staged
+// (gemv_takes_f32_x(K) says whether the kernel for K has that form).
+bool gemv_takes_f32_x(int64_t K);
 void launch_gemv(hipStream_t s, void* out, const void* x, const void* w, fo_dtype in_t, fo_dtype out_t, int64_t N,
-                 int64_t K, int64_t ldw, int64_t ldo);
+                 int64_t K, int64_t ldw, int64_t ldo, bool x_f32 = false);
 void launch_gemm(hipStream_t s, void* c, const void* a, const void* b, fo_dtype in_t, fo_dtype out_t,
                  const GemmDesc& d);
 bool gemm_supported(fo_dtype in_t, fo_dtype out_t);

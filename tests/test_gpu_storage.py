@@ -1249,6 +1249,36 @@ def test_zip_reads_deferred_map_chains(rt, case):
     assert np.array_equal(run(False), run(True))
 
 
+@pytest.mark.parametrize("k", [1024, 200, 4096, 4104])
+def test_gemv_reads_x_through_its_narrow(rt, k):
+    """A GEMV whose x is a deferred narrow of f32 data, widened for the contraction, reads the f32
+    data and rounds it as it stages x (K up to the fold kernel's 4096; past it the narrow runs
+    first): bit-identical to the same calls with the narrowed x read back first, on ties, f32
+    subnormals and values past the bf16 range."""
+    n = 300
+    rng = np.random.default_rng(51)
+    xv = special_f32(rng, k)
+    wb = emu.f32_to_bf16(rng.standard_normal(n * k).astype(np.float32))
+    maps = [fh.m(t, N=n, K=k) for t in ("K", "N, K", "N, K", "N")]
+    print(f"gemv x through narrow K {k}", flush=True)
+
+    def run(force):
+        x = rt.upload(xv)
+        t = rt.alloc(2 * k)
+        rt.map(t, BF16, x, F32, k, fh.op("CAST"))
+        if force:
+            t.read(np.uint16)
+        xw = rt.alloc(4 * k)
+        rt.map(xw, F32, t, BF16, k, fh.op("CAST"))
+        ww = rt.alloc(4 * n * k)
+        rt.map(ww, F32, rt.upload(wb), BF16, n * k, fh.op("CAST"))
+        out = rt.alloc(4 * n)
+        rt.contraction(out, xw, ww, F32, F32, *maps)
+        return out.read(np.uint32)
+
+    assert np.array_equal(run(False), run(True))
+
+
 def test_widen_of_a_dropped_narrow(rt):
     """The engine's narrow-then-widen idiom (map f32 -> bf16 into a temporary, widen it back, drop the
     temporary): the dropped temporary is kept while its widen is pending, so buffers allocated and
