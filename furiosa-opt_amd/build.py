@@ -70,10 +70,21 @@ def compile_one(src: str) -> Path:
     return obj
 
 
-def build(jobs: int = 8) -> Path:
+def stale(src: str) -> bool:
+    """The object is older than its source or any header (incremental builds only)."""
+    obj = BUILD / (Path(src).stem + ".o")
+    if not obj.exists():
+        return True
+    deps = [CSRC / src, *CSRC.glob("*.hpp"), HERE.parent / "include" / "furiosa_hip.h", Path(__file__)]
+    return any(d.stat().st_mtime > obj.stat().st_mtime for d in deps)
+
+
+def build(jobs: int = 8, incremental: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
+    todo = [s for s in SOURCES if stale(s)] if incremental else SOURCES
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(compile_one, SOURCES))
+        list(ex.map(compile_one, todo))
+    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
     tmp = OUT.with_suffix(".so.tmp")
     # -z defs: an unresolved symbol (e.g. a kernel stub the host pass failed to emit) fails the link
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs), "-o", str(tmp)]
@@ -87,6 +98,9 @@ def build(jobs: int = 8) -> Path:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
+    # recompile only translation units older than their sources (build() in __graft_entry__ always
+    # compiles everything)
+    ap.add_argument("--incremental", action="store_true")
     a = ap.parse_args()
-    print(build(a.jobs))
+    print(build(a.jobs, a.incremental))
     sys.exit(0)

@@ -76,9 +76,11 @@ namespace {
 // contraction over f32 (i32) operands usually reads buffers that are exact casts of bf16 or 8-bit
 // float (i8) data. fo_map records each such cast (dst, src, source type, element count) and defers
 // the cast itself: a contraction whose two operands both have a record of the same source type
-// reads the narrow sources instead -- the MFMA kernels consume them directly, and the generic fold
-// widens them the same way the map would, so its result is unchanged -- and never needs the wide
-// copy. The engine's kernels also round f32 results to bf16 and widen them back before the next
+// reads the narrow sources instead and never needs the wide copy. The GEMV and the generic folds
+// widen them the same way the map would, so their results are those of the wide copies bit for
+// bit; the MFMA kernels (both free extents at least 8 on an MFMA-able layout) consume them directly
+// and sum each cell in another order, so an f32 result from them is held to the contraction
+// tolerance, not to the fold's bits (i32 results stay exact). The engine's kernels also round f32 results to bf16 and widen them back before the next
 // f32 step (a narrow, then a widen); the f32 -> bf16 cast is deferred the same way, and a zip, map
 // or reduce that reads such a widen reads the f32 data and rounds it on load. Any other use of a
 // buffer with a deferred cast into it (check_buf) runs the cast first (and the cast into its source
@@ -249,13 +251,18 @@ bool retire_source(fo_buffer* b) {
   return true;
 }
 
-// Before a recording: retired sources whose casts have run are let go, so that no recorded kernel
-// reads a block the recording does not own.
-void free_run_retired() {
+// A record whose cast has run says dst = cast(src) only while neither buffer has been written
+// since; eager writes drop it (note_write), but a graph launch writes buffers without telling the
+// records. So before a recording starts (a recorded kernel must not read src in place of a dst that
+// later eager writes may make differ from it) and before a graph launches (later eager calls must
+// not take a replayed write of src or dst for the cast), every record that has run is dropped;
+// retired sources that no record reads any more go with them, so that no recorded kernel reads a
+// block the recording does not own.
+void drop_run_records() {
   std::vector<fo_buffer*> gone;
   {
     std::lock_guard<std::mutex> lock(g_widen_mu);
-    gone = erase_records([](const WidenRecord& r) { return r.src->retired && !r.deferred; });
+    gone = erase_records([](const WidenRecord& r) { return !r.deferred; });
   }
   free_retired(gone);
 }
@@ -842,6 +849,8 @@ int32_t fo_runtime_init(int32_t device_index, fo_runtime** out) {
       FO_HIP(hipGetDeviceProperties(&prop, device_index));
       rt->cus = prop.multiProcessorCount;
       rt->arch = prop.gcnArchName;
+      const char* eager = getenv("FO_EAGER");
+      rt->eager = eager && *eager && std::strcmp(eager, "0") != 0;
     } catch (...) {
       fo_runtime_free(rt);
       throw;
@@ -960,6 +969,7 @@ int32_t fo_buffer_alloc(fo_runtime* rt, uint64_t bytes, fo_buffer** out) {
       std::lock_guard<std::mutex> lock(rt->pool->mu);
       rt->pool->unfilled.insert(b.get());
     }
+    if (rt->eager) fill_pending(rt, b.get());
     *out = b.release();
   });
 }
@@ -1057,7 +1067,7 @@ int32_t fo_graph_begin(fo_runtime* rt) {
     // Everything owed to buffers that exist now runs eagerly, outside the graph: a launch must not
     // zero a cache that earlier launches filled, or redo a cast whose source has changed since.
     materialize_runtime(rt);
-    free_run_retired();
+    drop_run_records();
     std::vector<fo_buffer*> unfilled;
     {
       std::lock_guard<std::mutex> lock(rt->pool->mu);
@@ -1132,6 +1142,7 @@ int32_t fo_graph_launch(fo_runtime* rt, fo_graph* graph) {
     require(recording(rt) == nullptr, "a graph cannot be launched while one is being recorded");
     set_device(rt);
     materialize_runtime(rt);  // casts deferred since, which the graph may read
+    drop_run_records();
     TraceScope trace_span(rt, "graph");
     FO_HIP(hipGraphLaunch(graph->exec, rt->stream));
     rt->err_ops |= graph->err_ops;
@@ -1216,14 +1227,14 @@ int32_t fo_map(fo_runtime* rt, fo_buffer* dst, fo_dtype dst_t, const fo_buffer* 
     // bf16, is recorded and deferred until something reads its output other than through it. Its
     // source gets its zero fill now; a deferred cast into the source stays deferred (running this
     // one runs that one first).
-    const bool widen = op->code == FO_OP_CAST && dst != src &&
+    const bool widen = !rt->eager && op->code == FO_OP_CAST && dst != src &&
                        ((dst_t == FO_F32 && (src_t == FO_BF16 || src_t == FO_F8E4M3 || src_t == FO_F8E5M2)) ||
                         (dst_t == FO_I32 && src_t == FO_I8) || (dst_t == FO_BF16 && src_t == FO_F32 && rs.code == 4));
     // An f32 -> f32 map of f32 data with nothing deferred into it, or of a deferred chain of fewer
     // than three such maps, is recorded as a chain (extended by this op) that a zip applies on load.
     WidenRecord ch{};
     bool chain = false;
-    if (src_t == FO_F32 && dst_t == FO_F32 && dst != src && op->code != FO_OP_CAST && op->code != FO_OP_CAST_RELU &&
+    if (!rt->eager && src_t == FO_F32 && dst_t == FO_F32 && dst != src && op->code != FO_OP_CAST && op->code != FO_OP_CAST_RELU &&
         op->code != FO_OP_TABLE_LOOKUP && op->code != FO_OP_ZERO_POINT_SUB && op->code != FO_OP_FXP_TO_FP &&
         op->code != FO_OP_FP_TO_FXP) {
       if (!src->widen_pending) {
@@ -1401,7 +1412,7 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
         place *= w.size;
       }
       const int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
-      if (t == FO_F32 && src != dst && pure && src_base == 0 && dst_base == 0 && count > 0 &&
+      if (!rt->eager && t == FO_F32 && src != dst && pure && src_base == 0 && dst_base == 0 && count > 0 &&
           count * eb >= (int64_t)dst->bytes && count < (1ll << 31) && mod <= src_len && div < (1ll << 31) &&
           mod < (1ll << 31)) {
         check_filled(src, "src");
@@ -1837,7 +1848,7 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
     void* O = out->ptr;
     int64_t lhs_len, rhs_len;
     WidenRecord wl{}, wr{};
-    const bool narrow = (in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) &&
+    const bool narrow = !rt->eager && (in_t == FO_F32 || in_t == FO_I32) && out_t == in_t && find_widen(lhs, &wl) &&
                         find_widen(rhs, &wr) && wl.src_t == wr.src_t && (int64_t)wl.n >= plan.l_size &&
                         (int64_t)wr.n >= plan.r_size;
     if (!narrow) {
@@ -2036,7 +2047,7 @@ int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, c
 
 int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q, const fo_buffer* k,
                              const fo_buffer* v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                             float sqrt_d, int32_t causal) {
+                             float sqrt_d, int32_t causal, const fo_buffer* row_max) {
   return guard([&] {
     check_rt(rt);
     check_buf(out, "out");
@@ -2049,10 +2060,16 @@ int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q,
     uint64_t bytes = (uint64_t)(batch * heads * seq * head_dim * 2);
     require(bytes <= q->bytes && bytes <= k->bytes && bytes <= v->bytes && bytes <= out->bytes,
             "attention: shape exceeds a buffer");
+    if (row_max) {
+      check_buf(row_max, "row_max");
+      require((uint64_t)(batch * heads * seq) * 4 <= row_max->bytes, "attention: row_max smaller than batch*heads*seq");
+      require((uintptr_t)row_max->ptr % 4 == 0, "attention: row_max not aligned");
+    }
     set_device(rt);
     TraceScope trace_span(rt, "attention_prefill");
     launch_attention_prefill(rt->stream, (uint16_t*)out->ptr, (const uint16_t*)q->ptr, (const uint16_t*)k->ptr,
-                             (const uint16_t*)v->ptr, batch, heads, seq, head_dim, sqrt_d, causal);
+                             (const uint16_t*)v->ptr, row_max ? (const float*)row_max->ptr : nullptr, batch, heads,
+                             seq, head_dim, sqrt_d, causal);
   });
 }
 

@@ -10,6 +10,14 @@
 // scales the logits by RN(1/sqrt_d) instead of dividing and evaluates exp as exp2 of a fused
 // multiply-add, both within an f32 ulp of the reference's operation.
 //
+// Given row maxima (row_max, one f32 per query row): the reference subtracts one max per row, taken
+// over every key before masking (attention.rs:77-95), and rounds bf16(p) at that scale. A running
+// max rounds bf16(p) at another scale, and where a row's output is a near-cancelling average of
+// thousands of values those roundings do not cancel. With row_max given, the reference max starts
+// at the given value instead of -inf: for the reference's own max no block exceeds it, so no rescale
+// happens and every p = exp(s - m) is the reference's. (A smaller given value is rescaled past as
+// without it.)
+//
 // Workgroups of kWaves = 8 waves (256 queries, two waves per SIMD) share each K/V tile: one load of
 // it per 256 queries (measured 4% faster than two workgroups of four waves per CU).
 //
@@ -205,8 +213,8 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
 template <int D>
 __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
                                                      const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                                     int32_t heads_total, int32_t seq, int32_t nqb, float inv_sd,
-                                                     int32_t causal) {
+                                                     const float* __restrict__ row_max, int32_t heads_total,
+                                                     int32_t seq, int32_t nqb, float inv_sd, int32_t causal) {
   using C = AttnCfg<D>;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
 
@@ -301,6 +309,7 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[t][r] = 0.f;
   float m_run = -INFINITY, l_part = 0.f;
+  if (row_max && myq < seq) m_run = row_max[head * (int64_t)seq + myq];
 
   // Buffers: K(j) and V(j) live in buffer j % 2. Step j reads them, and after it writes K(j+1)
   // and V(j+1) (loaded during the step) into buffer (j+1) % 2, last read by step j-1 before the
@@ -334,8 +343,9 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
   }
 
   // out[myq][d] = bf16( bf16(o) / (l + EPS) ); lane holds d = 32t + 8*(r/4) + 4g + r%4. The
-  // quotient is correctly rounded (l >= 1, so it is finite and the divisor normal); both narrows
-  // are the hardware's round-to-nearest-even (finite inputs give finite, normal-or-zero o).
+  // quotient is correctly rounded (the divisor is normal: l >= 1 with the running max, l + EPS >=
+  // EPS with a given one; |o| <= l max|v| keeps the quotient finite); both narrows are the
+  // hardware's round-to-nearest-even (finite inputs give finite, normal-or-zero o).
   const LanePair lp = half_pair(l_part);
   const float l_run = lp.lo + lp.hi;
   // Every lane computes (a query past the end sees every key, so its l >= 1 too); lanes l and
@@ -364,21 +374,22 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
 
 template <int D>
 void launch_d(hipStream_t s, dim3 grid, uint16_t* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-              int64_t ht, int64_t seq, int64_t nqb, float inv_sd, int causal) {
+              const float* row_max, int64_t ht, int64_t seq, int64_t nqb, float inv_sd, int causal) {
   constexpr int lds = AttnCfg<D>::LDS;
   static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into
   if (!attr_set) {
     FO_HIP(hipFuncSetAttribute((const void*)k_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_attn_fwd<D>, grid, dim3(kNT), lds, s, out, q, k, v, (int32_t)ht, (int32_t)seq, (int32_t)nqb,
-                     inv_sd, causal);
+  hipLaunchKernelGGL(k_attn_fwd<D>, grid, dim3(kNT), lds, s, out, q, k, v, row_max, (int32_t)ht, (int32_t)seq,
+                     (int32_t)nqb, inv_sd, causal);
 }
 
 }  // namespace
 
 void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                              int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float sqrt_d, int causal) {
+                              const float* row_max, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                              float sqrt_d, int causal) {
   require(((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16 == 0, "attention: buffers not aligned");
   int64_t ht = batch * heads;
   int64_t nqb = (seq + kBM - 1) / kBM;
@@ -386,9 +397,9 @@ void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, c
   dim3 grid((unsigned)(ht * nqb));
   const float inv_sd = 1.0f / sqrt_d;
   if (head_dim == 128)
-    launch_d<128>(s, grid, out, q, k, v, ht, seq, nqb, inv_sd, causal);
+    launch_d<128>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
   else
-    launch_d<64>(s, grid, out, q, k, v, ht, seq, nqb, inv_sd, causal);
+    launch_d<64>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
   FO_HIP(hipGetLastError());
 }
 

@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <map>
 #include <memory>
@@ -85,6 +86,10 @@ struct fo_runtime {
   uint32_t err_ops_saved = 0;  // err_ops of the eager stream while a graph is recorded
   std::vector<struct fo_graph*> graveyard;  // graphs freed while recording, destroyed when it ends
   std::unordered_set<struct fo_graph*> graphs;  // live graphs recorded on this runtime
+  // FO_EAGER=1 in the environment when the runtime is created: nothing is deferred (zero fills run
+  // at allocation, casts, map chains and broadcasts run when issued), the reference check for the
+  // deferred forms.
+  bool eager = false;
 };
 
 // A recorded op stream (fo_graph_begin .. fo_graph_end), launched as one HIP graph.
@@ -107,7 +112,8 @@ struct fo_buffer {
   bool zero_pending = false;
   // An exact widening cast into this buffer recorded but not yet run (the runtime's pending
   // widens): a read runs it first.
-  bool widen_pending = false;
+  // Read without the records' lock (a fast check before taking it), so atomic.
+  std::atomic<bool> widen_pending{false};
   // Freed by its owner while a pending widen still reads it (the source of that widen): the block
   // stays until no widen record names it, then goes the way a free at retirement time would have
   // sent it (retired_in: the recording open then, if any).
@@ -323,7 +329,8 @@ void launch_w8a8(hipStream_t s, uint16_t* out, int32_t* acc_out, const int8_t* a
 void launch_rmsnorm_softmax(hipStream_t s, uint16_t* out, const uint16_t* x, const uint16_t* gain, int64_t rows,
                             int64_t cols, float eps);
 void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                              int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, float sqrt_d, int causal);
+                              const float* row_max, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                              float sqrt_d, int causal);
 void launch_mlp(hipStream_t s, int32_t* pred, uint16_t* logits, const uint16_t* x, const uint16_t* w1,
                 const uint16_t* b1, const uint16_t* w2, const uint16_t* b2, int64_t batch, int64_t in_f,
                 int64_t hidden, int64_t out_f);

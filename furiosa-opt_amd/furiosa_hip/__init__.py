@@ -128,7 +128,7 @@ _sig = {
     "fo_rmsnorm_softmax": (C.c_int32, [_P, _P, _P, _P, C.c_int64, C.c_int64, C.c_float]),
     "fo_attention_prefill": (
         C.c_int32,
-        [_P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int32],
+        [_P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_int32, _P],
     ),
     "fo_gemm_w8a8_dequant": (C.c_int32, [_P, _P, _P, _P, _P, _P, C.c_int64, C.c_int64, C.c_int64]),
     "fo_mlp": (
@@ -324,9 +324,10 @@ class Runtime:
     def rmsnorm_softmax(self, out: "Buffer", x: "Buffer", gain: "Buffer", rows: int, cols: int, eps: float):
         _check(_lib.fo_rmsnorm_softmax(self.h, out.h, x.h, gain.h, rows, cols, eps))
 
-    def attention_prefill(self, out, q, k, v, batch, heads, seq, head_dim, sqrt_d, causal=True):
+    def attention_prefill(self, out, q, k, v, batch, heads, seq, head_dim, sqrt_d, causal=True, row_max=None):
+        """row_max: optional f32 buffer of one max per query row ([B, H, S]) for p = exp(s - m)."""
         _check(_lib.fo_attention_prefill(self.h, out.h, q.h, k.h, v.h, batch, heads, seq, head_dim, sqrt_d,
-                                         int(causal)))
+                                         int(causal), row_max.h if row_max is not None else None))
 
     def gemm_w8a8_dequant(self, out, acc_out, a, w, scale, m_, n_, k_):
         _check(_lib.fo_gemm_w8a8_dequant(self.h, out.h, acc_out.h if acc_out else None, a.h, w.h, scale.h, m_, n_,

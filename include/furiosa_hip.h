@@ -403,10 +403,14 @@ int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, c
 /* Causal attention prefill, Q/K/V/O laid out m![B, H, S, D] bf16 (the QK^T / softmax / PV chain of
  * transformer/kernel/attention.rs:32-392): s = bf16(f32(q.k) / sqrt_d); p = exp(s - m);
  * o = bf16(sum bf16(p) * v); out = bf16(o / (sum p + 6.25e-8)). `sqrt_d` is the divisor
- * (attention.rs:10 uses 11.313708 for D = 128). */
+ * (attention.rs:10 uses 11.313708 for D = 128). `row_max` (optional, may be NULL): f32 per query
+ * row, laid out [B, H, S], the max m each row subtracts -- the reference's own is the max over every
+ * key, taken before masking (attention.rs:77-95), as its forward reads a stored running max
+ * (attention.rs:248-365); NULL takes the kernel's running max over the visible keys, which rounds
+ * bf16(p) at another scale. Inputs are expected finite. */
 int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q, const fo_buffer* k,
                              const fo_buffer* v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
-                             float sqrt_d, int32_t causal);
+                             float sqrt_d, int32_t causal, const fo_buffer* row_max);
 
 /* W8A8 contraction: acc[m,n] = sum_k a[m,k] * w[n,k] (i8 x i8 -> i32, exact), then
  * out[m,n] = bf16(fixedpoint_to_float(acc, 31) * scale[n]) (float/mod.rs:36-62; the VE FxpToFp

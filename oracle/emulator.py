@@ -70,9 +70,9 @@ def _load():
         "ref_zip3_slots": (C.c_int, [P, P, P, P, C.c_int, I64, C.c_int, U32, C.c_int, P, P, P, C.c_int, U32, U32]),
         "ref_branch_tag": (None, [P, P, C.c_int, I64, P, P]),
         "ref_rmsnorm_softmax": (None, [P, P, P, I64, I64, F]),
-        "ref_attention_prefill": (None, [P, P, P, P, I64, I64, I64, F, C.c_int, I64, I64, C.c_int]),
+        "ref_attention_prefill": (C.c_int, [P, P, P, P, I64, I64, I64, F, C.c_int, I64, I64, C.c_int, P]),
         "ref_w8a8": (None, [P, P, P, P, P, I64, I64, I64, I64, I64]),
-        "ref_mlp": (None, [P, P, P, P, P, P, P, I64, I64, I64, I64]),
+        "ref_mlp": (C.c_int, [P, P, P, P, P, P, P, I64, I64, I64, I64]),
         "ref_num_threads": (C.c_int, []),
         "ref_set_threads": (None, [C.c_int]),
     }
@@ -325,15 +325,18 @@ def rmsnorm_softmax(x: np.ndarray, g: np.ndarray, rows: int, cols: int, eps: flo
 
 
 def attention_prefill(q, k, v, bh: int, seq: int, d: int, sqrt_d: float, causal: bool = True, q_begin: int = 0,
-                      q_end: Optional[int] = None, causal_max: bool = False) -> np.ndarray:
+                      q_end: Optional[int] = None, causal_max: bool = False, row_max: Optional[np.ndarray] = None
+                      ) -> np.ndarray:
     """`causal_max=False` is the reference's semantics (row max over every key before masking);
-    `causal_max=True` takes the max over the unmasked keys only."""
-    if seq > 8192:
-        raise ValueError("oracle attention supports seq <= 8192")
+    `causal_max=True` takes the max over the unmasked keys only. `row_max` (f32, bh * seq), if
+    given, receives the max of every computed row."""
     out = np.zeros(bh * seq * d, dtype=np.uint16)
     q, k, v = (np.ascontiguousarray(a, np.uint16) for a in (q, k, v))
-    lib.ref_attention_prefill(_p(q), _p(k), _p(v), _p(out), bh, seq, d, sqrt_d, int(causal), q_begin,
-                              seq if q_end is None else q_end, int(causal_max))
+    if row_max is not None:
+        assert row_max.dtype == np.float32 and row_max.size >= bh * seq and row_max.flags.c_contiguous
+    if lib.ref_attention_prefill(_p(q), _p(k), _p(v), _p(out), bh, seq, d, sqrt_d, int(causal), q_begin,
+                                 seq if q_end is None else q_end, int(causal_max), _p(row_max)) != 0:
+        raise ValueError("oracle attention supports seq <= 8192")
     return out
 
 
@@ -350,7 +353,8 @@ def mlp(x, w1, b1, w2, b2, batch: int, in_f: int, hidden: int, out_f: int):
     pred = np.zeros(batch, dtype=np.int32)
     logits = np.zeros(batch * out_f, dtype=np.uint16)
     arrs = [np.ascontiguousarray(a, np.uint16) for a in (x, w1, b1, w2, b2)]
-    lib.ref_mlp(*[_p(a) for a in arrs], _p(pred), _p(logits), batch, in_f, hidden, out_f)
+    if lib.ref_mlp(*[_p(a) for a in arrs], _p(pred), _p(logits), batch, in_f, hidden, out_f) != 0:
+        raise ValueError("oracle mlp supports hidden <= 4096 and out_f <= 256")
     return pred, logits
 
 

@@ -591,17 +591,19 @@ void ref_rmsnorm_softmax(const uint16_t* x, const uint16_t* g, uint16_t* out, in
 
 /* One attention head over the whole key range as a single chunk. Layout [B, H, S, D].
  * max_mode 0: the reference's row max over every key, taken before masking (attention.rs:77-95);
- * max_mode 1: the max over the keys the causal mask keeps (what a causal online softmax uses). */
-void ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, int64_t bh,
-                           int64_t seq, int64_t d, float sqrt_d, int causal, int64_t q_begin, int64_t q_end,
-                           int max_mode) {
+ * max_mode 1: the max over the keys the causal mask keeps (what a causal online softmax uses).
+ * row_max (optional, [bh, seq] f32): each computed row's max is stored there.
+ * Returns 0, or -1 (nothing computed) when seq exceeds the per-row scratch of 8192 keys. */
+int ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, int64_t bh,
+                          int64_t seq, int64_t d, float sqrt_d, int causal, int64_t q_begin, int64_t q_end,
+                          int max_mode, float* row_max) {
   const float EPS = 6.25e-8f; /* attention.rs:13 */
+  if (seq > 8192) return -1;
 #pragma omp parallel for schedule(dynamic, 1) collapse(2)
   for (int64_t h = 0; h < bh; ++h)
     for (int64_t i = q_begin; i < q_end; ++i) {
       const uint16_t* qi = q + (h * seq + i) * d;
       float s[8192], p[8192];
-      if (seq > 8192) continue;
       float mx = -INFINITY;
       for (int64_t j = 0; j < seq; ++j) {
         const uint16_t* kj = k + (h * seq + j) * d;
@@ -610,6 +612,7 @@ void ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t*
         s[j] = ref_bf16_to_f32(ref_f32_to_bf16(acc / sqrt_d)); /* qk_scaled: fp_div then cast bf16 */
         if (max_mode == 0 || !causal || j <= i) mx = s[j] > mx ? s[j] : mx; /* row_max */
       }
+      if (row_max) row_max[h * seq + i] = mx;
       float l = 0.0f;
       for (int64_t j = 0; j < seq; ++j) {
         float e = expf(s[j] - mx);
@@ -627,6 +630,7 @@ void ref_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t*
         oi[e] = ref_f32_to_bf16(ob / l);                  /* norm: fp_div by the sum */
       }
     }
+  return 0;
 }
 
 void ref_w8a8(const int8_t* a, const int8_t* w, const float* scale, uint16_t* out, int32_t* acc_out, int64_t m,
@@ -649,12 +653,13 @@ static int32_t total_key(float f) {
   return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
 }
 
-void ref_mlp(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const uint16_t* w2, const uint16_t* b2,
-             int32_t* pred, uint16_t* logits, int64_t batch, int64_t in_f, int64_t hidden, int64_t out_f) {
+/* Returns 0, or -1 (nothing computed) when hidden or out_f exceed the per-row scratch. */
+int ref_mlp(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const uint16_t* w2, const uint16_t* b2,
+            int32_t* pred, uint16_t* logits, int64_t batch, int64_t in_f, int64_t hidden, int64_t out_f) {
+  if (hidden > 4096 || out_f > 256) return -1;
 #pragma omp parallel for schedule(static)
   for (int64_t b = 0; b < batch; ++b) {
     float h[4096], y[256];
-    if (hidden > 4096 || out_f > 256) continue;
     for (int64_t j = 0; j < hidden; ++j) {
       float acc = 0.0f;
       for (int64_t kk = 0; kk < in_f; ++kk) acc = acc + ref_bf16_to_f32(x[b * in_f + kk]) * ref_bf16_to_f32(w1[j * in_f + kk]);
@@ -675,6 +680,7 @@ void ref_mlp(const uint16_t* x, const uint16_t* w1, const uint16_t* b1, const ui
       if (total_key(y[o]) >= total_key(y[best])) best = (int)o;
     pred[b] = best;
   }
+  return 0;
 }
 
 int ref_num_threads(void) {

@@ -21,3 +21,22 @@ def rt():
     r = fh.Runtime(int(os.environ.get("FO_HIP_DEVICE", "0")))
     yield r
     r.close()
+
+
+@pytest.fixture(scope="session")
+def rt_eager():
+    """A second runtime created with FO_EAGER=1: it defers nothing (zero fills run at allocation,
+    casts, map chains and broadcasts when issued), the reference the deferred forms are held to."""
+    import furiosa_hip as fh
+
+    old = os.environ.get("FO_EAGER")
+    os.environ["FO_EAGER"] = "1"
+    try:
+        r = fh.Runtime(int(os.environ.get("FO_HIP_DEVICE", "0")))
+    finally:
+        if old is None:
+            del os.environ["FO_EAGER"]
+        else:
+            os.environ["FO_EAGER"] = old
+    yield r
+    r.close()

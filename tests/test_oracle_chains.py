@@ -155,6 +155,59 @@ def test_attention_equal_keys_are_weighted_equally():
         assert np.all(np.abs(got[i] - want) <= 2.0 ** -6 * np.abs(vf[: i + 1]).max()), i
 
 
+def test_attention_causal_max_is_attention_over_the_prefix():
+    # The oracle's causal-max mode (the max over the visible keys only) at query i is, by definition,
+    # the reference's non-causal chain over the first i + 1 keys alone: with no masked key, the max
+    # over every key is the max over the visible ones. Checked against the default (pinned) mode run
+    # on the truncated sequence, bit for bit; and it differs from the default causal mode, whose max
+    # includes the masked keys, on most rows.
+    s, d = 48, 64
+    rng = np.random.default_rng(10)
+    q, k, v = (bf16_of(rng.standard_normal(s * d) * 2.0) for _ in range(3))
+    cm = fl(emu.attention_prefill(q, k, v, 1, s, d, float(np.sqrt(d)), causal=True, causal_max=True)).reshape(s, d)
+    dm = fl(emu.attention_prefill(q, k, v, 1, s, d, float(np.sqrt(d)), causal=True)).reshape(s, d)
+    differ = 0
+    for i in range(s):
+        n = i + 1
+        pre = fl(emu.attention_prefill(q.reshape(s, d)[:n].ravel(), k.reshape(s, d)[:n].ravel(),
+                                       v.reshape(s, d)[:n].ravel(), 1, n, d, float(np.sqrt(d)),
+                                       causal=False)).reshape(n, d)
+        assert np.array_equal(cm[i].view(np.uint32), pre[i].view(np.uint32)), i
+        differ += not np.array_equal(cm[i], dm[i])
+    assert differ > s // 4
+    # query 0 sees key 0 alone: p = e^0 = 1, l = 1 + EPS, o = v_0, so out_0 = v_0 exactly
+    assert np.array_equal(cm[0], fl(v[:d]))
+
+
+def test_attention_row_max_is_the_premask_max():
+    # The oracle reports each computed row's max: over every key before masking by default (the
+    # reference's row_max, attention.rs:77-95), over the visible keys in the causal-max mode; both
+    # equal the max of the logits bf16(f32(q.k) / sqrt_d), whose f32 sums are exact here (small
+    # integer inputs), computed in numpy.
+    bh, s, d = 2, 40, 32
+    rng = np.random.default_rng(11)
+    q, k, v = (bf16_of(rng.integers(-3, 4, bh * s * d).astype(np.float32)) for _ in range(3))
+    sd = float(np.sqrt(d))
+    logits = np.stack([fl(bf16_of((fl(q).reshape(bh, s, d)[h] @ fl(k).reshape(bh, s, d)[h].T) / np.float32(sd)))
+                       for h in range(bh)])
+    for causal_max, want in ((False, logits.max(axis=2)),
+                             (True, np.where(np.tri(s, dtype=bool), logits, -np.inf).max(axis=2))):
+        rm = np.full(bh * s, np.nan, np.float32)
+        emu.attention_prefill(q, k, v, bh, s, d, sd, causal=True, q_begin=3, q_end=30, causal_max=causal_max,
+                              row_max=rm)
+        rm = rm.reshape(bh, s)
+        assert np.array_equal(rm[:, 3:30], want[:, 3:30].astype(np.float32))
+        assert np.isnan(rm[:, :3]).all() and np.isnan(rm[:, 30:]).all()  # rows not computed are untouched
+
+
+def test_attention_oracle_rejects_long_rows():
+    # The oracle's per-row scratch holds 8192 keys; a longer sequence raises instead of leaving rows
+    # unwritten.
+    z = np.zeros(8200 * 8, np.uint16)
+    with pytest.raises(ValueError):
+        emu.attention_prefill(z, z, z, 1, 8200, 8, 2.0, q_begin=0, q_end=1)
+
+
 # ---- W8A8 (i8 contraction, FxpToFp(31), MulF, cast to bf16) -----------------------------------------
 
 
