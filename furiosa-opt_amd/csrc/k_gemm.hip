@@ -25,6 +25,8 @@
 // k -> (lane, element) map, and the sum over k is order-free up to f32 rounding (exact for i32).
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "runtime.hpp"
 
 namespace fo {
@@ -32,6 +34,7 @@ namespace {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
 typedef __attribute__((__vector_size__(16 * sizeof(int)))) int i32x16_t;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2_t;
@@ -155,7 +158,8 @@ __device__ __forceinline__ typename OutT<OUT>::T convert_out(typename MfmaT<KIND
   } else if constexpr (OUT == 3) {
     return a[v];
   } else {
-    return f32_to_bf16(__fmul_rn(fixedpoint_to_float((int32_t)a[v], 31), sc));
+    // fixedpoint_to_float(acc, 31) is the nearest f32 of acc: the i32 -> f32 conversion (RNE)
+    return f32_to_bf16(__fmul_rn((float)(int32_t)a[v], sc));
   }
 }
 
@@ -530,6 +534,403 @@ __global__ void __launch_bounds__(64 * WM * WN) k_gemm(GemmArgs g) {
   }
 }
 
+// ---- four waves of 128x128 (16x16 MFMA tiles) ---------------------------------------------------
+//
+// The same contraction with one wave per SIMD: a 256x256 block tile split into 2x2 wave tiles of
+// 128x128, each an 8x8 grid of 16x16 MFMA tiles (v_mfma_f32_16x16x32_bf16 / v_mfma_i32_16x16x64_i8:
+// per instruction each lane supplies 16 bytes of one row -- row lane % 16, bytes 16 (lane / 16) ..
+// + 15 of a 64-byte k window). The 256 accumulators per lane live in the accumulation registers,
+// the fragments of two k-steps in the vector registers. Per k-step a wave reads 16 fragments for
+// 64 MFMAs, a third less LDS traffic per MFMA than the eight-wave form's 128x64 tiles. 128-byte
+// stages of k are double-buffered in LDS (the same LDS-DMA staging and XOR swizzle as k_gemm);
+// within a k-step, each group of four MFMAs is preceded by one fragment read of the next k-step
+// and, after a stage's readiness barrier, one refill DMA instruction, since no second wave on the
+// SIMD covers their issue. On MI355X at 4096^3 bf16 this measured 1300-1380 TFLOP/s against
+// 1240-1304 for the eight-wave form on the same boxes.
+//
+// The MFMAs are written as inline assembly with the accumulator tied to the output ("+a"): with
+// all 256 accumulation registers holding accumulators, the builtin's untied form made the register
+// allocator rotate accumulators through spare registers (~600 copies per 128 MFMAs). As volatile
+// statements they also keep their source order with the fragment reads and DMA between them, which
+// is the interleave wanted (the scheduler cannot classify them as MFMAs). Since the compiler does not
+// see them as MFMAs, the epilogue pads their latency before it reads the accumulators.
+template <int KIND>
+struct Mfma16;
+template <>
+struct Mfma16<kBf16> {
+  using acc_t = f32x4_t;
+  static __device__ __forceinline__ void mma(acc_t& c, const i32x4_t& a, const i32x4_t& b) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+template <>
+struct Mfma16<kI8> {
+  using acc_t = i32x4_t;
+  static __device__ __forceinline__ void mma(acc_t& c, const i32x4_t& a, const i32x4_t& b) {
+    asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+  }
+};
+
+// f(std::integral_constant<int, B>{}) ... f(std::integral_constant<int, E - 1>{}): loop indices that
+// are compile-time constants however large the body (register arrays stay registers).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+template <int OUT, typename A>
+__device__ __forceinline__ typename OutT<OUT>::T cvt4(const A& a, int v, float sc) {
+  if constexpr (OUT == 0) {
+    return f32_to_bf16(a[v]);
+  } else if constexpr (OUT == 1) {
+    return a[v];
+  } else if constexpr (OUT == 2) {
+    return (int8_t)a[v];
+  } else if constexpr (OUT == 3) {
+    return a[v];
+  } else {
+    static_assert(OUT == 4, "16x16 tiles: bf16, f32, i8, i32 or the W8A8 dequant");
+    // fixedpoint_to_float(acc, 31) is the nearest f32 of acc: the i32 -> f32 conversion (RNE)
+    return f32_to_bf16(__fmul_rn((float)(int32_t)a[v], sc));
+  }
+}
+
+// Elements e and e + 1 of a tile's accumulators as a packed bf16 pair (OUT 0: the f32 sums; OUT 4:
+// the W8A8 dequant), by the reference's narrow.
+template <int OUT, typename A>
+__device__ __forceinline__ uint32_t cvt_pair16(const A& a, int e, float s0, float s1) {
+  static_assert(OUT == 0 || OUT == 4, "bf16 outputs");
+  if constexpr (OUT == 4)
+    return pack_bf16_rule(__fmul_rn((float)(int32_t)a[e], s0), __fmul_rn((float)(int32_t)a[e + 1], s1));
+  else
+    return pack_bf16_rule(a[e], a[e + 1]);
+}
+
+template <int KIND, int OUT, int NSA>
+__global__ void __launch_bounds__(256, 1) k_gemm4(GemmArgs g) {
+  using MM = Mfma16<KIND>;
+  using acc_t = typename MM::acc_t;
+  using out_t = typename OutT<OUT>::T;
+  constexpr int EB = KIND == kBf16 ? 2 : 1;
+  constexpr int BM = 256, BN = 256, W = 4, TT = 8;  // TT x TT MFMA tiles of 16x16 per wave
+  constexpr int BKB = 128;                           // bytes of k per row per stage
+  constexpr int CPR = BKB / 16;                      // 16-byte chunks per row per stage
+  constexpr int RPC = 1024 / BKB;                    // rows per 1 KiB wave DMA
+  constexpr int A_CH = BM / RPC / W, B_CH = BN / RPC / W;  // DMA instructions per wave per stage
+  constexpr int KST = BKB / 64;                      // MFMA k-steps per stage (64 bytes of k each)
+  constexpr int NSB = 2;                             // B buffers; A has NSA
+  constexpr int ABYTES = BM * BKB, BBYTES = BN * BKB;
+  static_assert(NSA >= NSB && NSA * ABYTES + NSB * BBYTES <= 160 * 1024, "LDS");
+  static_assert(A_CH == 8 && B_CH == 8, "one DMA instruction per MFMA group");
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  auto sA = [&](int buf) { return smem + buf * ABYTES; };
+  auto sB = [&](int buf) { return smem + NSA * ABYTES + buf * BBYTES; };
+
+  const int ntiles = g.tiles_m * g.tiles_n;
+  int tile = blockIdx.x;
+  if ((ntiles % 8) == 0) tile = (tile % 8) * (ntiles / 8) + tile / 8;
+  const int group = 8;
+  const int gsize = group * g.tiles_n;
+  const int first_m = (tile / gsize) * group;
+  const int gm = min(g.tiles_m - first_m, group);
+  const int tm = first_m + (tile % gsize) % gm;
+  const int tn = (tile % gsize) / gm;
+  const int batch = blockIdx.y;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const uint32_t KB = (uint32_t)(g.K * EB);
+
+  const int64_t rows_a = min((int64_t)BM, g.M - m0), rows_b = min((int64_t)BN, g.N - n0);
+  const uint8_t* Abase = g.a + (g.a_batch * batch + m0 * g.lda) * EB;
+  const uint8_t* Bbase = g.b + (g.b_batch * batch + n0 * g.ldb) * EB;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Abase), (short)0, uniform_i32((rows_a - 1) * g.lda * EB + KB), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(Bbase), (short)0, uniform_i32((rows_b - 1) * g.ldb * EB + KB), 0x00020000);
+
+  // DMA: lane l of chunk q fills LDS slot l % CPR of row r = RPC q + l / CPR with global chunk
+  // (l % CPR) ^ swz(r), swz(r) = (r >> 1) & (CPR - 1). Chunks q and q + 2 differ by 2 RPC rows,
+  // which leaves swz unchanged, so two per-lane offsets serve every chunk (the rest is a uniform
+  // row stride in the scalar offset).
+  uint32_t a_off[2], a_kc[2], b_off[2], b_kc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int ra_ = RPC * (wave * A_CH + i) + lane / CPR, rb_ = RPC * (wave * B_CH + i) + lane / CPR;
+    a_kc[i] = (uint32_t)(((lane % CPR) ^ ((ra_ >> 1) & (CPR - 1))) * 16);
+    a_off[i] = (uint32_t)(ra_ * g.lda * EB) + a_kc[i];
+    b_kc[i] = (uint32_t)(((lane % CPR) ^ ((rb_ >> 1) & (CPR - 1))) * 16);
+    b_off[i] = (uint32_t)(rb_ * g.ldb * EB) + b_kc[i];
+  }
+  const uint32_t a_pair = (uint32_t)uniform_i32(2 * RPC * g.lda * EB), b_pair = (uint32_t)uniform_i32(2 * RPC * g.ldb * EB);
+  // DMA instruction i of operand A (isa) or B of stage st, into its ring's buffer. FULL: the stage
+  // lies within K (stage offset in the scalar offset, no per-lane check); otherwise chunks past K
+  // read zero.
+  auto issue_one = [&](bool isa, int st, int i, bool FULL) __attribute__((always_inline)) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const uint32_t kb = (uint32_t)st * BKB;
+    const bool tail = !FULL && kb + BKB > KB;
+    lds_ptr_t d = (lds_ptr_t)(isa ? sA(st % NSA) + (wave * A_CH + i) * 1024 : sB(st % NSB) + (wave * B_CH + i) * 1024);
+    const uint32_t rs = (uint32_t)(i >> 1) * (isa ? a_pair : b_pair);
+    const uint32_t vo = isa ? a_off[i & 1] : b_off[i & 1];
+    if (FULL) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb, d, 16, vo, kb + rs, 0, 0);
+    } else {
+      uint32_t off = vo + rs + kb;
+      if (tail && kb + (isa ? a_kc[i & 1] : b_kc[i & 1]) >= KB) off = 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ra : rb, d, 16, off, 0, 0, 0);
+    }
+#endif
+  };
+
+  acc_t acc[TT][TT];
+#pragma unroll
+  for (int i = 0; i < TT; ++i)
+#pragma unroll
+    for (int j = 0; j < TT; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[i][j][v] = 0;
+
+  // Fragment reads: lane (fr, kq) reads chunk (4 kk + kq) of row fr of each 16-row tile, found at
+  // slot chunk ^ swz(fr) (tile rows start at multiples of 16, so swz depends on fr only).
+  const int fr = lane & 15, kq = lane >> 4;
+  const int swz = (fr >> 1) & (CPR - 1);
+  const int a_row = (wm * 128 + fr) * BKB, b_row = (wn * 128 + fr) * BKB;
+  i32x4_t fa[2][TT], fb[2][TT];
+
+  const int nst = (int)((KB + BKB - 1) / BKB);
+  const int nsteps = nst * KST;
+  // DMA order: the prologue issues A0 B0 A1 B1 .. (A up to NSA - 1, B up to NSB - 1); then, after
+  // the readiness barrier of stage u + 1, B(u + NSB) and A(u + NSA), in that order. Stage u is
+  // complete once only DMAs issued after both of its halves are outstanding: for u >= 1 that is
+  // A(u + 1) when A runs a stage further ahead than B (issued right after B(u)); for u = 0 the
+  // rest of the prologue.
+  auto stage_ready = [&](int u, bool STEADY) __attribute__((always_inline)) {
+    int ahead;
+    if (u == 0)
+      ahead = (nst > 1 ? A_CH + B_CH : 0) + (NSA > 2 && nst > 2 ? A_CH : 0);
+    else
+      ahead = (NSA > NSB && (STEADY || u + 1 < nst)) ? A_CH : 0;
+    if (ahead >= 3 * A_CH)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(3 * A_CH));
+    else if (ahead == 2 * A_CH)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(2 * A_CH));
+    else if (ahead == A_CH)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(A_CH));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+  };
+
+  for (int st = 0; st < NSA; ++st) {
+    if (st < nst) {
+#pragma unroll
+      for (int q = 0; q < A_CH; ++q) issue_one(true, st, q, false);
+    }
+    if (st < NSB && st < nst) {
+#pragma unroll
+      for (int q = 0; q < B_CH; ++q) issue_one(false, st, q, false);
+    }
+  }
+  stage_ready(0, false);
+  {
+    const int sl = (kq ^ swz) * 16;
+#pragma unroll
+    for (int i = 0; i < TT; ++i) fa[0][i] = *(const i32x4_t*)(sA(0) + a_row + sl + i * 16 * BKB);
+#pragma unroll
+    for (int j = 0; j < TT; ++j) fb[0][j] = *(const i32x4_t*)(sB(0) + b_row + sl + j * 16 * BKB);
+  }
+
+  // k-step t (fragments in parity P): its 64 MFMAs in 16 groups of four, each group preceded by
+  // one fragment read of step t + 1 and, while refilling, one DMA instruction (B's first: it runs
+  // one stage ahead, A NSA - 1). Crossing into a new stage, the step first passes that stage's
+  // readiness barrier, which also frees the buffers of the stage just read, so their refills are
+  // issued during the step. STEADY: every stage touched is full and both refills exist.
+  auto step = [&](int t, int P, bool STEADY) __attribute__((always_inline)) {
+    const int s = t / KST, kk = t - s * KST;
+    const bool cross = kk + 1 == KST;  // the next k-step is in the next stage
+    const bool next = !cross || STEADY || t + 1 < nsteps;
+    const bool dma_b = cross && next && (STEADY || s + NSB < nst);
+    const bool dma_a = cross && next && (STEADY || s + NSA < nst);
+    if (cross && next) stage_ready(s + 1, STEADY);
+    const int u = cross ? s + 1 : s, nkk = cross ? 0 : kk + 1;
+    const int sl = ((4 * nkk + kq) ^ swz) * 16;
+    const uint8_t* a_s = sA(u % NSA) + a_row + sl;
+    const uint8_t* b_s = sB(u % NSB) + b_row + sl;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      if (next) {
+        if (q < TT)
+          fb[P ^ 1][q] = *(const i32x4_t*)(b_s + q * 16 * BKB);
+        else
+          fa[P ^ 1][q - TT] = *(const i32x4_t*)(a_s + (q - TT) * 16 * BKB);
+      }
+      if (q < B_CH) {
+        if (dma_b) issue_one(false, s + NSB, q, STEADY);
+      } else {
+        if (dma_a) issue_one(true, s + NSA, q - B_CH, STEADY);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = q >> 1, j = 4 * (q & 1) + e;
+        MM::mma(acc[i][j], fb[P][j], fa[P][i]);
+      }
+    }
+  };
+  // Steady k-steps: the refills they issue are of full stages before the last (s + NSA <= nst - 2).
+  int t = 0;
+  const int steady_end = (nst - NSA - 1) * KST;
+  for (; t + 1 < steady_end; t += 2) {
+    step(t, 0, true);
+    step(t + 1, 1, true);
+  }
+  for (; t + 1 < nsteps; t += 2) {
+    step(t, 0, false);
+    step(t + 1, 1, false);
+  }
+  if (t < nsteps) step(t, 0, false);
+  // the last MFMAs' results before any read of the accumulators (their latency is not modelled)
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+  // Epilogue: lane holds row fr of MFMA tile (i, j), columns 16 j + 4 kq + 0..3. Tiles are taken in
+  // pairs (j, j + 1), each accumulator read once. 16-bit outputs of a wave tile inside C are
+  // regrouped between lanes kq and kq ^ 1 (v_permlane16_swap): an even kq stores columns
+  // 16 j + 4 kq + 0..7, an odd kq columns 16 (j + 1) + 4 (kq - 1) + 0..7, one 16-byte store each.
+  const int64_t cb = g.c_batch * batch;
+  out_t* C = (out_t*)g.c;
+  constexpr int OB = (int)sizeof(out_t);
+  const int64_t wr0 = m0 + wm * 128, wc0 = n0 + wn * 128;
+  const bool inside = wr0 + 128 <= g.M && wc0 + 128 <= g.N && g.ldc_n == 1 && g.ldc_m % 8 == 0 && cb % 8 == 0 &&
+                      ((uintptr_t)g.c % 16) == 0 && (OUT != 4 || ((uintptr_t)g.scale % 16) == 0);
+  const bool wide = OB == 2 && inside && (OUT != 4 || !g.acc_out);
+  const bool odd = kq & 1;
+  static_for<0, TT * TT / 2>([&](auto P) {
+    constexpr int i = decltype(P)::value / (TT / 2), j = 2 * (decltype(P)::value % (TT / 2));
+    const int64_t row = wr0 + 16 * i + fr;
+    {
+      // one tile pair at a time: the scheduler would otherwise hoist every accumulator read
+      __builtin_amdgcn_sched_barrier(0);
+      acc_t t2[2] = {acc[i][j], acc[i][j + 1]};
+      if (wide) {
+        uint32_t w[2][2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          float sc[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (OUT == 4) {
+            const f32x4_t s4 = *(const f32x4_t*)(g.scale + wc0 + 16 * (j + d) + 4 * kq);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[e] = s4[e];
+          }
+          if constexpr (OUT == 0 || OUT == 4) {
+            w[d][0] = cvt_pair16<OUT>(t2[d], 0, sc[0], sc[1]);
+            w[d][1] = cvt_pair16<OUT>(t2[d], 2, sc[2], sc[3]);
+          } else {
+            uint16_t o4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o4[e] = (uint16_t)cvt4<OUT>(t2[d], e, sc[e]);
+            const i32x2_t v2 = __builtin_bit_cast(i32x2_t, o4);
+            w[d][0] = (uint32_t)v2[0];
+            w[d][1] = (uint32_t)v2[1];
+          }
+        }
+        // even lanes send tile j + 1, odd lanes tile j; each receives its partner's
+        const uint32_t keep0 = odd ? w[1][0] : w[0][0], keep1 = odd ? w[1][1] : w[0][1];
+        const uint32_t send0 = odd ? w[0][0] : w[1][0], send1 = odd ? w[0][1] : w[1][1];
+        const auto r0 = __builtin_amdgcn_permlane16_swap(send0, send0, false, false);
+        const auto r1 = __builtin_amdgcn_permlane16_swap(send1, send1, false, false);
+        const uint32_t got0 = odd ? (uint32_t)r0[0] : (uint32_t)r0[1];
+        const uint32_t got1 = odd ? (uint32_t)r1[0] : (uint32_t)r1[1];
+        const i32x4_t q4 = odd ? i32x4_t{(int)got0, (int)got1, (int)keep0, (int)keep1}
+                               : i32x4_t{(int)keep0, (int)keep1, (int)got0, (int)got1};
+        const int64_t col = wc0 + 16 * j + (odd ? 16 + 4 * (kq - 1) : 4 * kq);
+        *(i32x4_t*)((uint16_t*)C + cb + row * g.ldc_m + col) = q4;
+        return;
+      }
+      if (row >= g.M) return;
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int64_t col = wc0 + 16 * (j + d) + 4 * kq;
+        float sc[4] = {0.f, 0.f, 0.f, 0.f};
+        const bool vec4 = g.ldc_n == 1 && col + 3 < g.N && ((cb + row * g.ldc_m + col) * OB) % (4 * OB) == 0 &&
+                          ((uintptr_t)g.c % (4 * OB)) == 0;
+        if (vec4) {
+          if constexpr (OUT == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[e] = g.scale[col + e];
+          }
+          out_t o4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o4[e] = cvt4<OUT>(t2[d], e, sc[e]);
+          const int64_t off = cb + row * g.ldc_m + col;
+          if constexpr (OB == 1) {
+            *(uint32_t*)(C + off) = __builtin_bit_cast(uint32_t, o4);
+          } else if constexpr (OB == 2) {
+            *(i32x2_t*)(C + off) = __builtin_bit_cast(i32x2_t, o4);
+          } else {
+            *(i32x4_t*)(C + off) = __builtin_bit_cast(i32x4_t, o4);
+          }
+          if constexpr (OUT == 4) {
+            if (g.acc_out) *(i32x4_t*)(g.acc_out + off) = __builtin_bit_cast(i32x4_t, t2[d]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (col + e >= g.N) continue;
+            if constexpr (OUT == 4) sc[e] = g.scale[col + e];
+            const int64_t off = cb + row * g.ldc_m + (col + e) * g.ldc_n;
+            C[off] = cvt4<OUT>(t2[d], e, sc[e]);
+            if constexpr (OUT == 4) {
+              if (g.acc_out) g.acc_out[off] = (int32_t)t2[d][e];
+            }
+          }
+        }
+      }
+    }
+  });
+}
+
+template <int KIND, int OUT, int NSA>
+void gemm4_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b, const float* scale,
+                      int32_t* acc_out) {
+  GemmArgs g;
+  g.a = (const uint8_t*)a;
+  g.b = (const uint8_t*)b;
+  g.c = c;
+  g.M = d.M;
+  g.N = d.N;
+  g.K = d.K;
+  g.lda = d.lda;
+  g.ldb = d.ldb;
+  g.ldc_m = d.ldc_m;
+  g.ldc_n = d.ldc_n;
+  g.a_batch = d.a_batch;
+  g.b_batch = d.b_batch;
+  g.c_batch = d.c_batch;
+  g.scale = scale;
+  g.acc_out = acc_out;
+  g.tiles_m = (int)((d.M + 255) / 256);
+  g.tiles_n = (int)((d.N + 255) / 256);
+  const size_t lds = (size_t)(NSA + 2) * 256 * 128;
+  static bool attr_set = false;
+  if (!attr_set) {
+    FO_HIP(hipFuncSetAttribute((const void*)k_gemm4<KIND, OUT, NSA>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)lds));
+    attr_set = true;
+  }
+  dim3 grid((unsigned)(g.tiles_m * g.tiles_n), (unsigned)d.batch);
+  hipLaunchKernelGGL((k_gemm4<KIND, OUT, NSA>), grid, dim3(256), lds, s, g);
+  FO_HIP(hipGetLastError());
+}
+
 template <int KIND, int OUT, int BM, int BN, int WM, int WN>
 void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b, const float* scale,
                      int32_t* acc_out) {
@@ -563,10 +964,11 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
   FO_HIP(hipGetLastError());
 }
 
-// Tile choice: 256x256 with 8 waves of 128x64 (one tile per CU at 4096^2, two waves per SIMD)
-// when the problem is large, 128x128 otherwise (measured best on MI355X among 128, 256 with 4, 8
-// and 16 waves). FO_GEMM_TILE overrides it for measurement: 128, 256 (4 waves of 128x128),
-// 2568 (8 waves of 128x64) or 25616 (16 waves).
+// Tile choice: 256x256 when the problem is large -- four waves of 128x128 in 16x16 MFMA tiles
+// (k_gemm4) for bf16 and i8 with plain outputs, eight waves of 128x64 in 32x32 tiles (k_gemm) for
+// the 8-bit floats and the W8A8 dequant -- and 128x128 otherwise. FO_GEMM_TILE overrides it for
+// measurement: 128, 256 (k_gemm, 4 waves of 128x128), 2568 (8 waves of 128x64), 25616 (16 waves)
+// or 4128 (k_gemm4).
 template <int KIND, int OUT>
 void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const void* b,
                  const float* scale = nullptr, int32_t* acc_out = nullptr) {
@@ -579,7 +981,17 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
   // 4096^3 (same boxes, 200-launch runs); the 8-bit floats' 32-byte fragments make 16 waves of
   // 64x64 exceed 128 VGPRs and spill (1850 TFLOP/s against 367); i8 (the W8A8 config) 2175-2186
   // against 2135-2142 TOP/s with the refill split in parts.
-  int choice = forced ? forced : (tiles256 >= 128 ? 2568 : 128);
+  constexpr bool k16 = (KIND == kBf16 || KIND == kI8) && OUT <= 4;  // kinds with a 16x16 MFMA form here
+  // The W8A8 dequant measured 2190 TOP/s on the eight-wave kernel against 2112 on the four-wave one
+  // (same box); bf16 1258-1273 against 1319 TFLOP/s, i8 -> i32 1660 against 1930 TOP/s.
+  constexpr bool k16_default = k16 && OUT != 4;
+  int choice = forced ? forced : (tiles256 >= 128 ? (k16_default ? 4128 : 2568) : 128);
+  if constexpr (k16) {
+    // four waves of 128x128 (16x16 MFMA tiles), 128-byte stages, A and B double-buffered. (A
+    // triple-buffered, running a stage further ahead than B in the 32 KiB of LDS left over, measured
+    // 1030-1034 against 1300-1307 TFLOP/s on one box: correct, and slower.)
+    if (choice == 4128) return gemm4_launch_cfg<KIND, OUT, 2>(s, d, c, a, b, scale, acc_out);
+  }
   if (choice == 2568) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 25616) return gemm_launch_cfg<KIND, OUT, 256, 256, 4, 4>(s, d, c, a, b, scale, acc_out);
   if (choice == 256) return gemm_launch_cfg<KIND, OUT, 256, 256, 2, 2>(s, d, c, a, b, scale, acc_out);

@@ -682,6 +682,48 @@ def test_contraction_mfma(rt, case, types):
         close(emu.bf16_to_f32(got), emu.bf16_to_f32(want))
 
 
+@pytest.mark.parametrize("out_t", [BF16, F32])
+def test_gemm_special_sums(rt, out_t):
+    """The mapped GEMM at a size that takes the four-wave kernel, with rows holding a NaN (every cell
+    of the row NaN: 0x7fc0 after the narrow) and rows and columns of values near 2^-70, whose products
+    are f32 subnormals (the narrow's rule: signed zero), among ordinary cells in the same waves: the
+    bf16 pair conversion falls back to the rule where any lane needs it. Checked against the oracle's
+    fold on the special rows and a sample of ordinary ones."""
+    M, N, K = 4096, 2048, 64
+    s = dict(M=M, N=N, K=K)
+    rng = np.random.default_rng(41)
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((N, K)).astype(np.float32)
+    nan_rows, tiny_rows, tiny_cols = np.arange(0, M, 97), np.arange(1, M, 89), np.arange(3, N, 61)
+    a[nan_rows, 7] = np.nan
+    a[tiny_rows] *= np.float32(2.0 ** -70)
+    b[tiny_cols] *= np.float32(2.0 ** -70)
+    ab, bb = emu.f32_to_bf16(a.ravel()), emu.f32_to_bf16(b.ravel())
+    out = rt.alloc(M * N * (4 if out_t == F32 else 2))
+    maps = [fh.m(t, **s) for t in ("M / 8, M % 8, K", "N, K", "M / 8, M % 8, N, K", "M / 8, M % 8, N")]
+    rt.contraction(out, rt.upload(ab), rt.upload(bb), BF16, out_t, *maps)
+    got = out.read(out_t).reshape(M, N)
+    if out_t == BF16:
+        assert np.all(got[nan_rows] == 0x7FC0)
+        g = emu.bf16_to_f32(got)
+    else:
+        assert np.isnan(got[nan_rows]).all()
+        g = got
+    for r0 in list(tiny_rows[:6]) + [5, 2000, M - 3]:
+        want = emu.gemm_rows(ab, bb, M, N, K, int(r0), int(r0) + 1, out_t).reshape(N)
+        w = emu.bf16_to_f32(want) if out_t == BF16 else want
+        if r0 in tiny_rows:  # cells of tiny rows and tiny columns: subnormal sums
+            sub = g[r0, tiny_cols]
+            if out_t == BF16:
+                assert np.all(sub == 0), r0  # the rule's signed zero
+            else:
+                assert np.all(np.abs(sub) < 2.0 ** -126), r0
+            rest = np.setdiff1d(np.arange(N), tiny_cols)
+            close(g[r0, rest], w[rest])
+        else:
+            close(g[r0], w)
+
+
 # One vector against weight rows (k_gemv: a lane folds each cell in k order). Sizes cover each
 # rows-per-block choice (16, 32, 64), a ragged last block, K with a partial last stage, K = 8, rows
 # wider than K (a padded row stride) and a strided output.
