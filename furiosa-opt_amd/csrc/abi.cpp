@@ -105,6 +105,12 @@ struct WidenRecord {
   Wheels<1> wheels{};
   // A chain of f32 -> f32 maps (kind 2) instead of a cast: dst = pre.op[pre.n - 1](... pre.op[0](src)).
   PreOps pre{};
+  // A relayout (kind 3) instead of a cast: the full-view transposes views[0] -> views[1] -> ... of
+  // elements of type xt, as consecutive Tensor::transpose calls into fresh storages make them, in the
+  // direct form (one transpose views[0] -> views.back(): `wheels`, `count` positions of dst).
+  std::vector<std::string> views;
+  fo_dtype xt = FO_I8;
+  int64_t count = 0;
 };
 std::mutex g_widen_mu;
 std::vector<WidenRecord> g_widen;
@@ -113,6 +119,7 @@ std::vector<fo_buffer*> g_retired;  // freed by their owners, kept while a recor
 bool is_narrow(const WidenRecord& r) { return r.kind == 0 && r.src_t == FO_F32 && r.dst_t == FO_BF16; }
 bool is_bcast(const WidenRecord& r) { return r.kind == 1; }
 bool is_chain(const WidenRecord& r) { return r.kind == 2; }
+bool is_xpose(const WidenRecord& r) { return r.kind == 3; }
 
 // A buffer's block leaves it (the buffer is being freed, rec the recording open at that moment or
 // none), then the buffer goes. A block freed while recording stays with the recording's memory,
@@ -177,6 +184,30 @@ void free_retired(const std::vector<fo_buffer*>& gone) {
 }
 
 void materialize(const fo_buffer* b);
+void fill_pending(fo_runtime* rt, const fo_buffer* b);
+
+// One op's trace span: events recorded on the runtime's stream before and after its launches.
+struct TraceScope {
+  fo_runtime* rt;
+  const char* name;
+  hipEvent_t begin = nullptr;
+  TraceScope(fo_runtime* r, const char* n) : rt(r), name(n) {
+    if (!rt->trace_sink) return;
+    FO_HIP(hipEventCreate(&begin));
+    FO_HIP(hipEventRecord(begin, rt->stream));
+  }
+  ~TraceScope() {
+    if (!begin) return;
+    hipEvent_t end = nullptr;
+    if (hipEventCreate(&end) == hipSuccess && hipEventRecord(end, rt->stream) == hipSuccess) {
+      rt->spans.push_back({name, begin, end});
+    } else {
+      (void)hipEventDestroy(begin);
+      if (end) (void)hipEventDestroy(end);
+    }
+  }
+};
+
 
 // Runs deferred casts, in order, outside the lock; a cast whose source has a deferred cast into it
 // runs that one first.
@@ -186,6 +217,10 @@ void run_deferred(const std::vector<WidenRecord>& rs) {
     FO_HIP(hipSetDevice(r.rt->device));
     if (is_bcast(r)) {
       launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, 4, 0, 0, (int64_t)r.n, r.wheels);
+    } else if (is_xpose(r)) {
+      TraceScope span(r.rt, "transpose");  // the recorded op's own span, when it runs
+      fill_pending(r.rt, r.dst);            // cells the views leave dead read as zero
+      launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, dtype_bytes(r.xt), 0, 0, r.count, r.wheels);
     } else if (is_chain(r)) {
       for (int k = 0; k < r.pre.n; ++k)
         launch_map(r.rt->stream, r.dst->ptr, FO_F32, k == 0 ? r.src->ptr : r.dst->ptr, FO_F32, r.n, r.pre.op[k]);
@@ -222,6 +257,27 @@ void note_write(const fo_buffer* b) {
     std::lock_guard<std::mutex> lock(g_widen_mu);
     gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
   }
+  free_retired(gone);
+}
+
+// b is about to be overwritten whole: the deferred casts that read it run first (each after the
+// casts its own source waits for); a deferred op into it is dropped, since nothing can read its
+// result any more.
+void note_overwrite(const fo_buffer* b) {
+  if (!b) return;
+  std::vector<const fo_buffer*> readers;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    for (auto& r : g_widen)
+      if (r.src == b && r.deferred && r.dst != b) readers.push_back(r.dst);
+  }
+  for (const fo_buffer* d : readers) materialize(d);
+  std::vector<fo_buffer*> gone;
+  {
+    std::lock_guard<std::mutex> lock(g_widen_mu);
+    gone = erase_records([b](const WidenRecord& r) { return r.dst == b || r.src == b; });
+  }
+  const_cast<fo_buffer*>(b)->widen_pending = false;
   free_retired(gone);
 }
 
@@ -354,6 +410,19 @@ bool deferred_chain(const fo_runtime* rt, const fo_buffer* b, uint64_t n, WidenR
   for (auto& r : g_widen)
     if (r.dst == b && r.deferred) {
       if (r.rt != rt || !is_chain(r) || r.n < n) return false;
+      *out = r;
+      return true;
+    }
+  return false;
+}
+
+// b holds a recorded relayout, recorded on rt and not yet run.
+bool deferred_xpose(const fo_runtime* rt, const fo_buffer* b, WidenRecord* out) {
+  if (!b || !b->widen_pending) return false;
+  std::lock_guard<std::mutex> lock(g_widen_mu);
+  for (auto& r : g_widen)
+    if (r.dst == b && r.deferred) {
+      if (r.rt != rt || !is_xpose(r)) return false;
       *out = r;
       return true;
     }
@@ -593,27 +662,6 @@ std::pair<void*, uint64_t> take_block(fo_runtime* rt, uint64_t need) {
 
 void set_device(fo_runtime* rt) { FO_HIP(hipSetDevice(rt->device)); }
 
-// One op's trace span: events recorded on the runtime's stream before and after its launches.
-struct TraceScope {
-  fo_runtime* rt;
-  const char* name;
-  hipEvent_t begin = nullptr;
-  TraceScope(fo_runtime* r, const char* n) : rt(r), name(n) {
-    if (!rt->trace_sink) return;
-    FO_HIP(hipEventCreate(&begin));
-    FO_HIP(hipEventRecord(begin, rt->stream));
-  }
-  ~TraceScope() {
-    if (!begin) return;
-    hipEvent_t end = nullptr;
-    if (hipEventCreate(&end) == hipSuccess && hipEventRecord(end, rt->stream) == hipSuccess) {
-      rt->spans.push_back({name, begin, end});
-    } else {
-      (void)hipEventDestroy(begin);
-      if (end) (void)hipEventDestroy(end);
-    }
-  }
-};
 
 // Hands the recorded spans to the sink (the stream has drained), then releases their events.
 void flush_trace(fo_runtime* rt) {
@@ -1005,6 +1053,13 @@ int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out) {
 
 uint64_t fo_buffer_bytes(const fo_buffer* buf) { return buf ? buf->bytes : 0; }
 
+int32_t fo_buffer_flush(fo_runtime* rt, const fo_buffer* buf) {
+  return guard([&] {
+    check_rt(rt);
+    check_buf(buf, "buf");
+  });
+}
+
 int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst) {
   return guard([&] {
     check_rt(rt);
@@ -1355,6 +1410,58 @@ int32_t fo_branch_tag(fo_runtime* rt, fo_buffer* tag_u8, const fo_buffer* src, f
 
 // ---- mapping-driven ops --------------------------------------------------------------------------
 
+}  // extern "C"
+
+namespace {
+// The live coordinates of `sym` in `f` (digit weights and counts): `bound` is the largest live
+// coordinate plus one (0 when absent); `dense` says whether they fill [0, bound) exactly once.
+struct SymCover {
+  int64_t bound = 0;
+  bool dense = true;
+};
+SymCover sym_cover(const fm::Factors& f, const std::string& sym) {
+  std::vector<const fm::Factor*> ts;
+  for (auto& x : f)
+    if (x.kind == fm::Factor::Term && x.sym == sym && x.count > 0) ts.push_back(&x);
+  SymCover c;
+  if (ts.empty()) return c;
+  std::sort(ts.begin(), ts.end(), [](const fm::Factor* a, const fm::Factor* b) { return a->weight < b->weight; });
+  int64_t expect = 1;
+  for (size_t i = 0; i < ts.size(); ++i) {
+    if (ts[i]->weight != expect || (i + 1 < ts.size() && ts[i]->count != ts[i]->period)) c.dense = false;
+    expect = ts[i]->weight * ts[i]->period;
+    c.bound += (ts[i]->count - 1) * ts[i]->weight;
+  }
+  c.bound += 1;
+  return c;
+}
+
+// The chain of full-view transposes v[0] -> v[1] -> ... moves each element from its source cell to
+// its final cell untouched when every intermediate holds each coordinate the final view reads,
+// exactly once and live: then it is the one transpose v[0] -> v.back(). An axis the source lacks is
+// a broadcast; an intermediate may lack it too (a transpose cannot drop an axis, so it was added by
+// a later step), since no value depends on its coordinate.
+bool chain_direct(const std::vector<fm::Factors>& v) {
+  const int steps = (int)v.size() - 1;
+  bool direct = true;
+  for (auto& x : v.back())
+    if (x.kind == fm::Factor::Term && direct) {
+      const int64_t need = sym_cover(v.back(), x.sym).bound;
+      const bool in_src = sym_cover(v[0], x.sym).bound > 0;
+      for (int k = 1; k < steps && direct; ++k) {
+        const SymCover c = sym_cover(v[k], x.sym);
+        direct = c.bound == 0 ? !in_src : (c.dense && c.bound >= need);
+      }
+    }
+  return direct;
+}
+
+constexpr int kMaxXposeViews = 8;  // views of one recorded relayout chain
+
+}  // namespace
+
+extern "C" {
+
 int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, const char* src_view,
                      const char* dst_view, const char* src_map, const char* dst_map, const char* src_offset,
                      const char* dst_offset, int32_t allow_broadcast) {
@@ -1431,6 +1538,67 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
         return;
       }
     }
+    // A relayout that writes the whole of dst (the dst view is the buffer's size; no window or map),
+    // from a source with nothing deferred into it, or from a recorded relayout read with that
+    // relayout's own last view, is recorded instead of run. Consecutive relayouts -- the engine's
+    // fetch, switch, collect and commit, each into a fresh storage (tensor/mod.rs:302-306) --
+    // compose into one pass while the chain keeps the direct form, and run when anything else reads
+    // them (or their source is written). The intermediates' records stay for any other reader.
+    const bool plain = !(src_offset && *src_offset) && !(dst_offset && *dst_offset) && !(src_map && *src_map) &&
+                       !(dst_map && *dst_map);
+    if (!rt->eager && plain && src != dst && src_base == 0 && dst_base == 0 &&
+        plan.dv_size * eb == (int64_t)dst->bytes) {
+      std::vector<std::string> views;
+      WidenRecord xr{};
+      const bool compose = deferred_xpose(rt, src, &xr) && xr.xt == t && xr.views.back() == src_view &&
+                           xr.src != dst && (int)xr.views.size() < kMaxXposeViews;
+      if (compose) {
+        views = xr.views;
+        views.push_back(dst_view);
+      } else if (!src->widen_pending) {
+        views = {src_view, dst_view};
+      }
+      struct XPlan {
+        bool ok;
+        fm::Joint j;
+        int64_t count;
+      };
+      static Memo<XPlan> xmemo;
+      std::string key;
+      for (auto& v : views) key += v + '\x02';
+      const XPlan xp = views.empty() ? XPlan{false, {}, 0} : xmemo.get(key, [&] {
+        std::vector<fm::Factors> v;
+        for (auto& x : views) v.push_back(flat(x.c_str(), "view"));
+        if (!chain_direct(v)) return XPlan{false, {}, 0};
+        fm::Joint jj = views.size() == 2 ? j : fm::sequence({v[0]}, {v.back()}, fm::Mode::Carve);
+        return XPlan{true, jj, std::min<int64_t>(jj.stream_size, fm::size(v.back()))};
+      });
+      const fo_buffer* s0 = compose ? xr.src : src;
+      if (xp.ok && xp.count > 0 && xp.count < (1ll << 31) &&
+          max_live_offset(xp.j.wheels, 0) < (int64_t)(s0->bytes / eb)) {
+        check_filled(s0, "src");
+        set_device(rt);
+        bool live = true;
+        for (auto& w : xp.j.wheels) live &= w.live == w.size;
+        if (live && xp.count * eb >= (int64_t)dst->bytes) {  // every byte written
+          note_overwrite(dst);
+          claim_out(rt, dst, dst->bytes);
+        } else {
+          note_write(dst);  // the dead cells keep what dst holds
+        }
+        const int mem[1] = {0};
+        std::lock_guard<std::mutex> lock(g_widen_mu);
+        WidenRecord r{dst, s0, t, (uint64_t)xp.count, t, fo_op{}, rt, true};
+        r.kind = 3;
+        r.views = std::move(views);
+        r.xt = t;
+        r.count = xp.count;
+        r.wheels = to_desc<1>(xp.j.wheels, mem);
+        g_widen.push_back(std::move(r));
+        dst->widen_pending = true;
+        return;
+      }
+    }
     // An f32 source that is a still-deferred widen of bf16 data may be read from that data.
     WidenRecord wsrc{};
     const bool narrow = t == FO_F32 && src != dst &&
@@ -1464,29 +1632,6 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     if (narrow) check_buf(src, "src");  // no widening form for this layout: the cast runs first
     launch_relayout(rt->stream, dst->ptr, src->ptr, eb, dst_base, src_base, count, w);
   });
-}
-
-// The live coordinates of `sym` in `f` (digit weights and counts): `bound` is the largest live
-// coordinate plus one (0 when absent); `dense` says whether they fill [0, bound) exactly once.
-struct SymCover {
-  int64_t bound = 0;
-  bool dense = true;
-};
-SymCover sym_cover(const fm::Factors& f, const std::string& sym) {
-  std::vector<const fm::Factor*> ts;
-  for (auto& x : f)
-    if (x.kind == fm::Factor::Term && x.sym == sym && x.count > 0) ts.push_back(&x);
-  SymCover c;
-  if (ts.empty()) return c;
-  std::sort(ts.begin(), ts.end(), [](const fm::Factor* a, const fm::Factor* b) { return a->weight < b->weight; });
-  int64_t expect = 1;
-  for (size_t i = 0; i < ts.size(); ++i) {
-    if (ts[i]->weight != expect || (i + 1 < ts.size() && ts[i]->count != ts[i]->period)) c.dense = false;
-    expect = ts[i]->weight * ts[i]->period;
-    c.bound += (ts[i]->count - 1) * ts[i]->weight;
-  }
-  c.bound += 1;
-  return c;
 }
 
 int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dtype t, int32_t n_views,
@@ -1525,22 +1670,9 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
     set_device(rt);
     TraceScope trace_span(rt, "transpose_chain");
 
-    // Direct form: when every intermediate holds each coordinate the final view reads, exactly once
-    // and live, the chain moves each element from its source cell to its final cell untouched, so it
-    // is the one transpose first view -> last view (with that kernel's tiled and 16-byte paths). An
-    // axis the source lacks is a broadcast; an intermediate may lack it too (a transpose cannot drop
-    // an axis, so it was added by a later step), since no value depends on its coordinate.
-    bool direct = true;
-    for (auto& x : v.back())
-      if (x.kind == fm::Factor::Term && direct) {
-        const int64_t need = sym_cover(v.back(), x.sym).bound;
-        const bool in_src = sym_cover(v[0], x.sym).bound > 0;
-        for (int k = 1; k < steps && direct; ++k) {
-          const SymCover c = sym_cover(v[k], x.sym);
-          direct = c.bound == 0 ? !in_src : (c.dense && c.bound >= need);
-        }
-      }
-    if (direct) {
+    // Direct form (chain_direct): the one transpose first view -> last view, with that kernel's
+    // tiled and 16-byte paths.
+    if (chain_direct(v)) {
       if (!any_broadcast) require(fm::is_padding(fm::carve(v.back(), v[0])), "transpose_chain: broadcast mismatch");
       fm::Joint j = fm::sequence({v[0]}, {v.back()}, fm::Mode::Carve);
       const int64_t count = std::min<int64_t>({j.stream_size, fm::size(v.back()), (int64_t)(dst->bytes / eb)});

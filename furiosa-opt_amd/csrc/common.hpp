@@ -38,12 +38,12 @@ FO_HD uint16_t f32_to_bf16(float f) {
   return (uint16_t)r;
 }
 
-#if defined(__HIP_DEVICE_COMPILE__)
 // Two f32 -> bf16 packed (a low, b high) by f32_to_bf16's rule: the hardware's round-to-nearest-even
 // pair conversion (v_cvt_pk_bf16_f32), which agrees with the rule on every normal, zero and
 // infinite input; when some lane of the wave holds a NaN or a subnormal (class mask 0x93: both NaNs
 // and both denormal classes), those lanes take the rule element by element.
 __device__ __forceinline__ uint32_t pack_bf16_rule(float a, float b) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the host pass parses device code without the device builtins
   typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f2_t;
   typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 h2_t;
   uint32_t w = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, h2_t));
@@ -52,8 +52,10 @@ __device__ __forceinline__ uint32_t pack_bf16_rule(float a, float b) {
     if (sp) w = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
   }
   return w;
-}
+#else
+  return (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
 #endif
+}
 
 // bf16 + bf16 as `half`'s arithmetic does it: widen exactly, add in f32, round to nearest even
 // (no flush: half's from_f32 keeps subnormals).

@@ -84,6 +84,7 @@ _sig = {
     "fo_buffer_free": (None, [_P]),
     "fo_buffer_clone": (C.c_int32, [_P, _P, C.POINTER(_P)]),
     "fo_buffer_bytes": (C.c_uint64, [_P]),
+    "fo_buffer_flush": (C.c_int32, [_P, _P]),
     "fo_write": (C.c_int32, [_P, _P, C.c_uint64, _P]),
     "fo_read": (C.c_int32, [_P, _P, _P, C.c_uint64]),
     "fo_event_record": (C.c_int32, [_P, C.c_int32]),
@@ -360,6 +361,10 @@ class Buffer:
     def write(self, arr: np.ndarray):
         arr = np.ascontiguousarray(arr)
         _check(_lib.fo_write(self.rt.h, arr.ctypes.data, arr.nbytes, self.h))
+
+    def flush(self):
+        """Runs whatever the runtime still owes this buffer (zero fill, deferred cast or relayout)."""
+        _check(_lib.fo_buffer_flush(self.rt.h, self.h))
 
     def read(self, dtype, count: Optional[int] = None) -> np.ndarray:
         dt = np.dtype(NP_DTYPE[dtype] if isinstance(dtype, int) else dtype)

@@ -93,6 +93,12 @@ void fo_buffer_free(fo_buffer* buf);
  * caller has checked that both mappings have the same size. */
 int32_t fo_buffer_clone(fo_runtime* rt, const fo_buffer* src, fo_buffer** out);
 uint64_t fo_buffer_bytes(const fo_buffer* buf);
+
+/* Runs now whatever the runtime still owes `buf` -- its zero fill, and a deferred cast, map chain,
+ * broadcast or relayout into it -- as any op reading it would, on the runtime's stream. No
+ * counterpart in the reference (its storages are always materialised): for callers that hand the
+ * buffer's memory to code outside the runtime, or that time the ops issued into it. */
+int32_t fo_buffer_flush(fo_runtime* rt, const fo_buffer* buf);
 /* Host -> device (Backend::to_hbm, backend/mod.rs:236-239; NPU: furiosa_write, device_runtime.h). */
 int32_t fo_write(fo_runtime* rt, const void* host, uint64_t bytes, fo_buffer* dst);
 /* Device -> host, completes before returning (Backend::from_hbm, backend/mod.rs:240-243). */

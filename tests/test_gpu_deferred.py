@@ -24,6 +24,8 @@ BF16, F32 = fh.BF16, fh.F32
 R, C = 16, 256
 N = R * C
 SIZES = dict(R=R, C=C, N=R, K=C)
+# full views of the N-element buffers: consecutive relayouts between them compose (direct form)
+VIEWS = ("R, C", "C, R", "R / 4, C, R % 4", "C / 64, R, C % 64")
 
 
 def bf16_values(rng, n):
@@ -59,6 +61,7 @@ def same_bits(a, b, dtype):
 class Slot:
     def __init__(self, bufs, dtype, length):
         self.bufs, self.dtype, self.length = bufs, dtype, length
+        self.view = VIEWS[0]  # the view a relayout last wrote it with (its next relayout reads it so)
 
     @property
     def nbytes(self):
@@ -80,7 +83,7 @@ class Twin:
         self.pinned = set()
         self.recording = False  # no host writes while recording: src buffers must already exist
         self.log = []
-        self.views = {t: fh.m(t, **SIZES) for t in ("R", "C", "R, C", "K", "N, K", "N")}
+        self.views = {t: fh.m(t, **SIZES) for t in ("R", "C", "R, C", "K", "N, K", "N") + VIEWS}
 
     # -- buffers --
     def new(self, dtype, length, data=True):
@@ -170,6 +173,16 @@ class Twin:
             for i, rt in enumerate(self.rts):
                 rt.contraction(d.bufs[i], x.bufs[i], w.bufs[i], F32, F32, self.views["K"], self.views["N, K"],
                                self.views["N, K"], self.views["N"])
+        elif kind == "relayout":  # full-view transposes: consecutive ones compose into one pass
+            dtype = BF16 if self.rng.random() < 0.5 else F32
+            src = self.src(dtype, N)
+            sv = src.view if self.rng.random() < 0.8 else VIEWS[self.rng.integers(len(VIEWS))]
+            dv = VIEWS[self.rng.integers(len(VIEWS))]
+            d = self.dst(dtype, N, exclude=(src,))
+            for i, rt in enumerate(self.rts):
+                rt.transpose(d.bufs[i], src.bufs[i], dtype, self.views[sv], self.views[dv])
+            d.view = dv
+            kind += f":{sv}->{dv}"
         elif kind == "write":
             s = self.slots[self.rng.integers(len(self.slots))]
             self.write(s)
@@ -197,7 +210,7 @@ class Twin:
         self.recording = True
         try:
             for _ in range(int(self.rng.integers(2, 7))):
-                self.op(["widen", "narrow", "unary", "zip", "bcast", "reduce", "gemv"])
+                self.op(["widen", "narrow", "unary", "zip", "bcast", "reduce", "gemv", "relayout"])
         finally:
             self.recording = False
             graphs = [rt.graph_end() for rt in self.rts]
@@ -207,7 +220,7 @@ class Twin:
             g.launch()
         self.check_all("first launch")
         for _ in range(int(self.rng.integers(0, 4))):
-            self.op(["widen", "narrow", "unary", "zip", "bcast", "reduce", "gemv", "read"])
+            self.op(["widen", "narrow", "unary", "zip", "bcast", "reduce", "gemv", "relayout", "read"])
         inputs = [s for s in before if s in self.slots]
         if inputs:
             self.write(inputs[self.rng.integers(len(inputs))])
@@ -223,14 +236,14 @@ class Twin:
 @pytest.mark.parametrize("seed", range(6))
 def test_deferred_matches_eager(rt, rt_eager, seed):
     """200 seeded seam calls (widens, narrows, f32 maps, zips, broadcasts, row and column reduces,
-    GEMVs, host writes, frees, reads and recorded graphs) on the deferring runtime and on the eager
+    GEMVs, full-view relayouts, host writes, frees, reads and recorded graphs) on the deferring runtime and on the eager
     one: every buffer equal, bit for bit, at every read and at the end."""
     print(f"deferred vs eager, seed {seed}", flush=True)
     tw = Twin((rt, rt_eager), 1000 + seed)
     for dtype, length in ((BF16, N), (F32, N), (BF16, C), (F32, C), (F32, R), (BF16, R)):
         tw.new(dtype, length)
     ops = ["widen"] * 4 + ["narrow"] * 3 + ["unary"] * 4 + ["zip"] * 4 + ["bcast"] * 2 + ["reduce"] * 2 + \
-          ["gemv"] * 2 + ["write", "free", "free", "read"]
+          ["gemv"] * 2 + ["relayout"] * 4 + ["write", "free", "free", "read"]
     for step in range(200):
         if tw.rng.random() < 0.04:
             tw.graph()

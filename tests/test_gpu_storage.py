@@ -122,6 +122,65 @@ def test_transpose_chain(rt, case, dt):
     assert np.array_equal(d.read(dt[1]), want)
 
 
+@pytest.mark.parametrize("case", range(len(CHAINS)), ids=[" -> ".join(c[0]) for c in CHAINS])
+@pytest.mark.parametrize("keep", ["free", "keep", "read_first"])
+@pytest.mark.parametrize("dt", [(BF16, np.uint16), (I32, np.int32)], ids=["bf16", "i32"])
+def test_stepwise_transposes_compose(rt, case, keep, dt):
+    """The chain as an engine issues it: one fo_transpose per step, each into a fresh buffer. The
+    runtime records a transpose that writes its whole destination and composes the next one that
+    reads it into one pass while the chain keeps the direct form. Every intermediate that is kept,
+    and the last view, must equal the oracle's step-by-step chain (fresh zeroed intermediates), bit
+    for bit -- whether the intermediates are dropped as soon as read (free), kept and read at the end
+    (keep), or read back before the next step runs (read_first, which runs each record)."""
+    views, bc = CHAINS[case]
+    bc = bc or [False] * (len(views) - 1)
+    rng = np.random.default_rng(60 + case)
+    parsed = [mr.parse(v, CHAIN_AXES) for v in views]
+    src = rand_words(rng, mr.size(parsed[0]), dt[1])
+    want = [src]
+    for k in range(1, len(views)):
+        want.append(emu.transpose(np.zeros(mr.size(parsed[k]), dt[1]), want[-1], parsed[k - 1], parsed[k]))
+    eb = np.dtype(dt[1]).itemsize
+    bufs = [rt.upload(src)]
+    for k in range(1, len(views)):
+        bufs.append(rt.alloc(mr.size(parsed[k]) * eb))
+        rt.transpose(bufs[k], bufs[k - 1], dt[0], fh.m(views[k - 1], **CHAIN_AXES), fh.m(views[k], **CHAIN_AXES),
+                     allow_broadcast=bc[k - 1])
+        if keep == "read_first":
+            assert np.array_equal(bufs[k].read(dt[1]), want[k]), k
+        if keep == "free" and k >= 2:
+            bufs[k - 1].free()
+    assert np.array_equal(bufs[-1].read(dt[1]), want[-1])
+    if keep == "keep":
+        for k in range(1, len(views) - 1):
+            assert np.array_equal(bufs[k].read(dt[1]), want[k]), k
+
+
+def test_recorded_transpose_runs_before_its_source_changes(rt):
+    """A recorded transpose (and one composed onto it) reads its source as it was when issued: a host
+    write to the source, a map into it and a transpose into it each run the records first."""
+    s = dict(R=64, C=96)
+    rng = np.random.default_rng(61)
+    a0, a1 = rand_words(rng, 64 * 96, np.int32), rand_words(rng, 64 * 96, np.int32)
+    pr, pc, pp = (mr.parse(v, s) for v in ("R, C", "C, R", "R / 8, C, R % 8"))
+    t1 = emu.transpose(np.zeros(64 * 96, np.int32), a0, pr, pc)
+    t2 = emu.transpose(np.zeros(64 * 96, np.int32), t1, pc, pp)
+    for how in ("write", "map", "transpose"):
+        src = rt.upload(a0)
+        b1, b2 = rt.alloc(64 * 96 * 4), rt.alloc(64 * 96 * 4)
+        rt.transpose(b1, src, I32, fh.m("R, C", **s), fh.m("C, R", **s))
+        rt.transpose(b2, b1, I32, fh.m("C, R", **s), fh.m("R / 8, C, R % 8", **s))
+        if how == "write":
+            src.write(a1)
+        elif how == "map":
+            rt.map(src, I32, rt.upload(a1), I32, 64 * 96, fh.op("CAST"))
+        else:
+            rt.transpose(src, rt.upload(a1), I32, fh.m("R, C", **s), fh.m("R, C", **s))
+        assert np.array_equal(b2.read(np.int32), t2), how
+        assert np.array_equal(b1.read(np.int32), t1), how
+        assert np.array_equal(src.read(np.int32), a1), how
+
+
 def test_transpose_chain_requires_broadcast_flag(rt):
     views = [fh.m(v, **CHAIN_AXES) for v in ("A, B", "B, A", "B, X, A")]
     with pytest.raises(fh.FoError, match="allow its broadcast"):
