@@ -2053,6 +2053,20 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
         }
       }
       if (x_narrowed) check_buf(wl.src, "lhs");
+      // Batched dot products (every out wheel reads both operands, or neither: padding): one lane
+      // folds each cell's two rows in k order.
+      const bool rows_repeat_only =
+          std::all_of(mw.begin(), mw.end(), [](const Part& p) { return p.w.stride[0] == 0 && p.w.stride[1] == 0; });
+      if (unit_k && rows_repeat_only && nw.empty() && !bw.empty()) {
+        const int64_t K = rw[0].size;
+        if (max_live_offset(ow, 0) + K - 1 < lhs_len && max_live_offset(ow, 1) + K - 1 < rhs_len) {
+          const int64_t eb = dtype_bytes(ct);
+          bool vec = ((uintptr_t)L % 16) == 0 && ((uintptr_t)R % 16) == 0;
+          for (auto& p : bw) vec &= (p.w.stride[0] * eb) % 16 == 0 && (p.w.stride[1] * eb) % 16 == 0;
+          const int mem[2] = {0, 1};
+          if (launch_contraction_dot(rt->stream, O, L, R, ct, co, out_count, to_desc<2>(ow, mem), K, vec)) return;
+        }
+      }
       if (gemm_supported(ct, co) && unit_k) {
         // The tiled kernel: one affine row, column and batch wheel each, no padding.
         if (!padded && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1) {

@@ -1474,11 +1474,183 @@ __global__ void __launch_bounds__(kBlock) k_contract_generic(Out* __restrict__ o
   }
 }
 
+// Batched dot products: every output wheel reads both operands (or neither: padding) and the
+// residue is one run of K contiguous elements in both, so each output cell folds two rows. One lane
+// per cell folds its K products in k order -- k_contract_generic's arithmetic and order -- reading
+// 16 bytes of each row at a time, four such pairs in flight ahead of the fold (vec: every row start
+// 16-byte aligned). The MNIST fc1 stream (mnist/mod.rs:8-34) issues this shape: 256 cells of one
+// 800-long dot product, the rhs a copy of the input per cell.
+template <typename In, typename Acc, typename Out>
+__global__ void __launch_bounds__(kBlock) k_contract_dot(Out* __restrict__ out, const In* __restrict__ lhs,
+                                                         const In* __restrict__ rhs, uint32_t out_count,
+                                                         Wheels<2> ow, uint32_t K, int32_t vec) {
+  using M = MacT<In, Acc>;
+  constexpr int V = 16 / (int)sizeof(In);  // elements per 16-byte read
+  constexpr int U = 4;                      // 16-byte pairs per batch
+  const uint32_t o = blockIdx.x * kBlock + threadIdx.x;
+  if (o >= out_count) return;
+  int64_t bl = 0, br = 0;
+  uint32_t q = o;
+  bool dead = false;
+  for (int i = 0; i < ow.n; ++i) {
+    const uint32_t nq = ow.div[i].div(q);
+    const uint32_t d = q - nq * ow.size[i];
+    dead |= d >= ow.live[i];
+    bl += (int64_t)d * ow.stride[0][i];
+    br += (int64_t)d * ow.stride[1][i];
+    q = nq;
+  }
+  Acc acc = Acc(0);
+  if (!dead) {  // a padding cell has no reads and keeps its zero (buf.rs:425-437)
+    const In* a = lhs + bl;
+    const In* b = rhs + br;
+    uint32_t k = 0;
+    if (vec) {
+      typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+      i32x4_t va[U], vb[U];
+      auto load = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          va[u] = *(const i32x4_t*)(a + k0 + u * V);
+          vb[u] = *(const i32x4_t*)(b + k0 + u * V);
+        }
+      };
+      if (K >= (uint32_t)(U * V)) load(0);
+      for (; k + U * V <= K; k += U * V) {
+        i32x4_t ca[U], cb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) ca[u] = va[u], cb[u] = vb[u];
+        if (k + 2 * U * V <= K) load(k + U * V);  // the next batch in flight during this fold
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const In* ea = (const In*)&ca[u];
+          const In* eb = (const In*)&cb[u];
+#pragma unroll
+          for (int e = 0; e < V; ++e) acc = M::mac(acc, M::widen(ea[e]), M::widen(eb[e]));
+        }
+      }
+    }
+    for (; k < K; ++k) acc = M::mac(acc, M::widen(a[k]), M::widen(b[k]));
+  }
+  out[o] = narrow<In, Acc, Out>(acc);
+}
+
 // The product and the sum of contraction_in, as separate roundings (no fused multiply-add).
 __device__ __forceinline__ float mul_of(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_of(float a, float b) { return __fadd_rn(a, b); }
 __device__ __forceinline__ int32_t mul_of(int32_t a, int32_t b) { return (int32_t)((uint32_t)a * (uint32_t)b); }
 __device__ __forceinline__ int32_t add_of(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+
+// The same dot products with the reads spread over a block: 256 threads stage the products of 16
+// cells (one multiply each, MacT's rounding) in LDS, 512 positions of each row at a time and the next
+// 512 loading while the current ones are folded; lane c of wave 0 then adds cell c's products in k
+// order. The multiplies do not depend on the running sum, so only the adds stay serial, and the
+// result is the lane-per-cell kernel's bit for bit. Every row start is 16-byte aligned (vec).
+constexpr int kDotCells = 16;   // cells per block
+constexpr int kDotChunk = 512;  // positions per stage
+template <typename In, typename Acc, typename Out>
+__global__ void __launch_bounds__(kBlock) k_contract_dot_staged(Out* __restrict__ out, const In* __restrict__ lhs,
+                                                                const In* __restrict__ rhs, uint32_t out_count,
+                                                                Wheels<2> ow, uint32_t K) {
+  static_assert(kBlock == kDotCells * 16, "16 threads stage each cell");
+  using M = MacT<In, Acc>;
+  typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4_t;
+  constexpr int V = 16 / (int)sizeof(In);       // elements per 16-byte read
+  constexpr int NJ = kDotChunk / (16 * V);      // 16-byte reads per operand per thread per stage
+  constexpr int ROW = kDotChunk + 4;            // padded row: lane c's reads start on distinct banks
+  __shared__ Acc prod[2][kDotCells][ROW];
+  const int t = threadIdx.x, sub = t & 15, cl = t >> 4;
+  const uint32_t cell = blockIdx.x * kDotCells + cl;
+  int64_t bl = 0, br = 0;
+  bool dead = cell >= out_count;
+  if (!dead) {
+    uint32_t q = cell;
+    for (int i = 0; i < ow.n; ++i) {
+      const uint32_t nq = ow.div[i].div(q);
+      const uint32_t d = q - nq * ow.size[i];
+      dead |= d >= ow.live[i];
+      bl += (int64_t)d * ow.stride[0][i];
+      br += (int64_t)d * ow.stride[1][i];
+      q = nq;
+    }
+  }
+  const In* a = lhs + bl;
+  const In* b = rhs + br;
+  i32x4_t va[NJ], vb[NJ];
+  auto load = [&](uint32_t k0) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t e = k0 + (uint32_t)(j * 16 + sub) * V;
+      if (!dead && e + V <= K) {
+        va[j] = *(const i32x4_t*)(a + e);
+        vb[j] = *(const i32x4_t*)(b + e);
+      } else if (!dead && e < K) {  // the ragged end of a row, element by element
+        In ta[V], tb[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) ta[v] = e + v < K ? a[e + v] : In(0), tb[v] = e + v < K ? b[e + v] : In(0);
+        va[j] = *(const i32x4_t*)ta;
+        vb[j] = *(const i32x4_t*)tb;
+      }
+    }
+  };
+  const uint32_t stages = (K + kDotChunk - 1) / kDotChunk;
+  const bool folds = t < kDotCells && blockIdx.x * kDotCells + t < out_count;
+  bool fold_dead = false;
+  if (folds) {  // lane t folds cell blockIdx.x * 16 + t; its liveness, decoded again
+    uint32_t q = blockIdx.x * kDotCells + t;
+    for (int i = 0; i < ow.n; ++i) {
+      const uint32_t nq = ow.div[i].div(q);
+      fold_dead |= q - nq * ow.size[i] >= ow.live[i];
+      q = nq;
+    }
+  }
+  Acc acc = Acc(0);
+  load(0);
+  for (uint32_t s = 0; s < stages; ++s) {
+    const uint32_t k0 = s * kDotChunk;
+    Acc* row = prod[s & 1][cl];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const uint32_t e = (uint32_t)(j * 16 + sub) * V;
+      if (!dead && k0 + e < K) {
+        const In* ea = (const In*)&va[j];
+        const In* eb = (const In*)&vb[j];
+#pragma unroll
+        for (int v = 0; v < V; v += 4) {
+          Acc p4[4];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) p4[w] = mul_of(M::widen(ea[v + w]), M::widen(eb[v + w]));
+          *(i32x4_t*)(row + e + v) = *(const i32x4_t*)p4;
+        }
+      }
+    }
+    __syncthreads();
+    if (s + 1 < stages) load(k0 + kDotChunk);  // in flight while this stage is folded
+    if (folds && !fold_dead) {
+      const Acc* pr = prod[s & 1][t];
+      const uint32_t klen = min((uint32_t)kDotChunk, K - k0);
+      uint32_t k = 0;
+      for (; k + 32 <= klen; k += 32) {  // eight reads in flight ahead of the adds
+        i32x4_t p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = *(const i32x4_t*)(pr + k + 4 * u);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const Acc* pe = (const Acc*)&p[u];
+          acc = add_of(add_of(add_of(add_of(acc, pe[0]), pe[1]), pe[2]), pe[3]);
+        }
+      }
+      for (; k + 4 <= klen; k += 4) {
+        const i32x4_t p = *(const i32x4_t*)(pr + k);
+        const Acc* pe = (const Acc*)&p;
+        acc = add_of(add_of(add_of(add_of(acc, pe[0]), pe[1]), pe[2]), pe[3]);
+      }
+      for (; k < klen; ++k) acc = add_of(acc, pr[k]);
+    }
+  }
+  if (folds) out[blockIdx.x * kDotCells + t] = narrow<In, Acc, Out>(acc);  // a padding cell keeps zero
+}
+
 
 // The same fold with coalesced reads: one wave per 64 consecutive output cells, the residue taken
 // 64 positions at a time. Lane l decodes residue position r0 + l; for each of the wave's cells in
@@ -1569,7 +1741,31 @@ void contract_t(hipStream_t s, void* out, const void* lhs, const void* rhs, int6
   FO_HIP(hipGetLastError());
 }
 
+template <typename In, typename Acc, typename Out>
+void contract_dot_t(hipStream_t s, void* out, const void* lhs, const void* rhs, int64_t n, const Wheels<2>& ow,
+                    int64_t K, bool vec) {
+  if (vec && K >= 64)
+    hipLaunchKernelGGL((k_contract_dot_staged<In, Acc, Out>), dim3((unsigned)((n + kDotCells - 1) / kDotCells)),
+                       dim3(kBlock), 0, s, (Out*)out, (const In*)lhs, (const In*)rhs, (uint32_t)n, ow, (uint32_t)K);
+  else
+    hipLaunchKernelGGL((k_contract_dot<In, Acc, Out>), dim3((unsigned)((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s,
+                       (Out*)out, (const In*)lhs, (const In*)rhs, (uint32_t)n, ow, (uint32_t)K, (int32_t)vec);
+  FO_HIP(hipGetLastError());
+}
+
 }  // namespace
+
+bool launch_contraction_dot(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
+                            int64_t n, const Wheels<2>& ow, int64_t K, bool vec) {
+  if (n <= 0 || n >= (1ll << 31) || K >= (1ll << 31)) return false;
+  if (in_t == FO_BF16 && out_t == FO_BF16) return contract_dot_t<uint16_t, float, uint16_t>(s, out, lhs, rhs, n, ow, K, vec), true;
+  if (in_t == FO_BF16 && out_t == FO_F32) return contract_dot_t<uint16_t, float, float>(s, out, lhs, rhs, n, ow, K, vec), true;
+  if (in_t == FO_F32 && out_t == FO_F32) return contract_dot_t<float, float, float>(s, out, lhs, rhs, n, ow, K, vec), true;
+  if (in_t == FO_I8 && out_t == FO_I8) return contract_dot_t<int8_t, int32_t, int8_t>(s, out, lhs, rhs, n, ow, K, vec), true;
+  if (in_t == FO_I8 && out_t == FO_I32) return contract_dot_t<int8_t, int32_t, int32_t>(s, out, lhs, rhs, n, ow, K, vec), true;
+  if (in_t == FO_I32 && out_t == FO_I32) return contract_dot_t<int32_t, int32_t, int32_t>(s, out, lhs, rhs, n, ow, K, vec), true;
+  return false;
+}
 
 void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t,
                                 fo_dtype out_t, int64_t ll, int64_t rl, int64_t n, const Wheels<2>& ow,

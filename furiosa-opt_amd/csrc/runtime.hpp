@@ -285,6 +285,11 @@ void launch_reduce_split(hipStream_t s, void* dst, const void* src, fo_dtype t, 
                          const ReduceSplit& plan, void* scratch);
 
 // Generic contraction: out wheels / residue wheels with strides into (lhs, rhs).
+// Batched dot products (k_contract_dot): every out wheel reads both operands, the residue K
+// contiguous elements in both; vec: every row start 16-byte aligned. False for a type pair it does
+// not take.
+bool launch_contraction_dot(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
+                            int64_t n, const Wheels<2>& ow, int64_t K, bool vec);
 void launch_contraction_generic(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t,
                                 fo_dtype out_t, int64_t lhs_len, int64_t rhs_len, int64_t out_count,
                                 const Wheels<2>& out_w, const Wheels<2>& res_w);

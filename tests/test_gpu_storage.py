@@ -783,6 +783,47 @@ def test_gemm_special_sums(rt, out_t):
             close(g[r0], w)
 
 
+# Batched dot products (k_contract_dot): every output wheel reads both operands, the residue one
+# contiguous run in both -- the MNIST fc1 stream's shape. Padded output cells (zero), rows whose
+# starts are not 16-byte aligned (the element-wise reads), K not a multiple of the 16-byte batch, and
+# two batch wheels.
+DOT_CASES = [
+    (dict(B=37, K=800), "B, K", "B, K", "B, K", "B"),
+    (dict(B=37, K=800), "B, K", "B, K", "B, K", "B # 40"),
+    (dict(B=50, K=803), "B, K", "B, K", "B, K", "B"),
+    (dict(A=3, B=12, K=72), "A, B, K", "B, A, K", "A, B, K", "A, B"),
+    (dict(A=2, B=8, K=256), "A # 4, B, K", "A # 4, B, K", "A # 4, B, K", "A # 4, B"),
+    # Three 512-position stages, the last ragged (16-byte aligned rows padded past K), a partial block.
+    (dict(B=40, K=1100), "B, K # 1104", "B, K # 1104", "B, K", "B"),
+    # MNIST fc1's shape: a padded chip axis that neither operand reads, then H dot products of X.
+    (dict(H=256, X=800), "1, 1 # 2, H, X / 16, X % 16", "1, 1 # 2, H, X", "1, 1 # 2, H, X / 32, X % 32",
+     "1, 1 # 2, H"),
+]
+
+
+@pytest.mark.parametrize("case", DOT_CASES, ids=lambda c: f"{c[1]}|{c[2]}->{c[4]}")
+@pytest.mark.parametrize("types", [(BF16, F32), (BF16, BF16), (F32, F32), (I8, I32), (I8, I8)],
+                         ids=["bf16-f32", "bf16", "f32", "i8-i32", "i8"])
+def test_contraction_batched_dot(rt, case, types):
+    sizes, l_t, r_t, p_t, o_t = case
+    in_t, out_t = types
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
+    rng = np.random.default_rng(24)
+    if in_t == BF16:
+        lhs, rhs = special_bf16(rng, mr.size(lo)), special_bf16(rng, mr.size(ro))
+    elif in_t == F32:
+        lhs = rng.standard_normal(mr.size(lo)).astype(np.float32)
+        rhs = rng.standard_normal(mr.size(ro)).astype(np.float32)
+    else:
+        lhs = rng.integers(-128, 128, mr.size(lo)).astype(np.int8)
+        rhs = rng.integers(-128, 128, mr.size(ro)).astype(np.int8)
+    want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
+    print(f"batched dot {sizes} {l_t} -> {o_t} {in_t}->{out_t}", flush=True)
+    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[out_t]))  # dead cells must come out zero
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
+
+
 # One vector against weight rows (k_gemv: a lane folds each cell in k order). Sizes cover each
 # rows-per-block choice (16, 32, 64), a ragged last block, K with a partial last stage, K = 8, rows
 # wider than K (a padded row stride) and a strided output.
