@@ -383,6 +383,114 @@ def bench_engine(fh, rt, steps, warmup, rng):
     return out
 
 
+# The sizes of the reference's storage microbenchmark (furiosa-opt-examples/benches/storage.rs:20-28).
+STORAGE_SQ = dict(A=512, B=512)
+STORAGE_CUBE = dict(M=128, K=128, N=128)
+STORAGE_WIDE = dict(W=1 << 20, T=4)
+
+
+def storage_data(seed: int = 42):
+    """f32 inputs of storage.rs's shapes: two 512-squares, the 128 x 128 contraction operands and the
+    2^20 x 4 wide-thin tensor."""
+    rng = np.random.default_rng(seed)
+    g = lambda n: rng.standard_normal(n, dtype=np.float32)
+    return dict(x=g(512 * 512), y=g(512 * 512), l=g(128 * 128), r=g(128 * 128), w=g((1 << 20) * 4))
+
+
+def storage_gpu(fh, rt, data):
+    """storage.rs's ten ops (benches/storage.rs:33-100) as one seam call each: map (x * 2), zip
+    (x + y), reduce_add and transpose on the 512-square, reduce_add of 2^20 x 4 over its thin axis,
+    the fused 128^3 contraction, and that contraction's composed parts (the two broadcast
+    transposes, the zip and the reduce). The mappings are built once, outside the thunks, as an
+    engine binding holds its compile-time layouts; thunks that relayout flush their output, so the
+    runtime does the pass it would otherwise leave recorded for the next reader."""
+    F32, sq, cube, wide = fh.F32, STORAGE_SQ, STORAGE_CUBE, STORAGE_WIDE
+    ab, a_, ba = (fh.m(t, **sq) for t in ("A, B", "A", "B, A"))
+    wt, w_ = fh.m("W, T", **wide), fh.m("W", **wide)
+    mk, kn, mkn, mn = (fh.m(t, **cube) for t in ("M, K", "K, N", "M, K, N", "M, N"))
+    x, y, l, r, w = (rt.upload(data[k]) for k in "xylrw")
+    d_sq, d_a, d_w, d_mn = rt.alloc(4 * 512 * 512), rt.alloc(4 * 512), rt.alloc(4 << 20), rt.alloc(4 * 128 * 128)
+    d_mkn1, d_mkn2, d_prod = (rt.alloc(4 << 21) for _ in range(3))
+    mul2, add, mul = fh.op("MUL_F", fh.RHS_IMM, 2.0), fh.op("ADD_F"), fh.op("MUL_F")
+    ADD = fh.RED["ADD"]
+
+    def bcast(dst, src, view):
+        rt.transpose(dst, src, F32, view, mkn, allow_broadcast=True)
+        dst.flush()
+
+    def transpose():
+        rt.transpose(d_sq, x, F32, ab, ba)
+        d_sq.flush()
+
+    bcast(d_mkn1, l, mk)
+    bcast(d_mkn2, r, kn)
+    rt.zip_with(d_prod, F32, d_mkn1, d_mkn2, F32, 1 << 21, mul)
+    return {
+        "map_512x512": lambda: rt.map(d_sq, F32, x, F32, 512 * 512, mul2),
+        "zip_with_512x512": lambda: rt.zip_with(d_sq, F32, x, y, F32, 512 * 512, add),
+        "reduce_add_512x512_to_512": lambda: rt.reduce(d_a, x, F32, ab, a_, ADD, 0),
+        "reduce_add_2p20x4_to_2p20": lambda: rt.reduce(d_w, w, F32, wt, w_, ADD, 0),
+        "transpose_512x512": transpose,
+        "contraction_128x128x128": lambda: rt.contraction(d_mn, l, r, F32, F32, mk, kn, mkn, mn),
+        "part_transpose_bcast_MK_to_MKN": lambda: bcast(d_mkn1, l, mk),
+        "part_transpose_bcast_KN_to_MKN": lambda: bcast(d_mkn2, r, kn),
+        "part_zip_128p3": lambda: rt.zip_with(d_prod, F32, d_mkn1, d_mkn2, F32, 1 << 21, mul),
+        "part_reduce_128p3_to_128p2": lambda: rt.reduce(d_mn, d_prod, F32, mkn, mn, ADD, 0),
+    }
+
+
+def storage_oracle(fh, data):
+    """The same ten ops through the oracle (oracle/fo_cpu.c and its numpy relayouts), the CPU port
+    timed beside each GPU line."""
+    from oracle import emulator as emu
+    from oracle import mapping_ref as mr
+
+    F32, sq, cube, wide = fh.F32, STORAGE_SQ, STORAGE_CUBE, STORAGE_WIDE
+    P = mr.parse
+    x, y, l, r, w = (data[k] for k in "xylrw")
+    ADD, MUL_F, ADD_F = fh.RED["ADD"], fh.OP["MUL_F"], fh.OP["ADD_F"]
+    two = int(np.float32(2.0).view(np.uint32))
+    bcast = lambda src, view: emu.transpose(np.zeros(1 << 21, np.float32), src, P(view, cube), P("M, K, N", cube))
+    lb, rb = bcast(l, "M, K"), bcast(r, "K, N")
+    prod = emu.zip_(lb, rb, F32, F32, MUL_F)
+    return {
+        "map_512x512": lambda: emu.map_(x, F32, F32, MUL_F, fh.RHS_IMM, two),
+        "zip_with_512x512": lambda: emu.zip_(x, y, F32, F32, ADD_F),
+        "reduce_add_512x512_to_512": lambda: emu.reduce(x, F32, P("A, B", sq), P("A", sq), ADD, 0),
+        "reduce_add_2p20x4_to_2p20": lambda: emu.reduce(w, F32, P("W, T", wide), P("W", wide), ADD, 0),
+        "transpose_512x512": lambda: emu.transpose(np.zeros(512 * 512, np.float32), x, P("A, B", sq), P("B, A", sq)),
+        "contraction_128x128x128": lambda: emu.contraction(l, r, F32, F32, P("M, K", cube), P("K, N", cube),
+                                                            P("M, K, N", cube), P("M, N", cube)),
+        "part_transpose_bcast_MK_to_MKN": lambda: bcast(l, "M, K"),
+        "part_transpose_bcast_KN_to_MKN": lambda: bcast(r, "K, N"),
+        "part_zip_128p3": lambda: emu.zip_(lb, rb, F32, F32, MUL_F),
+        "part_reduce_128p3_to_128p2": lambda: emu.reduce(prod, F32, P("M, K, N", cube), P("M, N", cube), ADD, 0),
+    }
+
+
+def bench_storage(fh, rt, steps, warmup, rng):
+    """storage.rs's ten lines on the GPU: the per-call time of each seam op over `steps` launches
+    after the warm-up (the reference's criterion reports per-iteration time for its CPU backend)."""
+    out = {}
+    for name, fn in storage_gpu(fh, rt, storage_data()).items():
+        wall, ev = timed_steady(rt, fn, steps, warmup)
+        out[name] = dict(ms=ev, wall_ms=wall, us=ev * 1e3)
+    return out
+
+
+def cpu_storage(fh):
+    """The oracle port of each storage.rs line on this host's cores, median of 3 after a warm-up."""
+    from oracle import emulator as emu
+
+    cores = emu.num_threads()
+    out = {}
+    for name, fn in storage_oracle(fh, storage_data()).items():
+        t = median_time(fn)
+        out[name] = dict(value=t * 1e6, unit="us", cores=cores, kind="port", median_of=3, seconds=t,
+                         sample="the whole op")
+    return out
+
+
 def flushed(out):
     """Runs what the runtime still owes a chain's output buffer(s) (a deferred relayout or cast, as
     the next op reading it would), so that a timed chain does all of its work."""
@@ -625,7 +733,8 @@ def main():
     res = {}
     for name, fnb in (("gemm", bench_gemm), ("gemm_f8", bench_gemm_f8), ("norm", bench_norm),
                       ("attention", bench_attention), ("chain", bench_chain),
-                      ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("engine", bench_engine), ("relayout", bench_relayout),
+                      ("w8a8", bench_w8a8), ("mlp", bench_mlp), ("engine", bench_engine), ("storage", bench_storage),
+                      ("relayout", bench_relayout),
                       ("scatter_gather", bench_scatter_gather), ("vector", bench_vector),
                       ("decode", bench_decode)):
         if only and name not in only:
@@ -665,6 +774,8 @@ def main():
             configs[k] = dict(value=r["tflops"], unit="TFLOP/s", ms=r["ms"], roofline_frac=r["tflops"] / PEAK_BF16_TFLOPS)
         else:
             configs[k] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)
+    for k, r in res.get("storage", {}).items():
+        configs[f"storage_{k}"] = dict(value=r["us"], unit="us", ms=r["ms"], roofline_frac=None)
     if "scatter_gather" in res:
         for k, r in res["scatter_gather"].items():
             configs[k] = dict(value=r["gbs"], unit="GB/s", ms=r["ms"], roofline_frac=r["gbs"] / PEAK_HBM_GBS)
@@ -695,6 +806,9 @@ def main():
         for name, cb in cpu_baselines().items():
             if name in configs:
                 configs[name]["cpu_baseline"] = dict(cb, host=host)
+        if "storage" in res:
+            for name, cb in cpu_storage(fh).items():
+                configs[f"storage_{name}"]["cpu_baseline"] = dict(cb, host=host)
         if cpu is not None:
             cpu["host"] = host
 
