@@ -176,12 +176,51 @@ std::vector<fo_buffer*> erase_records(Pred drop) {
   return gone;
 }
 
-void free_retired(const std::vector<fo_buffer*>& gone) {
+// Records being run (run_deferred) are copies that still point at their buffers, and running one
+// can drop the records of others (a source's own cast runs first, then run records go), which may
+// let a retired source go. So while any run is in progress, retired buffers that lose their last
+// reader are held here and freed when the outermost run has launched everything it copied.
+std::mutex g_free_mu;
+int g_run_depth = 0;
+std::vector<fo_buffer*> g_free_later;
+
+void free_now(const std::vector<fo_buffer*>& gone) {
   for (fo_buffer* b : gone) {
     std::shared_ptr<fo_graph_mem> rec = std::move(b->retired_in);
     free_block(b, rec);
   }
 }
+
+void free_retired(const std::vector<fo_buffer*>& gone) {
+  if (gone.empty()) return;
+  {
+    std::lock_guard<std::mutex> lock(g_free_mu);
+    if (g_run_depth > 0) {
+      g_free_later.insert(g_free_later.end(), gone.begin(), gone.end());
+      return;
+    }
+  }
+  free_now(gone);
+}
+
+// Marks a run of deferred records in progress for its lifetime (see free_retired).
+struct RunScope {
+  RunScope() {
+    std::lock_guard<std::mutex> lock(g_free_mu);
+    ++g_run_depth;
+  }
+  ~RunScope() {
+    std::vector<fo_buffer*> gone;
+    {
+      std::lock_guard<std::mutex> lock(g_free_mu);
+      if (--g_run_depth == 0) gone.swap(g_free_later);
+    }
+    try {
+      free_now(gone);
+    } catch (...) {  // a failed free leaves its error for the next call to report
+    }
+  }
+};
 
 void materialize(const fo_buffer* b);
 void fill_pending(fo_runtime* rt, const fo_buffer* b);
@@ -212,6 +251,7 @@ struct TraceScope {
 // Runs deferred casts, in order, outside the lock; a cast whose source has a deferred cast into it
 // runs that one first.
 void run_deferred(const std::vector<WidenRecord>& rs) {
+  RunScope running;  // no buffer a copied record points at is freed before the loop ends
   for (auto& r : rs) {
     materialize(r.src);
     FO_HIP(hipSetDevice(r.rt->device));
@@ -2139,6 +2179,27 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
           launch_gemm_wheels(rt->stream, O, L, R, ct, co, M, N, rw[0].size, B, dm, dn, db);
           return;
         }
+      }
+      // f32 and i32 operands with one row, column, batch and contracted wheel each: the vector-unit
+      // tile kernel, each cell folded in k order (any k strides).
+      if ((ct == FO_F32 || ct == FO_I32) && co == ct && !padded && rw.size() == 1 && mw.size() <= 1 &&
+          nw.size() <= 1 && bw.size() <= 1) {
+        GemmDesc d;
+        d.M = mw.empty() ? 1 : mw[0].w.size;
+        d.N = nw.empty() ? 1 : nw[0].w.size;
+        d.K = rw[0].size;
+        d.batch = bw.empty() ? 1 : bw[0].w.size;
+        d.lda = mw.empty() ? 0 : mw[0].w.stride[0];
+        d.ldb = nw.empty() ? 0 : nw[0].w.stride[1];
+        d.ldc_m = mw.empty() ? 0 : mw[0].place;
+        d.ldc_n = nw.empty() ? 0 : nw[0].place;
+        d.a_batch = bw.empty() ? 0 : bw[0].w.stride[0];
+        d.b_batch = bw.empty() ? 0 : bw[0].w.stride[1];
+        d.c_batch = bw.empty() ? 0 : bw[0].place;
+        const int64_t sa = rw[0].stride[0], sb = rw[0].stride[1];
+        const int64_t amax = (d.batch - 1) * d.a_batch + (d.M - 1) * d.lda + (d.K - 1) * sa;
+        const int64_t bmax = (d.batch - 1) * d.b_batch + (d.N - 1) * d.ldb + (d.K - 1) * sb;
+        if (amax < lhs_len && bmax < rhs_len && launch_contraction_simt(rt->stream, O, L, R, ct, co, d, sa, sb)) return;
       }
       const int mem[2] = {0, 1};
       launch_contraction_generic(rt->stream, O, L, R, ct, co, lhs_len, rhs_len, out_count, to_desc<2>(ow, mem),

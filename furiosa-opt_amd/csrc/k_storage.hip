@@ -1274,7 +1274,7 @@ ReduceSplit plan_reduce_split(fo_dtype t, int op, const void* src, int64_t src_l
   if (total < 64 || total >= (1ll << 31) || max_off >= src_len || out_count % 4 != 0) return p;
   const int64_t groups = out_count / 4, tiles = (groups + 63) / 64;
   int64_t nchunks = (kColsTargetBlocks + tiles - 1) / tiles;
-  nchunks = std::max<int64_t>(1, std::min<int64_t>({nchunks, (total + 255) / 256, 65535}));
+  nchunks = std::max<int64_t>(1, std::min<int64_t>({nchunks, (total + 15) / 16, 65535}));  // >= 16 rows a chunk
   p.nchunks = nchunks;
   p.chunk_len = (total + nchunks - 1) / nchunks;
   p.nchunks = (total + p.chunk_len - 1) / p.chunk_len;
@@ -1652,6 +1652,94 @@ __global__ void __launch_bounds__(kBlock) k_contract_dot_staged(Out* __restrict_
 }
 
 
+// Affine contractions of 4-byte types (f32, i32) on the vector units: one wave per T x T cells of a
+// batch cell (T = 8 R), lane (ty, tx) = (lane / 8, lane % 8) holding rows R ty .. R ty + R - 1 and
+// columns R tx .. R tx + R - 1 (R = 4, or 2 when 32 x 32 tiles would leave most of the chip idle).
+// K goes through LDS 32 positions at a time, k-major (a lane's rows or columns are one 8- or 16-byte
+// read), the next 32 loading into registers while the current ones are folded. A stage's loads run
+// k-fastest across lanes for an operand whose k stride is 1, else row-fastest. Each cell adds
+// mul(a, b) to its sum in k order from zero: contraction_in's arithmetic, bit for bit.
+constexpr int kSimtK = 32;  // contracted positions per stage
+template <typename In, typename Acc, typename Out, int R>
+__global__ void __launch_bounds__(64) k_contract_simt(Out* __restrict__ out, const In* __restrict__ lhs,
+                                                      const In* __restrict__ rhs, GemmDesc d, int64_t sa, int64_t sb) {
+  using M = MacT<In, Acc>;
+  constexpr int T = 8 * R;       // rows and columns per wave
+  constexpr int NE = T / 2;      // elements of each operand per lane per stage
+  typedef Acc accr_t __attribute__((ext_vector_type(R)));
+  __shared__ Acc As[kSimtK][T + 4];
+  __shared__ Acc Bs[kSimtK][T + 4];
+  const int lane = threadIdx.x, ty = lane >> 3, tx = lane & 7;
+  const int64_t m0 = (int64_t)blockIdx.y * T, n0 = (int64_t)blockIdx.x * T, bb = blockIdx.z;
+  // Lane element i of a stage is tile position (r0 + i dr, kk + i dk): k fixed and rows every two
+  // (k-fast), or the row fixed and k every 64 / T (row-fast).
+  struct Walk {
+    const In* p;    // the lane's first element
+    int64_t step;   // elements between its consecutive ones
+    int64_t kstep;  // elements per contracted position
+    int r0, kk, dr, dk;
+  };
+  auto walk = [&](const In* base, int64_t row0, int64_t ld, int64_t sk) {
+    Walk w;
+    if (sk == 1) w.kk = lane & 31, w.r0 = lane >> 5, w.dr = 2, w.dk = 0;
+    else w.r0 = lane % T, w.kk = lane / T, w.dr = 0, w.dk = 64 / T;
+    w.p = base + (row0 + w.r0) * ld + w.kk * sk;
+    w.step = w.dr * ld + w.dk * sk;
+    w.kstep = sk;
+    return w;
+  };
+  const Walk wa = walk(lhs + bb * d.a_batch, m0, d.lda, sa), wb = walk(rhs + bb * d.b_batch, n0, d.ldb, sb);
+  const int64_t ra_rows = d.M - m0, rb_rows = d.N - n0;
+  In ra[NE], rb[NE];
+  auto load = [&](int64_t k0) {
+    const int64_t kl = d.K - k0;
+    const In* pa = wa.p + k0 * wa.kstep;
+    const In* pb = wb.p + k0 * wb.kstep;
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      ra[i] = (wa.r0 + i * wa.dr < ra_rows && wa.kk + i * wa.dk < kl) ? pa[i * wa.step] : In(0);
+      rb[i] = (wb.r0 + i * wb.dr < rb_rows && wb.kk + i * wb.dk < kl) ? pb[i * wb.step] : In(0);
+    }
+  };
+  Acc acc[R][R];
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < R; ++j) acc[i][j] = Acc(0);
+  auto step = [&](int k) {
+    const accr_t a = *(const accr_t*)&As[k][ty * R];
+    const accr_t b = *(const accr_t*)&Bs[k][tx * R];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int j = 0; j < R; ++j) acc[i][j] = add_of(acc[i][j], mul_of(a[i], b[j]));
+  };
+  load(0);
+  for (int64_t k0 = 0; k0 < d.K; k0 += kSimtK) {
+    __syncthreads();  // the previous stage's reads are done
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+      As[wa.kk + i * wa.dk][wa.r0 + i * wa.dr] = M::widen(ra[i]);
+      Bs[wb.kk + i * wb.dk][wb.r0 + i * wb.dr] = M::widen(rb[i]);
+    }
+    __syncthreads();
+    if (k0 + kSimtK < d.K) load(k0 + kSimtK);
+    if (d.K - k0 >= kSimtK) {
+#pragma unroll
+      for (int k = 0; k < kSimtK; ++k) step(k);  // unrolled: the LDS reads run ahead of the adds
+    } else {
+      for (int k = 0; k < (int)(d.K - k0); ++k) step(k);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int64_t m = m0 + ty * R + i, n = n0 + tx * R + j;
+      if (m < d.M && n < d.N) out[bb * d.c_batch + m * d.ldc_m + n * d.ldc_n] = narrow<In, Acc, Out>(acc[i][j]);
+    }
+}
+
 // The same fold with coalesced reads: one wave per 64 consecutive output cells, the residue taken
 // 64 positions at a time. Lane l decodes residue position r0 + l; for each of the wave's cells in
 // turn every lane reads that cell's operands at position r0 + l (consecutive lanes, consecutive
@@ -1754,6 +1842,30 @@ void contract_dot_t(hipStream_t s, void* out, const void* lhs, const void* rhs, 
 }
 
 }  // namespace
+
+bool launch_contraction_simt(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
+                             const GemmDesc& d, int64_t sa, int64_t sb) {
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0 || d.batch <= 0 || d.batch > 65535 || out_t != in_t) return false;
+  if (in_t != FO_F32 && in_t != FO_I32) return false;
+  // 32 x 32 cells a wave when that gives at least two waves per CU, else 16 x 16.
+  const int64_t waves32 = ((d.M + 31) / 32) * ((d.N + 31) / 32) * d.batch;
+  const int T = waves32 >= 512 ? 32 : 16;
+  const int64_t gy = (d.M + T - 1) / T, gx = (d.N + T - 1) / T;
+  if (gy > 65535 || gx > (1ll << 31) - 1) return false;
+  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)d.batch);
+#define FO_SIMT(TY, RR) \
+  hipLaunchKernelGGL((k_contract_simt<TY, TY, TY, RR>), grid, dim3(64), 0, s, (TY*)out, (const TY*)lhs, (const TY*)rhs, d, sa, sb)
+  if (in_t == FO_F32) {
+    if (T == 32) FO_SIMT(float, 4);
+    else FO_SIMT(float, 2);
+  } else {
+    if (T == 32) FO_SIMT(int32_t, 4);
+    else FO_SIMT(int32_t, 2);
+  }
+#undef FO_SIMT
+  FO_HIP(hipGetLastError());
+  return true;
+}
 
 bool launch_contraction_dot(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
                             int64_t n, const Wheels<2>& ow, int64_t K, bool vec) {

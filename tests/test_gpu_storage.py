@@ -824,6 +824,40 @@ def test_contraction_batched_dot(rt, case, types):
     assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
 
 
+# Affine f32 / i32 contractions (k_contract_simt: 32 x 32 cells per wave, each cell folded in k
+# order): k-fast and row-fast operands, ragged tiles, a batch wheel, a transposed output and K
+# below, at and past one 32-position stage.
+SIMT_CASES = [
+    (dict(M=128, K=128, N=128), "M, K", "K, N", "M, K, N", "M, N"),
+    (dict(M=37, K=70, N=45), "K, M", "N, K", "M, N, K", "M, N"),
+    (dict(B=3, M=40, K=33, N=24), "B, M, K", "B, K, N", "B, M, K, N", "B, M, N"),
+    (dict(M=50, K=5, N=70), "M, K", "N, K", "M, N, K", "N, M"),
+    (dict(M=64, K=32, N=1), "M, K", "K, N", "M, K, N", "M, N"),
+    # Enough cells for 32 x 32 tiles (512 waves); both operands row-fast, a full and a partial stage.
+    (dict(M=512, K=36, N=1024), "K, M", "K, N", "M, N, K", "M, N"),
+]
+
+
+@pytest.mark.parametrize("case", SIMT_CASES, ids=lambda c: f"{c[1]}|{c[2]}->{c[4]}:{c[0]}")
+@pytest.mark.parametrize("dtype", [F32, I32], ids=["f32", "i32"])
+def test_contraction_simt_exact(rt, case, dtype):
+    sizes, l_t, r_t, p_t, o_t = case
+    lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
+    rng = np.random.default_rng(31)
+    if dtype == F32:
+        lhs = rng.standard_normal(mr.size(lo)).astype(np.float32)
+        rhs = rng.standard_normal(mr.size(ro)).astype(np.float32)
+        lhs[::7] = -0.0  # signed zeros through the fold
+    else:
+        lhs = rng.integers(-(1 << 31), 1 << 31, mr.size(lo), dtype=np.int64).astype(np.int32)  # wrapping products
+        rhs = rng.integers(-(1 << 31), 1 << 31, mr.size(ro), dtype=np.int64).astype(np.int32)
+    want = emu.contraction(lhs, rhs, dtype, dtype, lo, ro, po, oo)
+    print(f"simt contraction {sizes} {l_t} x {r_t} -> {o_t} dtype {dtype}", flush=True)
+    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[dtype]))
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), dtype, dtype, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    assert np.array_equal(out.read(dtype).view(np.uint8), want.view(np.uint8))
+
+
 # One vector against weight rows (k_gemv: a lane folds each cell in k order). Sizes cover each
 # rows-per-block choice (16, 32, 64), a ragged last block, K with a partial last stage, K = 8, rows
 # wider than K (a padded row stride) and a strided output.
