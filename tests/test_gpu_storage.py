@@ -694,6 +694,10 @@ MFMA_CASES = [
     (dict(G=5, M=40, K=32, N=24), "M, K", "N, K", "G, M, N, K", "M, G, N"),
     (dict(I=64, J=64, K=64), "1 # 2, I / 32, J / 32, I % 32, J / 8 % 4, K", "1 # 2, I / 32, J / 32, J % 8, J / 8 % 4, K",
      "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4, K", "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4"),
+    # The template stream's layout with K past one 128-byte batch per row and a tail of single steps.
+    (dict(I=64, J=64, K=288), "1 # 2, I / 32, J / 32, I % 32, J / 8 % 4, K",
+     "1 # 2, I / 32, J / 32, J % 8, J / 8 % 4, K", "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4, K",
+     "1 # 2, I / 32, J / 32, J % 8, I % 32, J / 8 % 4"),
 ]
 
 
