@@ -2180,10 +2180,10 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
           return;
         }
       }
-      // f32 and i32 operands with one row, column, batch and contracted wheel each: the vector-unit
-      // tile kernel, each cell folded in k order (any k strides).
-      if ((ct == FO_F32 || ct == FO_I32) && co == ct && !padded && rw.size() == 1 && mw.size() <= 1 &&
-          nw.size() <= 1 && bw.size() <= 1) {
+      // One row, column, batch and contracted wheel each, no padding, and no MFMA form above (f32 and
+      // i32 operands, or K strided, or fewer than 8 rows or columns): the vector-unit tile kernel,
+      // each cell folded in k order (any k strides).
+      if (!padded && rw.size() == 1 && mw.size() <= 1 && nw.size() <= 1 && bw.size() <= 1) {
         GemmDesc d;
         d.M = mw.empty() ? 1 : mw[0].w.size;
         d.N = nw.empty() ? 1 : nw[0].w.size;

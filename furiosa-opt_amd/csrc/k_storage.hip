@@ -1652,7 +1652,8 @@ __global__ void __launch_bounds__(kBlock) k_contract_dot_staged(Out* __restrict_
 }
 
 
-// Affine contractions of 4-byte types (f32, i32) on the vector units: one wave per T x T cells of a
+// Affine contractions on the vector units (f32, i32, and bf16 or i8 operands widened as they are
+// staged): one wave per T x T cells of a
 // batch cell (T = 8 R), lane (ty, tx) = (lane / 8, lane % 8) holding rows R ty .. R ty + R - 1 and
 // columns R tx .. R tx + R - 1 (R = 4, or 2 when 32 x 32 tiles would leave most of the chip idle).
 // K goes through LDS 32 positions at a time, k-major (a lane's rows or columns are one 8- or 16-byte
@@ -1843,26 +1844,32 @@ void contract_dot_t(hipStream_t s, void* out, const void* lhs, const void* rhs, 
 
 }  // namespace
 
+template <typename In, typename Acc, typename Out>
+void simt_t(hipStream_t s, void* out, const void* lhs, const void* rhs, const GemmDesc& d, int64_t sa, int64_t sb, int T) {
+  const dim3 grid((unsigned)((d.N + T - 1) / T), (unsigned)((d.M + T - 1) / T), (unsigned)d.batch);
+  if (T == 32)
+    hipLaunchKernelGGL((k_contract_simt<In, Acc, Out, 4>), grid, dim3(64), 0, s, (Out*)out, (const In*)lhs,
+                       (const In*)rhs, d, sa, sb);
+  else
+    hipLaunchKernelGGL((k_contract_simt<In, Acc, Out, 2>), grid, dim3(64), 0, s, (Out*)out, (const In*)lhs,
+                       (const In*)rhs, d, sa, sb);
+}
+
 bool launch_contraction_simt(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
                              const GemmDesc& d, int64_t sa, int64_t sb) {
-  if (d.M <= 0 || d.N <= 0 || d.K <= 0 || d.batch <= 0 || d.batch > 65535 || out_t != in_t) return false;
-  if (in_t != FO_F32 && in_t != FO_I32) return false;
+  if (d.M <= 0 || d.N <= 0 || d.K <= 0 || d.batch <= 0 || d.batch > 65535) return false;
   // 32 x 32 cells a wave when that gives at least two waves per CU, else 16 x 16.
   const int64_t waves32 = ((d.M + 31) / 32) * ((d.N + 31) / 32) * d.batch;
   const int T = waves32 >= 512 ? 32 : 16;
-  const int64_t gy = (d.M + T - 1) / T, gx = (d.N + T - 1) / T;
-  if (gy > 65535 || gx > (1ll << 31) - 1) return false;
-  const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)d.batch);
-#define FO_SIMT(TY, RR) \
-  hipLaunchKernelGGL((k_contract_simt<TY, TY, TY, RR>), grid, dim3(64), 0, s, (TY*)out, (const TY*)lhs, (const TY*)rhs, d, sa, sb)
-  if (in_t == FO_F32) {
-    if (T == 32) FO_SIMT(float, 4);
-    else FO_SIMT(float, 2);
-  } else {
-    if (T == 32) FO_SIMT(int32_t, 4);
-    else FO_SIMT(int32_t, 2);
-  }
-#undef FO_SIMT
+  if ((d.M + T - 1) / T > 65535 || (d.N + T - 1) / T > (1ll << 31) - 1) return false;
+  if (in_t == FO_F32 && out_t == FO_F32) simt_t<float, float, float>(s, out, lhs, rhs, d, sa, sb, T);
+  else if (in_t == FO_I32 && out_t == FO_I32) simt_t<int32_t, int32_t, int32_t>(s, out, lhs, rhs, d, sa, sb, T);
+  else if (in_t == FO_BF16 && out_t == FO_F32) simt_t<uint16_t, float, float>(s, out, lhs, rhs, d, sa, sb, T);
+  else if (in_t == FO_BF16 && out_t == FO_BF16) simt_t<uint16_t, float, uint16_t>(s, out, lhs, rhs, d, sa, sb, T);
+  else if (in_t == FO_I8 && out_t == FO_I32) simt_t<int8_t, int32_t, int32_t>(s, out, lhs, rhs, d, sa, sb, T);
+  else if (in_t == FO_I8 && out_t == FO_I8) simt_t<int8_t, int32_t, int8_t>(s, out, lhs, rhs, d, sa, sb, T);
+  else
+    return false;
   FO_HIP(hipGetLastError());
   return true;
 }

@@ -288,9 +288,10 @@ void launch_reduce_split(hipStream_t s, void* dst, const void* src, fo_dtype t, 
 // Batched dot products (k_contract_dot): every out wheel reads both operands, the residue K
 // contiguous elements in both; vec: every row start 16-byte aligned. False for a type pair it does
 // not take.
-// k_storage.hip: an affine contraction of f32 or i32 operands (one row, column, batch and contracted
-// wheel each; A(m, k) = a_batch*b + lda*m + sa*k, B(n, k) = b_batch*b + ldb*n + sb*k), each cell the
-// serial fold in k order (bit-exact); false when the shape or types do not fit the kernel.
+// k_storage.hip: an affine contraction (one row, column, batch and contracted wheel each; A(m, k) =
+// a_batch*b + lda*m + sa*k, B(n, k) = b_batch*b + ldb*n + sb*k) of f32 -> f32, i32 -> i32, bf16 ->
+// f32 / bf16 or i8 -> i32 / i8, each cell the serial fold in k order (bit-exact); false when the
+// shape or types do not fit the kernel.
 struct GemmDesc;
 bool launch_contraction_simt(hipStream_t s, void* out, const void* lhs, const void* rhs, fo_dtype in_t, fo_dtype out_t,
                              const GemmDesc& d, int64_t sa, int64_t sb);

@@ -843,23 +843,32 @@ SIMT_CASES = [
 
 
 @pytest.mark.parametrize("case", SIMT_CASES, ids=lambda c: f"{c[1]}|{c[2]}->{c[4]}:{c[0]}")
-@pytest.mark.parametrize("dtype", [F32, I32], ids=["f32", "i32"])
-def test_contraction_simt_exact(rt, case, dtype):
+@pytest.mark.parametrize("types", [(F32, F32), (I32, I32), (BF16, F32), (BF16, BF16), (I8, I32), (I8, I8)],
+                         ids=["f32", "i32", "bf16-f32", "bf16", "i8-i32", "i8"])
+def test_contraction_simt_exact(rt, case, types):
     sizes, l_t, r_t, p_t, o_t = case
+    in_t, out_t = types
+    if in_t == BF16 and l_t == "M, K" and r_t == "N, K":
+        pytest.skip("unit-stride K on both sides with 8+ rows and columns: the bf16 MFMA kernel (tolerance tests)")
     lo, ro, po, oo = (mr.parse(t, sizes) for t in (l_t, r_t, p_t, o_t))
     rng = np.random.default_rng(31)
-    if dtype == F32:
+    if in_t == F32:
         lhs = rng.standard_normal(mr.size(lo)).astype(np.float32)
         rhs = rng.standard_normal(mr.size(ro)).astype(np.float32)
         lhs[::7] = -0.0  # signed zeros through the fold
-    else:
+    elif in_t == I32:
         lhs = rng.integers(-(1 << 31), 1 << 31, mr.size(lo), dtype=np.int64).astype(np.int32)  # wrapping products
         rhs = rng.integers(-(1 << 31), 1 << 31, mr.size(ro), dtype=np.int64).astype(np.int32)
-    want = emu.contraction(lhs, rhs, dtype, dtype, lo, ro, po, oo)
-    print(f"simt contraction {sizes} {l_t} x {r_t} -> {o_t} dtype {dtype}", flush=True)
-    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[dtype]))
-    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), dtype, dtype, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
-    assert np.array_equal(out.read(dtype).view(np.uint8), want.view(np.uint8))
+    elif in_t == BF16:
+        lhs, rhs = special_bf16(rng, mr.size(lo)), special_bf16(rng, mr.size(ro))
+    else:
+        lhs = rng.integers(-128, 128, mr.size(lo)).astype(np.int8)
+        rhs = rng.integers(-128, 128, mr.size(ro)).astype(np.int8)
+    want = emu.contraction(lhs, rhs, in_t, out_t, lo, ro, po, oo)
+    print(f"simt contraction {sizes} {l_t} x {r_t} -> {o_t} {in_t}->{out_t}", flush=True)
+    out = rt.upload(np.full(mr.size(oo), 0x5A, dtype=fh.NP_DTYPE[out_t]))
+    rt.contraction(out, rt.upload(lhs), rt.upload(rhs), in_t, out_t, *(fh.m(t, **sizes) for t in (l_t, r_t, p_t, o_t)))
+    assert np.array_equal(out.read(out_t).view(np.uint8), want.view(np.uint8))
 
 
 # One vector against weight rows (k_gemv: a lane folds each cell in k order). Sizes cover each
