@@ -15,8 +15,9 @@
 // max rounds bf16(p) at another scale, and where a row's output is a near-cancelling average of
 // thousands of values those roundings do not cancel. With row_max given, the reference max starts
 // at the given value instead of -inf: for the reference's own max no block exceeds it, so no rescale
-// happens and every p = exp(s - m) is the reference's. (A smaller given value is rescaled past as
-// without it.)
+// happens and every p = exp(s - m) is the reference's, at most 1; p is then clipped at 1 as the
+// reference's mask clip does, which changes only a NaN p (a NaN logit), into 1. The given value must
+// be at least the max over the row's visible keys (the reference's max over every key is).
 //
 // Workgroups of kWaves = 8 waves (256 queries, two waves per SIMD) share each K/V tile: one load of
 // it per 256 queries (measured 4% faster than two workgroups of four waves per CU).
@@ -126,7 +127,7 @@ __device__ __forceinline__ void qk(const uint8_t* __restrict__ sK, const i32x4_t
 }
 
 // One step: S of the block (K from sK), its softmax, then its PV product (V^T from sVt).
-template <int D, bool MASK>
+template <int D, bool MASK, bool GIVEN>
 __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const uint8_t* __restrict__ sVt,
                                           const i32x4_t (&qf)[AttnCfg<D>::KS], f32x16_t (&o)[AttnCfg<D>::DT],
                                           float& m_run, float& l_part,
@@ -193,6 +194,19 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
         float x0 = __builtin_bit_cast(float, w << 16), x1 = __builtin_bit_cast(float, w & 0xffff0000u);
         float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, kL2E, -ms));
         float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, kL2E, -ms));
+        if (GIVEN) {
+          // The reference's mask is vector_clip(Min, mask) on p (attention.rs:98-134): with the
+          // reference's max every p <= 1 and min(p, 1) = p, while a NaN p (a NaN logit) becomes 1;
+          // a masked key's p is min(p, 0) = 0 whatever p is (also where a row's max is -inf and
+          // exp(-inf - m) is NaN).
+          p0 = __builtin_fminf(p0, 1.0f);
+          p1 = __builtin_fminf(p1, 1.0f);
+          if (MASK) {
+            const int thr = lim - kv0 - kt * 32 - 4 * g;
+            p0 = (8 * (r >> 2) + (r & 3) > thr) ? 0.0f : p0;
+            p1 = (8 * ((r + 1) >> 2) + ((r + 1) & 3) > thr) ? 0.0f : p1;
+          }
+        }
         psum += p0 + p1;
         pf[kt * 2 + h][e] = (int)pack_bf16(p0, p1);
       }
@@ -210,7 +224,7 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
   }
 }
 
-template <int D>
+template <int D, bool GIVEN>
 __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __restrict__ out, const uint16_t* __restrict__ q,
                                                      const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                      const float* __restrict__ row_max, int32_t heads_total,
@@ -325,7 +339,7 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
     load_k(kv0 + kBN);
     load_v(kv0 + kBN);
     __builtin_amdgcn_sched_barrier(0);
-    attn_step<D, false>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
+    attn_step<D, false, GIVEN>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
     store_k((j + 1) & 1);
     store_v((j + 1) & 1);
     __syncthreads();
@@ -336,7 +350,7 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
     load_v(kv0 + kBN);
     __builtin_amdgcn_sched_barrier(0);
     if (!(causal && kv0 > q0w + 31))  // wave-uniform
-      attn_step<D, true>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
+      attn_step<D, true, GIVEN>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
     store_k((j + 1) & 1);
     store_v((j + 1) & 1);
     __syncthreads();
@@ -365,23 +379,26 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
           const int blk = bp + d;
           const uint32_t ob = pack_bf16(o[t][blk * 4 + 2 * e], o[t][blk * 4 + 2 * e + 1]);
           const float a = __builtin_bit_cast(float, ob << 16), b = __builtin_bit_cast(float, ob & 0xffff0000u);
-          wv[d][e] = (int)pack_bf16(div_cr(a, denom, rinv), div_cr(b, denom, rinv));
+          // An infinite o (an infinite value in V) divides to itself; div_cr's remainder would be NaN.
+          const float qa = __builtin_isinf(a) ? a : div_cr(a, denom, rinv);
+          const float qb = __builtin_isinf(b) ? b : div_cr(b, denom, rinv);
+          wv[d][e] = (int)pack_bf16(qa, qb);
         }
       const i32x4_t q4 = regroup8(wv[0], wv[1]);
       if (myq < seq) *(i32x4_t*)(orow + t * 32 + 8 * bp + 8 * g) = q4;
     }
 }
 
-template <int D>
+template <int D, bool GIVEN>
 void launch_d(hipStream_t s, dim3 grid, uint16_t* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
               const float* row_max, int64_t ht, int64_t seq, int64_t nqb, float inv_sd, int causal) {
   constexpr int lds = AttnCfg<D>::LDS;
   static bool attr_set = false;  // dynamic LDS above 64 KiB must be opted into
   if (!attr_set) {
-    FO_HIP(hipFuncSetAttribute((const void*)k_attn_fwd<D>, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+    FO_HIP(hipFuncSetAttribute((const void*)k_attn_fwd<D, GIVEN>, hipFuncAttributeMaxDynamicSharedMemorySize, lds));
     attr_set = true;
   }
-  hipLaunchKernelGGL(k_attn_fwd<D>, grid, dim3(kNT), lds, s, out, q, k, v, row_max, (int32_t)ht, (int32_t)seq,
+  hipLaunchKernelGGL((k_attn_fwd<D, GIVEN>), grid, dim3(kNT), lds, s, out, q, k, v, row_max, (int32_t)ht, (int32_t)seq,
                      (int32_t)nqb, inv_sd, causal);
 }
 
@@ -397,9 +414,11 @@ void launch_attention_prefill(hipStream_t s, uint16_t* out, const uint16_t* q, c
   dim3 grid((unsigned)(ht * nqb));
   const float inv_sd = 1.0f / sqrt_d;
   if (head_dim == 128)
-    launch_d<128>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
+    row_max ? launch_d<128, true>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal)
+            : launch_d<128, false>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
   else
-    launch_d<64>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
+    row_max ? launch_d<64, true>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal)
+            : launch_d<64, false>(s, grid, out, q, k, v, row_max, ht, seq, nqb, inv_sd, causal);
   FO_HIP(hipGetLastError());
 }
 

@@ -412,8 +412,10 @@ int32_t fo_rmsnorm_softmax(fo_runtime* rt, fo_buffer* out, const fo_buffer* x, c
  * (attention.rs:10 uses 11.313708 for D = 128). `row_max` (optional, may be NULL): f32 per query
  * row, laid out [B, H, S], the max m each row subtracts -- the reference's own is the max over every
  * key, taken before masking (attention.rs:77-95), as its forward reads a stored running max
- * (attention.rs:248-365); NULL takes the kernel's running max over the visible keys, which rounds
- * bf16(p) at another scale. Inputs are expected finite. */
+ * (attention.rs:248-365). A given m must be at least the max over the row's visible keys; p = exp(s - m)
+ * is then clipped at 1 like the reference's mask clip, so a NaN logit gives p = 1 as there, and an
+ * infinite value in V gives an infinite output. NULL takes the kernel's running max over the visible
+ * keys, which rounds bf16(p) at another scale; a NaN logit then makes its row NaN. */
 int32_t fo_attention_prefill(fo_runtime* rt, fo_buffer* out, const fo_buffer* q, const fo_buffer* k,
                              const fo_buffer* v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
                              float sqrt_d, int32_t causal, const fo_buffer* row_max);

@@ -317,6 +317,50 @@ def test_attention_given_max_small(rt, shape, causal):
     given_max_report(emu.bf16_to_f32(out.read(np.uint16)), want, f"attention {shape} causal={causal} given max vs oracle")
 
 
+# Non-finite inputs (the kernel is built with -fno-honor-nans): NaN and infinity in one element of
+# q, k or v, with the reference's row max given so that the semantics are the reference's (its max
+# over every key before masking: an infinite logit of a key a row does not see still sets that
+# row's max; its mask clip min(p, mask) turns a NaN p into 1). Every NaN and infinity lands where
+# the oracle's do; the other cells are held to the 1e-2 bar. (An infinite v under causal masking is left out: a masked key's p = 0 times v = inf is
+# NaN wherever the masked key is multiplied at all, which depends on how keys are blocked -- the
+# reference's 512-key chunks, the oracle's visible keys only.)
+NONFINITE = [
+    ("q", (0, 10, 5), np.nan, True),      # one query row: all NaN
+    ("k", (1, 100, 0), np.nan, True),     # one key: the rows that see it NaN
+    ("k", (0, 30, 2), np.inf, True),      # +-inf logits: NaN rows, or the key's p = 0
+    ("v", (0, 50, 7), np.inf, False),     # one value column: +inf for every row (no masking)
+]
+
+
+@pytest.mark.parametrize("case", NONFINITE, ids=lambda c: f"{c[0]}{c[1]}={c[2]}-causal{c[3]}")
+def test_attention_nonfinite(rt, case):
+    which, (hh, row, col), val, causal = case
+    b, h, s, d = 1, 2, 256, 128
+    rng = np.random.default_rng(43)
+    q, k, v = (bf16(rng, b * h * s * d) for _ in range(3))
+    clean = emu.bf16_to_f32(emu.attention_prefill(q, k, v, b * h, s, d, float(SQRT_HEAD_DIM), causal,
+                                                  row_max=np.empty(b * h * s, np.float32)))
+    arr = {"q": q, "k": k, "v": v}[which]
+    arr[(hh * s + row) * d + col] = emu.f32_to_bf16(np.array([val], np.float32))[0]
+    rm = np.empty(b * h * s, np.float32)
+    want = emu.bf16_to_f32(emu.attention_prefill(q, k, v, b * h, s, d, float(SQRT_HEAD_DIM), causal, row_max=rm))
+    print(f"attention non-finite {case}", flush=True)
+    out = rt.alloc(b * h * s * d * 2)
+    rt.attention_prefill(out, rt.upload(q), rt.upload(k), rt.upload(v), b, h, s, d, float(SQRT_HEAD_DIM), causal,
+                         row_max=rt.upload(rm))
+    got = emu.bf16_to_f32(out.read(np.uint16))
+    assert not np.array_equal(want, clean, equal_nan=True)  # the injected value reaches the output
+    for name, t in (("kernel", got), ("oracle", want)):
+        cells = t.reshape(b * h, s, d)
+        rows = sorted({(int(x), int(y)) for x, y, _ in np.argwhere(~np.isfinite(cells))})
+        print(f"  {name}: {np.isnan(t).sum()} NaN, {np.isinf(t).sum()} inf; non-finite in {len(rows)} rows "
+              f"{rows[:3]}..{rows[-3:]}", flush=True)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want)) and np.array_equal(got[np.isinf(got)], want[np.isinf(want)])
+    fin = np.isfinite(want)
+    close(got[fin], want[fin])
+
+
 def test_attention_config_given_max(rt):
     """The attention config with the reference's own row max given to the kernel: every head's first
     and last 64 queries and a seeded spread of 8 blocks of 16 queries (17,408 rows, 2.2 M cells)
