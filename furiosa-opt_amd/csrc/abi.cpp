@@ -1528,6 +1528,27 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
         });
     const fm::Joint& j = plan.j;
     const int64_t src_base = plan.src_base, dst_base = plan.dst_base;
+    if (is_nibble(t)) {  // 4-bit storage, two elements a byte: the one-step form of the nibble chain
+      check_buf(src, "src");
+      check_buf(dst, "dst");
+      note_write(dst);
+      const int64_t dst_len = (int64_t)dst->bytes * 2, src_len = (int64_t)src->bytes * 2;
+      require(dst_base <= dst_len, "transpose: dst window starts past the buffer");
+      const int64_t count = std::min<int64_t>({j.stream_size, plan.dv_size, dst_len - dst_base});
+      if (count <= 0) return;
+      require(src_base + max_live_offset(j.wheels, 0) < src_len, "transpose: the src window reads past the buffer");
+      require(count < (1ll << 31), "transpose: more than 2^31 positions");
+      set_device(rt);
+      TraceScope trace_span(rt, "transpose");
+      const int mem[1] = {0};
+      Chain c;
+      c.n = 1;
+      c.zero_unwritten = 0;
+      c.total = (uint32_t)count;
+      c.step[0] = ChainStep{to_desc<1>(j.wheels, mem), src_base, (uint32_t)count};
+      launch_relayout_chain_nibble(rt->stream, dst->ptr, src->ptr, c, (uint64_t)dst_base);
+      return;
+    }
     int64_t eb = dtype_bytes(t);
     int64_t dst_len = (int64_t)(dst->bytes / eb), src_len = (int64_t)(src->bytes / eb);
     // A broadcast of f32 data over the whole of dst (every digit live, the src digits one contiguous
@@ -1682,7 +1703,9 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
     note_write(dst);
     check_buf(src, "src");
     require(n_views >= 2 && views != nullptr, "transpose_chain: needs at least two views");
-    const int64_t eb = dtype_bytes(t);
+    const bool nib = is_nibble(t);                 // 4-bit storage: two elements a byte
+    const int64_t eb = nib ? 1 : dtype_bytes(t);
+    auto elems = [&](const fo_buffer* b) { return nib ? (int64_t)b->bytes * 2 : (int64_t)(b->bytes / eb); };
     std::vector<fm::Factors> v;
     for (int i = 0; i < n_views; ++i) v.push_back(flat(views[i], "views[i]"));
     const int steps = n_views - 1;
@@ -1695,8 +1718,8 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
         require(fm::is_padding(fm::carve(v[k + 1], v[k])),
                 "transpose_chain: step " + std::to_string(k) + " adds axes absent from its source; allow its broadcast");
       fm::Joint j = fm::sequence({v[k]}, {v[k + 1]}, fm::Mode::Carve);
-      const int64_t src_len = k == 0 ? (int64_t)(src->bytes / eb) : fm::size(v[k]);
-      const int64_t dst_len = k == steps - 1 ? (int64_t)(dst->bytes / eb) : fm::size(v[k + 1]);
+      const int64_t src_len = k == 0 ? elems(src) : fm::size(v[k]);
+      const int64_t dst_len = k == steps - 1 ? elems(dst) : fm::size(v[k + 1]);
       const int64_t count = std::max<int64_t>(0, std::min<int64_t>({j.stream_size, fm::size(v[k + 1]), dst_len}));
       require(max_live_offset(j.wheels, 0) < src_len || count == 0,
               "transpose_chain: step " + std::to_string(k) + " reads past its source");
@@ -1715,9 +1738,19 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
     if (chain_direct(v)) {
       if (!any_broadcast) require(fm::is_padding(fm::carve(v.back(), v[0])), "transpose_chain: broadcast mismatch");
       fm::Joint j = fm::sequence({v[0]}, {v.back()}, fm::Mode::Carve);
-      const int64_t count = std::min<int64_t>({j.stream_size, fm::size(v.back()), (int64_t)(dst->bytes / eb)});
-      require(max_live_offset(j.wheels, 0) < (int64_t)(src->bytes / eb), "transpose_chain: reads past the source");
+      const int64_t count = std::min<int64_t>({j.stream_size, fm::size(v.back()), elems(dst)});
+      require(max_live_offset(j.wheels, 0) < elems(src), "transpose_chain: reads past the source");
       const int mem[1] = {0};
+      if (nib) {
+        if (count <= 0) return;
+        Chain c;
+        c.n = 1;
+        c.zero_unwritten = 0;
+        c.total = (uint32_t)count;
+        c.step[0] = ChainStep{to_desc<1>(j.wheels, mem), 0, (uint32_t)count};
+        launch_relayout_chain_nibble(rt->stream, dst->ptr, src->ptr, c, 0);
+        return;
+      }
       launch_relayout(rt->stream, dst->ptr, src->ptr, eb, 0, 0, count, to_desc<1>(j.wheels, mem));
       return;
     }
@@ -1743,7 +1776,7 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
         if (!sc) {
           int64_t most = 0;
           for (int k = 1; k < steps; ++k) most = std::max(most, fm::size(v[k]));
-          half = ((uint64_t)most * eb + 255) & ~(uint64_t)255;
+          half = ((nib ? (uint64_t)(most + 1) / 2 : (uint64_t)most * eb) + 255) & ~(uint64_t)255;
           sc = (uint8_t*)runtime_scratch(rt, 2 * half);
         }
         c.total = (uint32_t)fm::size(v[k1]);
@@ -1751,7 +1784,10 @@ int32_t fo_transpose_chain(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src,
         out = sc + (flip ? half : 0);
         flip ^= 1;
       }
-      launch_relayout_chain(rt->stream, out, in, eb, c);
+      if (nib)
+        launch_relayout_chain_nibble(rt->stream, out, in, c, 0);
+      else
+        launch_relayout_chain(rt->stream, out, in, eb, c);
       in = out;
       k0 = k1;
     }

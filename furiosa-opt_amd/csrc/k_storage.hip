@@ -420,38 +420,65 @@ void relayout_t(hipStream_t s, void* dst, const void* src, int64_t dst_base, int
 // position a step did not write reads as the zero of its fresh storage (Tensor::transpose zeroes
 // its destination, tensor/mod.rs:302-306); one the last step does not write is left alone.
 // ---------------------------------------------------------------------------------------------
+// Walks final position `pos` (< c.total) back through the steps: 0 = read src at *pos, 1 = zero,
+// 2 = not written.
+__device__ __forceinline__ int chain_walk(const Chain& c, int64_t* pos_io) {
+  const int unwritten = c.zero_unwritten ? 1 : 2;
+  int64_t pos = *pos_io;
+  for (int k = c.n - 1; k >= 0; --k) {
+    const ChainStep& st = c.step[k];
+    if (pos >= (int64_t)st.count) return k == c.n - 1 ? unwritten : 1;
+    uint32_t q = (uint32_t)pos;
+    int64_t off = 0;
+    bool live = true;
+    for (int i = 0; i < st.w.n; ++i) {
+      const uint32_t nq = st.w.div[i].div(q);
+      const uint32_t d = q - nq * st.w.size[i];
+      live &= d < st.w.live[i];
+      off += (int64_t)d * st.w.stride[0][i];
+      q = nq;
+    }
+    if (!live) return k == c.n - 1 ? unwritten : 1;
+    pos = st.src_base + off;
+  }
+  *pos_io = pos;
+  return 0;
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kBlock) k_relayout_chain(T* __restrict__ dst, const T* __restrict__ src, Chain c) {
-  const int unwritten = c.zero_unwritten ? 1 : 2;
   for (uint32_t p = blockIdx.x * kBlock + threadIdx.x; p < c.total; p += gridDim.x * kBlock) {
     int64_t pos = p;
-    int state = 0;  // 0: read src at pos, 1: zero, 2: not written
-    for (int k = c.n - 1; k >= 0; --k) {
-      const ChainStep& st = c.step[k];
-      if (pos >= (int64_t)st.count) {
-        state = k == c.n - 1 ? unwritten : 1;
-        break;
-      }
-      uint32_t q = (uint32_t)pos;
-      int64_t off = 0;
-      bool live = true;
-      for (int i = 0; i < st.w.n; ++i) {
-        const uint32_t nq = st.w.div[i].div(q);
-        const uint32_t d = q - nq * st.w.size[i];
-        live &= d < st.w.live[i];
-        off += (int64_t)d * st.w.stride[0][i];
-        q = nq;
-      }
-      if (!live) {
-        state = k == c.n - 1 ? unwritten : 1;
-        break;
-      }
-      pos = st.src_base + off;
-    }
+    const int state = chain_walk(c, &pos);
     if (state == 0)
       dst[p] = src[pos];
     else if (state == 1)
       dst[p] = T(0);
+  }
+}
+
+// The same walk over 4-bit elements (two per byte, element 2k in the low nibble of byte k; the
+// reference packs sub-byte storage this way, storage/buf.rs:56-80, scalar.rs:1093-1117). Final
+// position p is element dst_base + p of dst. One thread owns one dst byte and writes it whole, so
+// the byte's other nibble -- outside the window, or not written -- keeps what dst holds.
+__global__ void __launch_bounds__(kBlock) k_relayout_chain_nibble(uint8_t* __restrict__ dst,
+                                                                  const uint8_t* __restrict__ src, Chain c,
+                                                                  uint64_t dst_base) {
+  const uint64_t b0 = dst_base / 2, nbytes = (dst_base + c.total + 1) / 2 - b0;
+  for (uint64_t t = blockIdx.x * (uint64_t)kBlock + threadIdx.x; t < nbytes; t += (uint64_t)gridDim.x * kBlock) {
+    const uint64_t b = b0 + t;
+    uint32_t byte = dst[b];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t p = (int64_t)(2 * b + h) - (int64_t)dst_base;
+      if (p < 0 || p >= (int64_t)c.total) continue;
+      int64_t pos = p;
+      const int state = chain_walk(c, &pos);
+      if (state == 2) continue;
+      const uint32_t v = state == 0 ? (src[pos >> 1] >> (4 * (pos & 1))) & 0xfu : 0u;
+      byte = (byte & ~(0xfu << (4 * h))) | (v << (4 * h));
+    }
+    dst[b] = (uint8_t)byte;
   }
 }
 
@@ -612,6 +639,13 @@ __global__ void __launch_bounds__(kBlock) k_scatter(T* __restrict__ dst, const T
 }
 
 }  // namespace
+
+void launch_relayout_chain_nibble(hipStream_t s, void* dst, const void* src, const Chain& c, uint64_t dst_base) {
+  const int64_t nbytes = (int64_t)((dst_base + c.total + 1) / 2 - dst_base / 2);
+  hipLaunchKernelGGL(k_relayout_chain_nibble, dim3(grid_for(nbytes)), dim3(kBlock), 0, s, (uint8_t*)dst,
+                     (const uint8_t*)src, c, dst_base);
+  FO_HIP(hipGetLastError());
+}
 
 void launch_relayout_chain(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, const Chain& c) {
   dim3 g(grid_for((int64_t)c.total)), b(kBlock);

@@ -165,7 +165,7 @@ inline int64_t dtype_bytes(fo_dtype t) {
       return 4;
     case FO_I4:
     case FO_F4E2M1:
-      throw InvalidArg("4-bit (nibble-packed) elements are taken by map and contraction only");
+      throw InvalidArg("4-bit (nibble-packed) elements are taken by map, contraction and transpose only");
   }
   throw InvalidArg("unknown dtype");
 }
@@ -217,6 +217,9 @@ struct Chain {
   ChainStep step[kMaxChain];
 };
 void launch_relayout_chain(hipStream_t s, void* dst, const void* src, int64_t elem_bytes, const Chain& c);
+// The chain over 4-bit elements (two per byte); final position p goes to dst element dst_base + p,
+// and a byte's nibble the chain does not write keeps its value.
+void launch_relayout_chain_nibble(hipStream_t s, void* dst, const void* src, const Chain& c, uint64_t dst_base);
 // Gather: dst[off_d(p*slots + r)] = src[off_s(p*axis + index[r] / div)]; bad indices skipped, *flag = 1.
 // `*_slot_wheels`: how many innermost wheels of each list belong to the slot / axis part (the
 // payload's wheels follow), for the 16-byte payload path.

@@ -59,8 +59,10 @@ typedef enum fo_dtype {
   FO_F8E5M2 = 7,
   /* 4-bit types, two per byte, element 2k in the low nibble of byte k (get_nibble / set_nibble,
    * scalar.rs:1093-1117): i4 (two's complement, scalar.rs:585-690) and f4e2m1 (OCP E2M1,
-   * scalar.rs:925-1091). Taken by fo_map (casts, table lookup) and fo_contraction; a 4-bit
-   * stream has an even element count (pack_nibbles, scalar.rs:1119-1131). */
+   * scalar.rs:925-1091). Taken by fo_map (casts, table lookup), fo_contraction, fo_transpose and
+   * fo_transpose_chain (positions count nibbles: a 4-bit relayout writes only the nibbles its
+   * window holds, and the other nibble of a shared byte keeps its value); a 4-bit map or
+   * contraction stream has an even element count (pack_nibbles, scalar.rs:1119-1131). */
   FO_I4 = 8,
   FO_F4E2M1 = 9
 } fo_dtype;

@@ -11,6 +11,9 @@ import pytest
 
 import furiosa_hip as fh
 from oracle import emulator as emu
+from oracle import mapping_ref as mr
+from test_gpu_storage import CHAIN_AXES, CHAINS
+from test_mapping_resolver import PAIRS
 
 pytestmark = pytest.mark.gpu
 
@@ -50,8 +53,73 @@ def test_4bit_errors(rt):
                                (I32, I4, "ADD_FXP")]:
         with pytest.raises(fh.FoError):
             rt.map(y, dst_t, x, src_t, 8, fh.op(code))
-    with pytest.raises(fh.FoError, match="4-bit"):
-        rt.transpose(y, x, I4, fh.m("A", A=16), fh.m("A", A=16))
+    with pytest.raises(fh.FoError, match="reads past"):  # 129 nibbles from a 128-nibble buffer
+        rt.transpose(y, x, I4, fh.m("A", A=129), fh.m("A", A=129))
+
+
+# ---- 4-bit relayouts: Backend::transpose over a packed stream (storage/buf.rs:56-80, 257-313) ------
+# Each case runs on the unpacked elements in the oracle and is packed back; a destination whose
+# element count is odd has a pad nibble, and every nibble the relayout does not write (dead cells,
+# cells outside a window, the pad) must keep the random value the destination started with.
+
+def i4_stream(rng, n):
+    """n random i4 elements, packed (an odd count gets a random pad nibble)."""
+    return rng.integers(0, 256, (n + 1) // 2, dtype=np.uint8)
+
+
+def i4_want(init, src, n_dst, n_src, fn):
+    cells = emu.unpack_i4(init)
+    cells[:n_dst] = fn(cells[:n_dst].copy(), emu.unpack_i4(src)[:n_src])
+    return emu.pack_nibbles(cells)
+
+
+@pytest.mark.parametrize("case", PAIRS, ids=[f"{c[1]} -> {c[2]}" for c in PAIRS])
+def test_i4_transpose_pairs(rt, case):
+    sizes, a, b = case
+    rng = np.random.default_rng(74)
+    so, do = mr.parse(a, sizes), mr.parse(b, sizes)
+    ns, nd = mr.size(so), mr.size(do)
+    src, init = i4_stream(rng, ns), i4_stream(rng, nd)
+    want = i4_want(init, src, nd, ns, lambda d, s_: emu.transpose(d, s_, so, do))
+    d = rt.upload(init)
+    rt.transpose(d, rt.upload(src), I4, fh.m(a, **sizes), fh.m(b, **sizes), allow_broadcast=True)
+    assert np.array_equal(d.read(np.uint8), want)
+
+
+@pytest.mark.parametrize("case", range(len(CHAINS)), ids=[" -> ".join(c[0]) for c in CHAINS])
+def test_i4_transpose_chain(rt, case):
+    views, bc = CHAINS[case]
+    rng = np.random.default_rng(75 + case)
+    parsed = [mr.parse(v, CHAIN_AXES) for v in views]
+    ns, nd = mr.size(parsed[0]), mr.size(parsed[-1])
+    src, init = i4_stream(rng, ns), i4_stream(rng, nd)
+    want = i4_want(init, src, nd, ns, lambda d, s_: emu.transpose_chain(d, s_, parsed))
+    d = rt.upload(init)
+    rt.transpose_chain(d, rt.upload(src), I4, [fh.m(v, **CHAIN_AXES) for v in views], bc)
+    assert np.array_equal(d.read(np.uint8), want)
+
+
+def test_i4_transpose_odd_windows(rt):
+    """Windows that start on an odd element: the first and last bytes are shared with cells the
+    relayout must not touch."""
+    s = dict(A=3, B=7)
+    rng = np.random.default_rng(76)
+    full, row = mr.parse("A, B", s), mr.parse("B", s)
+    # a row into the middle of a [3, 7] storage: elements 7 .. 13 (bytes 3 .. 6, both ends shared)
+    src, init = i4_stream(rng, 7), i4_stream(rng, 21)
+    want = i4_want(init, src, 21, 7, lambda d, s_: emu.transpose(d, s_, row, row, dst_map=full, dst_offset={"A": 1}))
+    d = rt.upload(init)
+    rt.transpose(d, rt.upload(src), I4, fh.m("B", **s), fh.m("B", **s), dst_map=fh.m("A, B", **s),
+                 dst_offset={"A": 1})
+    assert np.array_equal(d.read(np.uint8), want)
+    # the middle row of a [3, 7] storage (elements 7 .. 13, starting in a byte's high nibble) into
+    # a 7-cell stream with a pad nibble
+    src, init = i4_stream(rng, 21), i4_stream(rng, 7)
+    want = i4_want(init, src, 7, 21, lambda d, s_: emu.transpose(d, s_, row, row, src_map=full, src_offset={"A": 1}))
+    d = rt.upload(init)
+    rt.transpose(d, rt.upload(src), I4, fh.m("B", **s), fh.m("B", **s), src_map=fh.m("A, B", **s),
+                 src_offset={"A": 1})
+    assert np.array_equal(d.read(np.uint8), want)
 
 
 def run_gemm(rt, out_t, Mm, Nn, Kk, seed):

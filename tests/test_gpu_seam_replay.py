@@ -15,12 +15,18 @@ ones those stages build from each kernel's type parameters.
   * furiosa-opt-examples/src/mnist/mod.rs:8-34 (fc1, X = 800, H = 256): 256 batch cells of one
     800-long dot product each (M = N = 1), which the generic fold runs, bit-exact, on the bf16
     sources.
+  * furiosa-opt-examples/src/contract_element_types.rs:24-232, one single-flit contraction per
+    engine input type (i8, f8e4m3, the i8 zero-point subtraction, i4, f8e5m2, bf16; A = R = 8,
+    Cluster m![1 # 2], Slice m![1 # 256], Lane m![R]): every stage, the 4-bit ones included, as the
+    seam sees it, checked against the integer matmul the reference's answer key computes by hand
+    (tests/contract_element_types_answer_tests.rs:19-54) and against the oracle.
 """
 import numpy as np
 import pytest
 
 import furiosa_hip as fh
 from oracle import emulator as emu
+from oracle import mapping_ref as mr
 from test_gpu_storage import close
 
 pytestmark = pytest.mark.gpu
@@ -167,3 +173,140 @@ def test_widened_contraction_matches_the_f32_fold(rt):
     out = rt.alloc(4 * 96 * 4)
     rt.contraction(out, la, lb, F32, F32, *(fh.m(t, **s) for t in ("K, M", "N, K", "M, N, K", "M, N")))
     assert np.array_equal(out.read(np.float32), emu.gemm_rows(a, b, 4, 96, 160, 0, 4, out_t=F32))
+
+
+# ---- contract_element_types.rs: one single-flit contract_outer per engine input type -----------
+# (kernel, element type, packet axis K, accumulator). K is one 32-byte flit of the type.
+ELEMENT_KERNELS = [
+    ("i8_contract", fh.I8, 32, fh.I32),                    # contract_element_types.rs:24-57
+    ("f8e4m3_contract", fh.F8E4M3, 32, F32),               # :59-90
+    ("zero_point_sub_contract", fh.I8, 32, fh.I32),        # :92-128, zero point 3
+    ("i4_contract", fh.I4, 64, fh.I32),                    # :130-163
+    ("f8e5m2_contract", fh.F8E5M2, 32, F32),               # :165-196
+    ("bf16_contract", BF16, 16, F32),                      # :198-232
+]
+ELEM_CC = "1, 1 # 2, 1 # 256"  # [Chip, Cluster, Slice] = m![1], m![1 # 2], m![1 # 256]
+ZERO_POINT = 3
+
+
+def nbytes_of(t, n):
+    return (n + 1) // 2 if t == fh.I4 else n * np.dtype(fh.NP_DTYPE[t]).itemsize
+
+
+def relayout_any(rt, src, sizes, views, t):
+    """relayout() for any element type, 4-bit streams included."""
+    ms = [fh.m(v, **sizes) for v in views]
+    out = rt.upload(np.zeros(nbytes_of(t, mapping_size(ms[-1])), np.uint8))
+    rt.transpose_chain(out, src, t, ms)
+    return out
+
+
+def encode(t, vals):
+    """Integer values in [-8, 8) -> the kernel's storage encoding of them (exact in every type)."""
+    if t == fh.I4:
+        return emu.pack_nibbles(vals)
+    if t == fh.I8:
+        return vals.astype(np.int8)
+    if t == BF16:
+        return emu.f32_to_bf16(vals.astype(np.float32))
+    return emu.f32_to_f8(vals.astype(np.float32), t)
+
+
+def element_kernel_stream(rt, name, t, K, acc_t, x, w):
+    """The seam calls of one contract_element_types kernel on encoded inputs x [A, K], w [R, K]."""
+    s = dict(A=8, R=8, K=K)
+    dm_a, dm_r = f"{ELEM_CC}, A, K", f"{ELEM_CC}, R, K"
+    # to_dm (memory.rs:365-422) of both inputs; the padded cluster and slice cells stay zero
+    x_dm = relayout_any(rt, rt.upload(x), s, ["A, K", dm_a], t)
+    w_dm = relayout_any(rt, rt.upload(w), s, ["R, K", dm_r], t)
+    n_a, n_r = mapping_size(fh.m(dm_a, **s)), mapping_size(fh.m(dm_r, **s))
+    # sub: fetch -> fetch_cast::<D> (the identity map) -> collect -> to_trf, TRF [.., Lane = R, K]
+    w_f = relayout_any(rt, w_dm, s, [dm_r, dm_r], t)
+    w_c = rt.alloc(nbytes_of(t, n_r))
+    rt.map(w_c, t, w_f, t, n_r, fh.op("CAST"))
+    trf = relayout_any(rt, w_c, s, [dm_r, dm_r, dm_r], t)
+    # main: fetch -> fetch_cast (or fetch_zero_point_sub, which widens as it subtracts) -> collect
+    x_f = relayout_any(rt, x_dm, s, [dm_a, dm_a], t)
+    if name == "zero_point_sub_contract":
+        x_c = rt.alloc(n_a * 4)
+        rt.map(x_c, fh.I32, x_f, t, n_a, fh.op("ZERO_POINT_SUB", 0, ZERO_POINT))
+        lhs = relayout_any(rt, x_c, s, [dm_a, dm_a], fh.I32)
+    else:
+        x_c = rt.alloc(nbytes_of(t, n_a))
+        rt.map(x_c, t, x_f, t, n_a, fh.op("CAST"))
+        x_col = relayout_any(rt, x_c, s, [dm_a, dm_a], t)
+        lhs = rt.alloc(n_a * 4)  # contract_outer's map(widen) of the stream operand
+        rt.map(lhs, acc_t, x_col, t, n_a, fh.op("CAST"))
+    rhs = rt.alloc(n_r * 4)      # ... and of the TRF operand
+    rt.map(rhs, acc_t, trf, t, n_r, fh.op("CAST"))
+    # contract_lane: contraction_prewidened onto [Chip, Cluster, Slice, Lane, Time = A, Packet = 1]
+    pre, out_view = f"{ELEM_CC}, R, A, K", f"{ELEM_CC}, R, A"
+    acc_np = np.int32 if acc_t == fh.I32 else np.float32
+    acc = rt.upload(np.full(mapping_size(fh.m(out_view, **s)), 5, acc_np))  # dead cells must become 0
+    rt.contraction(acc, lhs, rhs, acc_t, acc_t, *(fh.m(v, **s) for v in (dm_a, dm_r, pre, out_view)))
+    raw = acc.read(acc_np)
+    # the lane fold's transpose(false) to [.., A, R], commit_trim, commit, to_hbm [Chip, A, R]
+    ct = f"{ELEM_CC}, A, R"
+    out = relayout_any(rt, acc, s, [out_view, ct, ct, ct, "1, A, R"], acc_t)
+    return raw, out.read(acc_np).reshape(8, 8)
+
+
+def element_inputs(rng, t, K, lo, hi):
+    xv, wv = rng.integers(lo, hi, 8 * K), rng.integers(lo, hi, 8 * K)
+    return xv, wv, encode(t, xv), encode(t, wv)
+
+
+@pytest.mark.parametrize("kernel", ELEMENT_KERNELS, ids=[k[0] for k in ELEMENT_KERNELS])
+def test_element_type_kernel_seam_stream(rt, kernel):
+    """Inputs in [-8, 8), as the answer key draws them (its SmallRng stream is Rust's, so the
+    values here are numpy's, of the same distribution): every product and partial sum is a small
+    integer, exact in f32 and i32, so the result is the hand-computed integer matmul
+    out[a, r] = sum_k (x[a, k] - zp) * w[r, k] bit for bit, in any order the kernel folds."""
+    name, t, K, acc_t = kernel
+    rng = np.random.default_rng(42)
+    xv, wv, x, w = element_inputs(rng, t, K, -8, 8)
+    raw, got = element_kernel_stream(rt, name, t, K, acc_t, x, w)
+    zp = ZERO_POINT if name == "zero_point_sub_contract" else 0
+    want = (xv.reshape(8, K).astype(np.int64) - zp) @ wv.reshape(8, K).astype(np.int64).T
+    assert np.array_equal(got, want.astype(got.dtype))
+    # the contraction's own layout [cluster 2, slice 256, R, A]: one live cell, the rest zero
+    cells = raw.reshape(2, 256, 8, 8)
+    assert np.array_equal(cells[0, 0].T, want.astype(got.dtype))
+    assert not cells.reshape(512, 64)[1:].any()
+
+
+@pytest.mark.parametrize("kernel", ELEMENT_KERNELS, ids=[k[0] for k in ELEMENT_KERNELS])
+def test_element_type_kernel_full_range(rt, kernel):
+    """Every code of the type (the NaN codes of the 8-bit floats aside): the integer kernels are
+    exact; bf16 matches the oracle's sequential f32 fold of the widened operands
+    (contraction_prewidened, storage/buf.rs:401-447) to 1e-5; the 8-bit floats run on the f8f6f4
+    MFMA, which multiplies exactly but sums each 64-wide k block at reduced internal precision, and
+    are held to |got - ref| <= 2^-11 * sum_k |x_k * w_k| per cell (the bound of the f8 GEMM tests)."""
+    name, t, K, acc_t = kernel
+    rng = np.random.default_rng(43)
+    if t in (fh.I8, fh.I4):
+        lo, hi = (-128, 128) if t == fh.I8 else (-8, 8)
+        xv, wv, x, w = element_inputs(rng, t, K, lo, hi)
+        zp = ZERO_POINT if name == "zero_point_sub_contract" else 0
+        want = (xv.reshape(8, K).astype(np.int64) - zp) @ wv.reshape(8, K).astype(np.int64).T
+        _, got = element_kernel_stream(rt, name, t, K, acc_t, x, w)
+        assert np.array_equal(got, want.astype(np.int32))
+        return
+    if t == BF16:
+        x = emu.f32_to_bf16(rng.standard_normal(8 * K).astype(np.float32))
+        w = emu.f32_to_bf16(rng.standard_normal(8 * K).astype(np.float32))
+        xf, wf = emu.bf16_to_f32(x), emu.bf16_to_f32(w)
+    else:
+        finite = np.array([c for c in range(256) if np.isfinite(emu.f8_to_f32(np.array([c], np.uint8), t)[0])],
+                          np.uint8)
+        x, w = rng.choice(finite, 8 * K), rng.choice(finite, 8 * K)
+        xf, wf = emu.f8_to_f32(x, t), emu.f8_to_f32(w, t)
+    _, got = element_kernel_stream(rt, name, t, K, acc_t, x, w)
+    maps = (mr.parse(v, dict(A=8, R=8, K=K)) for v in ("A, K", "R, K", "A, R, K", "A, R"))
+    want = emu.contraction(xf, wf, F32, F32, *maps).reshape(8, 8)
+    if t == BF16:
+        close(got, want, rel=1e-5)
+        return
+    bound = 2.0 ** -11 * (np.abs(xf.reshape(8, K).astype(np.float64)) @ np.abs(wf.reshape(8, K).astype(np.float64)).T)
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= bound), f"worst excess {(err - bound).max()}"
