@@ -527,6 +527,18 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
             mx, sm, out = fd.forward(ops, q, ks[c], vs[c], masks[c], mx, sm, out)
         return fd.norm(ops, out, sm)
 
+    # The same four chunks at the engine's own layouts (furiosa_hip/engine_attention.py: every fetch,
+    # switch, collect, commit, cast and vector-engine pass on the padded slice / cluster layouts).
+    import furiosa_hip.engine_attention as ea
+
+    eops = ea.EngineOps(rt)
+    eq = ea.Val(q, fh.BF16, "1, N, G, D")
+    eks = [ea.Val(k, fh.BF16, "1, T, N, D") for k in ks]
+    evs = [ea.Val(v, fh.BF16, "1, T, N, D") for v in vs]
+    emasks = [ea.Val(mk, fh.F32, "1, T") for mk in masks]
+    estate = ea.state(eops)
+    attention_layouts = lambda: ea.chunks(eops, eq, eks, evs, emasks, estate).data
+
     mops = fd.SeamOps(rt, fd.MLP_SIZES)
     x = rt.upload(f32_to_bf16(rng.standard_normal(fd.H, dtype=np.float32)))
     wu, wg = (rt.upload(f32_to_bf16(rng.standard_normal(fd.L * fd.H, dtype=np.float32) / 32)) for _ in range(2))
@@ -577,6 +589,7 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
     res = {}
     for name, fn, o, extra in (
             ("attention_4x512_keys", attention, ops, dict(keys=4 * fd.T)),
+            ("attention_4x512_keys_engine_layouts", attention_layouts, eops, dict(keys=4 * fd.T)),
             ("mlp_silu_h1024_l3072", mlp, mops, {}),
             # HBM floor: the layer's seven weights (15.7 M bf16) and two chunks of K and V read once
             ("layer_step_pos600", layer, sops, dict(hbm_bytes=2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q

@@ -12,6 +12,16 @@ for p in (ROOT, ROOT / "furiosa-opt_amd"):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the HIP library on cuda:0)")
+    config.addinivalue_line("markers", "slow: minutes of CPU work; runs only with FO_SLOW=1 in the environment")
+
+
+def pytest_collection_modifyitems(config, items):
+    if os.environ.get("FO_SLOW") == "1":
+        return
+    skip = pytest.mark.skip(reason="slow (minutes of oracle work); set FO_SLOW=1 to run")
+    for item in items:
+        if "slow" in item.keywords:
+            item.add_marker(skip)
 
 
 @pytest.fixture(scope="session")
