@@ -26,9 +26,11 @@ inline int grid_for(int64_t n) {
 }
 
 // ---- vector register images ------------------------------------------------------------------
-// BYTES bytes of one thread's elements as 32-bit words (BYTES a multiple of 4). Loads and stores
-// are non-temporal 16-byte accesses where BYTES >= 16: streams are touched once.
+// BYTES bytes of one thread's elements as 32-bit words (BYTES a multiple of 4). Loads are
+// non-temporal (streams are read once); stores are plain (a
+// bf16 -> f32 cast with non-temporal 16-byte stores measured 6.3 TB/s against 6.9 with plain ones).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 template <int BYTES>
 struct Regs {
@@ -42,17 +44,16 @@ struct Regs {
         w[4 * k] = v.x, w[4 * k + 1] = v.y, w[4 * k + 2] = v.z, w[4 * k + 3] = v.w;
       }
     } else if constexpr (BYTES == 8) {
-      uint2 v = *(const uint2*)p;
+      u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
       w[0] = v.x, w[1] = v.y;
     } else {
-      w[0] = *(const uint32_t*)p;
+      w[0] = __builtin_nontemporal_load((const uint32_t*)p);
     }
   }
   __device__ __forceinline__ void store(void* p) const {
     if constexpr (BYTES >= 16) {
 #pragma unroll
-      for (int k = 0; k < BYTES / 16; ++k)
-        __builtin_nontemporal_store(u32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]}, (u32x4*)p + k);
+      for (int k = 0; k < BYTES / 16; ++k) *((u32x4*)p + k) = u32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
     } else if constexpr (BYTES == 8) {
       *(uint2*)p = make_uint2(w[0], w[1]);
     } else {
@@ -272,6 +273,25 @@ constexpr int lanes_for() {
   return 16 / (SB < DB ? SB : DB);
 }
 
+// Wave tiles. A wave takes tiles of 64 * V elements; in a tile, lane l holds K = V / C chunks of C
+// consecutive elements, chunk k starting at element (k * 64 + l) * C, with C set so the widest
+// stream moves 16 bytes per lane per chunk. Every load and store instruction of a wave then covers
+// one contiguous run of 64 * C elements. (With lane l holding elements [V l, V l + V) instead, each
+// 16-byte instruction of the wider stream strides across two or four times its span: measured
+// 4.6 TB/s against 6.9 for a bf16 -> f32 cast, 4.5 against 6.7 for an f32 -> u8 tag pass.)
+template <int MAXB>
+constexpr int chunk_for() {
+  return 16 / MAXB;
+}
+__device__ __forceinline__ uint64_t first_tile() { return ((uint64_t)blockIdx.x * kBlock + threadIdx.x) >> 6; }
+__device__ __forceinline__ uint64_t tile_step() { return ((uint64_t)gridDim.x * kBlock) >> 6; }
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// Blocks for n elements in tiles of 64 * V.
+template <int V>
+int tile_grid(uint64_t n) {
+  return grid_for((int64_t)((n + 64 * V - 1) / (64 * V)) * 64);
+}
+
 // map_word over V words at once, with the (wave-uniform) op dispatch hoisted out of the element
 // loop for the common ops; the rest go element by element through map_word.
 template <int V>
@@ -316,23 +336,34 @@ __device__ __forceinline__ void map_words(const uint32_t* w, uint32_t* r, fo_dty
 template <int SB, int DB>
 __global__ void __launch_bounds__(kBlock) k_map_v(void* __restrict__ dst, const void* __restrict__ src, uint64_t n,
                                                   fo_dtype src_t, fo_dtype dst_t, fo_op op) {
-  constexpr int V = lanes_for<SB, DB>();
-  const uint64_t nv = (n + V - 1) / V;
-  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
-    if ((j + 1) * V <= n) {
-      Regs<V * SB> in;
-      Regs<V * DB> out;
-      in.load((const uint8_t*)src + j * V * SB);
+  constexpr int V = lanes_for<SB, DB>(), C = chunk_for<(SB > DB ? SB : DB)>(), K = V / C;
+  const int lane = lane_id();
+  const uint64_t ntiles = (n + 64 * V - 1) / (64 * V);
+  for (uint64_t t = first_tile(); t < ntiles; t += tile_step()) {
+    const uint64_t base = t * 64 * V;
+    if (base + 64 * V <= n) {
       uint32_t w[V], r[V];
 #pragma unroll
-      for (int e = 0; e < V; ++e) w[e] = widen_raw(in.template get<SB>(e), src_t);
+      for (int k = 0; k < K; ++k) {
+        Regs<C * SB> in;
+        in.load((const uint8_t*)src + (base + (uint64_t)(k * 64 + lane) * C) * SB);
+#pragma unroll
+        for (int e = 0; e < C; ++e) w[k * C + e] = widen_raw(in.template get<SB>(e), src_t);
+      }
       map_words<V>(w, r, src_t, dst_t, op);
 #pragma unroll
-      for (int e = 0; e < V; ++e) out.template set<DB>(e, r[e]);
-      out.store((uint8_t*)dst + j * V * DB);
+      for (int k = 0; k < K; ++k) {
+        Regs<C * DB> out;
+#pragma unroll
+        for (int e = 0; e < C; ++e) out.template set<DB>(e, r[k * C + e]);
+        out.store((uint8_t*)dst + (base + (uint64_t)(k * 64 + lane) * C) * DB);
+      }
     } else {
-      for (uint64_t i = j * V; i < n; ++i)
-        store_raw<DB>(dst, i, map_word(widen_raw(load_raw<SB>(src, i), src_t), src_t, dst_t, op));
+      for (int k = 0; k < K; ++k)
+        for (int e = 0; e < C; ++e) {
+          const uint64_t i = base + (uint64_t)(k * 64 + lane) * C + e;
+          if (i < n) store_raw<DB>(dst, i, map_word(widen_raw(load_raw<SB>(src, i), src_t), src_t, dst_t, op));
+        }
     }
   }
 }
@@ -341,23 +372,36 @@ __global__ void __launch_bounds__(kBlock) k_map_v(void* __restrict__ dst, const 
 template <int IB, int OB>
 __global__ void __launch_bounds__(kBlock) k_zip_v(void* __restrict__ dst, const void* __restrict__ a,
                                                   const void* __restrict__ b, uint64_t n, fo_dtype in_t, fo_op op) {
-  constexpr int V = lanes_for<IB, OB>();
-  const uint64_t nv = (n + V - 1) / V;
-  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
-    if ((j + 1) * V <= n) {
-      Regs<V * IB> ra, rb;
-      Regs<V * OB> out;
-      ra.load((const uint8_t*)a + j * V * IB);
-      rb.load((const uint8_t*)b + j * V * IB);
+  constexpr int V = lanes_for<IB, OB>(), C = chunk_for<(IB > OB ? IB : OB)>(), K = V / C;
+  const int lane = lane_id();
+  const uint64_t ntiles = (n + 64 * V - 1) / (64 * V);
+  for (uint64_t t = first_tile(); t < ntiles; t += tile_step()) {
+    const uint64_t base = t * 64 * V;
+    if (base + 64 * V <= n) {
+      Regs<C * IB> ra[K], rb[K];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        out.template set<OB>(e, combine(op, widen_raw(ra.template get<IB>(e), in_t),
-                                        widen_raw(rb.template get<IB>(e), in_t), op.imm1));
-      out.store((uint8_t*)dst + j * V * OB);
+      for (int k = 0; k < K; ++k) {
+        const uint64_t at = base + (uint64_t)(k * 64 + lane) * C;
+        ra[k].load((const uint8_t*)a + at * IB);
+        rb[k].load((const uint8_t*)b + at * IB);
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        Regs<C * OB> out;
+#pragma unroll
+        for (int e = 0; e < C; ++e)
+          out.template set<OB>(e, combine(op, widen_raw(ra[k].template get<IB>(e), in_t),
+                                          widen_raw(rb[k].template get<IB>(e), in_t), op.imm1));
+        out.store((uint8_t*)dst + (base + (uint64_t)(k * 64 + lane) * C) * OB);
+      }
     } else {
-      for (uint64_t i = j * V; i < n; ++i)
-        store_raw<OB>(dst, i, combine(op, widen_raw(load_raw<IB>(a, i), in_t), widen_raw(load_raw<IB>(b, i), in_t),
-                                      op.imm1));
+      for (int k = 0; k < K; ++k)
+        for (int e = 0; e < C; ++e) {
+          const uint64_t i = base + (uint64_t)(k * 64 + lane) * C + e;
+          if (i < n)
+            store_raw<OB>(dst, i, combine(op, widen_raw(load_raw<IB>(a, i), in_t),
+                                          widen_raw(load_raw<IB>(b, i), in_t), op.imm1));
+        }
     }
   }
 }
@@ -397,24 +441,38 @@ __global__ void __launch_bounds__(kBlock) k_zip_w(void* __restrict__ dst, const 
                                                   PreOps pb) {
   constexpr int AB = code_bytes(AC), BB = code_bytes(BC);
   constexpr int MINB = AB < BB ? (AB < OB ? AB : OB) : (BB < OB ? BB : OB);
-  constexpr int V = 16 / MINB;
-  const uint64_t nv = (n + V - 1) / V;
-  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
-    if ((j + 1) * V <= n) {
-      Regs<V * AB> ra;
-      Regs<V * BB> rb;
-      Regs<V * OB> out;
-      ra.load((const uint8_t*)a + j * V * AB);
-      rb.load((const uint8_t*)b + j * V * BB);
+  constexpr int MAXB = AB > BB ? (AB > OB ? AB : OB) : (BB > OB ? BB : OB);
+  constexpr int V = 16 / MINB, C = chunk_for<MAXB>(), K = V / C;
+  const int lane = lane_id();
+  const uint64_t ntiles = (n + 64 * V - 1) / (64 * V);
+  for (uint64_t t = first_tile(); t < ntiles; t += tile_step()) {
+    const uint64_t base = t * 64 * V;
+    if (base + 64 * V <= n) {
+      Regs<C * AB> ra[K];
+      Regs<C * BB> rb[K];
 #pragma unroll
-      for (int e = 0; e < V; ++e)
-        out.template set<OB>(e, combine(op, read_word<PRE>(ra.template get<AB>(e), AC, pa),
-                                        read_word<PRE>(rb.template get<BB>(e), BC, pb), op.imm1));
-      out.store((uint8_t*)dst + j * V * OB);
+      for (int k = 0; k < K; ++k) {
+        const uint64_t at = base + (uint64_t)(k * 64 + lane) * C;
+        ra[k].load((const uint8_t*)a + at * AB);
+        rb[k].load((const uint8_t*)b + at * BB);
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        Regs<C * OB> out;
+#pragma unroll
+        for (int e = 0; e < C; ++e)
+          out.template set<OB>(e, combine(op, read_word<PRE>(ra[k].template get<AB>(e), AC, pa),
+                                          read_word<PRE>(rb[k].template get<BB>(e), BC, pb), op.imm1));
+        out.store((uint8_t*)dst + (base + (uint64_t)(k * 64 + lane) * C) * OB);
+      }
     } else {
-      for (uint64_t i = j * V; i < n; ++i)
-        store_raw<OB>(dst, i, combine(op, read_word<PRE>(load_raw<AB>(a, i), AC, pa),
-                                      read_word<PRE>(load_raw<BB>(b, i), BC, pb), op.imm1));
+      for (int k = 0; k < K; ++k)
+        for (int e = 0; e < C; ++e) {
+          const uint64_t i = base + (uint64_t)(k * 64 + lane) * C + e;
+          if (i < n)
+            store_raw<OB>(dst, i, combine(op, read_word<PRE>(load_raw<AB>(a, i), AC, pa),
+                                          read_word<PRE>(load_raw<BB>(b, i), BC, pb), op.imm1));
+        }
     }
   }
 }
@@ -451,23 +509,25 @@ template <int SC, int DB>
 __global__ void __launch_bounds__(kBlock) k_map_w(void* __restrict__ dst, const void* __restrict__ src, uint64_t n,
                                                   fo_dtype dst_t, fo_op op) {
   constexpr int SB = code_bytes(SC);
-  constexpr int V = 16 / (SB > DB ? SB : DB);
-  const uint64_t nv = (n + V - 1) / V;
-  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
-    if ((j + 1) * V <= n) {
+  constexpr int V = 16 / (SB > DB ? SB : DB);  // one 16-byte chunk of the wider side per lane
+  const int lane = lane_id();
+  const uint64_t ntiles = (n + 64 * V - 1) / (64 * V);
+  for (uint64_t t = first_tile(); t < ntiles; t += tile_step()) {
+    const uint64_t at = t * 64 * V + (uint64_t)lane * V;
+    if (t * 64 * V + 64 * V <= n) {
       Regs<V * SB> in;
       Regs<V * DB> out;
-      in.load((const uint8_t*)src + j * V * SB);
+      in.load((const uint8_t*)src + at * SB);
       uint32_t w[V], r[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) w[e] = widened_word(in.template get<SB>(e), SC);
       map_words<V>(w, r, FO_F32, dst_t, op);
 #pragma unroll
       for (int e = 0; e < V; ++e) out.template set<DB>(e, r[e]);
-      out.store((uint8_t*)dst + j * V * DB);
+      out.store((uint8_t*)dst + at * DB);
     } else {
-      for (uint64_t i = j * V; i < n; ++i)
-        store_raw<DB>(dst, i, map_word(widened_word(load_raw<SB>(src, i), SC), FO_F32, dst_t, op));
+      for (int e = 0; e < V; ++e)
+        if (at + e < n) store_raw<DB>(dst, at + e, map_word(widened_word(load_raw<SB>(src, at + e), SC), FO_F32, dst_t, op));
     }
   }
 }
@@ -583,21 +643,36 @@ __device__ __forceinline__ void tag_bits(const fo_cmp& c, int b, const uint32_t*
 template <bool F32>
 __global__ void __launch_bounds__(kBlock) k_branch_tag_v(uint8_t* __restrict__ dst, const uint32_t* __restrict__ src,
                                                          uint64_t n, Cmps cs) {
-  constexpr int V = 16;
-  const uint64_t nv = (n + V - 1) / V;
-  for (uint64_t j = (uint64_t)blockIdx.x * kBlock + threadIdx.x; j < nv; j += (uint64_t)gridDim.x * kBlock) {
-    if ((j + 1) * V <= n) {
-      Regs<64> in;
-      Regs<16> out;
-      in.load(src + j * V);
+  constexpr int V = 16, C = 4, K = V / C;  // chunks of four words in, four tag bytes out
+  const int lane = lane_id();
+  const uint64_t ntiles = (n + 64 * V - 1) / (64 * V);
+  for (uint64_t t = first_tile(); t < ntiles; t += tile_step()) {
+    const uint64_t base = t * 64 * V;
+    if (base + 64 * V <= n) {
+      uint32_t x[V];
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        Regs<16> in;
+        in.load(src + base + (uint64_t)(k * 64 + lane) * C);
+#pragma unroll
+        for (int e = 0; e < C; ++e) x[k * C + e] = in.w[e];
+      }
       uint32_t id[V] = {};
 #pragma unroll
-      for (int b = 0; b < 4; ++b) tag_bits<V, F32>(cs.c[b], b, in.w, id);
+      for (int b = 0; b < 4; ++b) tag_bits<V, F32>(cs.c[b], b, x, id);
 #pragma unroll
-      for (int e = 0; e < V; ++e) out.template set<1>(e, id[e]);
-      out.store(dst + j * V);
+      for (int k = 0; k < K; ++k) {
+        Regs<4> out;
+#pragma unroll
+        for (int e = 0; e < C; ++e) out.template set<1>(e, id[k * C + e]);
+        out.store(dst + base + (uint64_t)(k * 64 + lane) * C);
+      }
     } else {
-      for (uint64_t i = j * V; i < n; ++i) dst[i] = (uint8_t)tag_of(cs, src[i], F32);
+      for (int k = 0; k < K; ++k)
+        for (int e = 0; e < C; ++e) {
+          const uint64_t i = base + (uint64_t)(k * 64 + lane) * C + e;
+          if (i < n) dst[i] = (uint8_t)tag_of(cs, src[i], F32);
+        }
     }
   }
 }
@@ -706,15 +781,13 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <int SB, int DB>
 void map_launch(hipStream_t s, void* dst, const void* src, uint64_t n, fo_dtype src_t, fo_dtype dst_t, const fo_op& op) {
-  constexpr int V = lanes_for<SB, DB>();
-  hipLaunchKernelGGL((k_map_v<SB, DB>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, src, n,
+  hipLaunchKernelGGL((k_map_v<SB, DB>), dim3(tile_grid<lanes_for<SB, DB>()>(n)), dim3(kBlock), 0, s, dst, src, n,
                      src_t, dst_t, op);
 }
 
 template <int IB, int OB>
 void zip_launch(hipStream_t s, void* dst, const void* a, const void* b, uint64_t n, fo_dtype in_t, const fo_op& op) {
-  constexpr int V = lanes_for<IB, OB>();
-  hipLaunchKernelGGL((k_zip_v<IB, OB>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, a, b, n,
+  hipLaunchKernelGGL((k_zip_v<IB, OB>), dim3(tile_grid<lanes_for<IB, OB>()>(n)), dim3(kBlock), 0, s, dst, a, b, n,
                      in_t, op);
 }
 
@@ -822,7 +895,7 @@ void launch_zip_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* a,
 #define FO_ZIPW_CASE(A, B)                                                                                     \
   if (a_code == A && b_code == B) {                                                                            \
     constexpr int MINB = code_bytes(A) < code_bytes(B) ? code_bytes(A) : code_bytes(B);                        \
-    const dim3 grid(grid_for((int64_t)((n + 16 / MINB - 1) / (16 / MINB))));                                  \
+    const dim3 grid(tile_grid<16 / MINB>(n));                                                                 \
     if (a_pre.n != 0 || b_pre.n != 0)                                                                          \
       hipLaunchKernelGGL((k_zip_w<A, B, 4, true>), grid, dim3(kBlock), 0, s, dst, a, b, n, op, a_pre, b_pre);  \
     else                                                                                                       \
@@ -867,7 +940,7 @@ void launch_map_widened(hipStream_t s, void* dst, fo_dtype dst_t, const void* sr
 #define FO_MAPW_CASE(SC, DB)                                                                                   \
   if (src_code == SC && (int)dtype_bytes(dst_t) == DB) {                                                       \
     constexpr int V = 16 / (code_bytes(SC) > DB ? code_bytes(SC) : DB);                                        \
-    hipLaunchKernelGGL((k_map_w<SC, DB>), dim3(grid_for((int64_t)((n + V - 1) / V))), dim3(kBlock), 0, s, dst, \
+    hipLaunchKernelGGL((k_map_w<SC, DB>), dim3(tile_grid<V>(n)), dim3(kBlock), 0, s, dst,                      \
                        src, n, dst_t, op);                                                                     \
     FO_HIP(hipGetLastError());                                                                                 \
     return;                                                                                                    \
@@ -899,10 +972,10 @@ void launch_branch_tag(hipStream_t s, uint8_t* dst, const void* src, fo_dtype t,
     cs.c[b] = cmps[b];
   }
   if (t == FO_F32)
-    hipLaunchKernelGGL(k_branch_tag_v<true>, dim3(grid_for((int64_t)((n + 15) / 16))), dim3(kBlock), 0, s, dst,
+    hipLaunchKernelGGL(k_branch_tag_v<true>, dim3(tile_grid<16>(n)), dim3(kBlock), 0, s, dst,
                        (const uint32_t*)src, n, cs);
   else
-    hipLaunchKernelGGL(k_branch_tag_v<false>, dim3(grid_for((int64_t)((n + 15) / 16))), dim3(kBlock), 0, s, dst,
+    hipLaunchKernelGGL(k_branch_tag_v<false>, dim3(tile_grid<16>(n)), dim3(kBlock), 0, s, dst,
                        (const uint32_t*)src, n, cs);
   FO_HIP(hipGetLastError());
 }
