@@ -562,6 +562,11 @@ __global__ void __launch_bounds__(kBlock) k_gather(T* __restrict__ dst, const T*
 // 16-byte form: the innermost payload wheel is contiguous in both memories and a whole number of
 // V-element chunks, so payload positions c*V .. c*V+V-1 are adjacent on both sides. Thread (r, c)
 // moves chunk c of slot r; consecutive threads take consecutive chunks of one row.
+// The scatter's threads move kChunkRuns chunks a grid stride apart, each chunk's data read issued
+// with its index read (it does not depend on it), the winner checks and writes after all of them
+// (measured 21.6 -> 21.0 us for 131072 rows of 256 bytes; the same for the gather, whose data read
+// waits for the index, measured 22.6 -> 27.0 us and is not used).
+constexpr int kChunkRuns = 4;
 template <int V>
 __global__ void __launch_bounds__(kBlock) k_gather_vec(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src,
                                                        int64_t eb, const int32_t* __restrict__ idx, uint32_t total,
@@ -588,13 +593,25 @@ __global__ void __launch_bounds__(kBlock) k_scatter_vec(uint8_t* __restrict__ ds
                                                         FastDiv cdiv, uint32_t keys, uint32_t axis_size, int32_t div,
                                                         Wheels<1> ws, Wheels<1> wd) {
   typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
-  for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
-    uint32_t k = cdiv.div(t), c = t - k * cdiv.d;
-    int32_t a = decode_index(idx, k, div, axis_size);
-    if (a < 0 || win[a] != (tag | k)) continue;
-    const uint32_t p = c * V;
-    *(vec_t*)(dst + wheel_offset(wd, p * axis_size + (uint32_t)a) * eb) =
-        *(const vec_t*)(src + wheel_offset(ws, p * keys + k) * eb);
+  constexpr int U = kChunkRuns;  // as in k_gather_vec; the data read does not wait for the index
+  const uint64_t stride = (uint64_t)gridDim.x * kBlock;
+  for (uint64_t t0 = (uint64_t)blockIdx.x * kBlock + threadIdx.x; t0 < total; t0 += U * stride) {
+    uint32_t k[U], c[U];
+    int32_t a[U];
+    vec_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint64_t t = t0 + u * stride;
+      const uint32_t tt = t < total ? (uint32_t)t : 0u;
+      k[u] = cdiv.div(tt);
+      c[u] = tt - k[u] * cdiv.d;
+      a[u] = t < total ? decode_index(idx, k[u], div, axis_size) : -1;
+      if (t < total) v[u] = *(const vec_t*)(src + wheel_offset(ws, c[u] * V * keys + k[u]) * eb);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (a[u] >= 0 && win[a[u]] == (tag | k[u]))
+        *(vec_t*)(dst + wheel_offset(wd, c[u] * V * axis_size + (uint32_t)a[u]) * eb) = v[u];
   }
 }
 
@@ -2000,7 +2017,7 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
   if (((uintptr_t)dst | (uintptr_t)src) % 16 == 0 && payload_vec_ok(ws, ws_slot_wheels, V) &&
       payload_vec_ok(wd, wd_slot_wheels, V)) {
     const uint32_t nch = (uint32_t)(payload / V), total = (uint32_t)(nch * keys);
-    dim3 g(grid_for(total)), b(kBlock);
+    dim3 g(grid_for(((int64_t)total + kChunkRuns - 1) / kChunkRuns)), b(kBlock);
     const FastDiv cdiv(nch);
     if (V == 8)
       hipLaunchKernelGGL(k_scatter_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, tag,
