@@ -544,6 +544,16 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
     wu, wg = (rt.upload(f32_to_bf16(rng.standard_normal(fd.L * fd.H, dtype=np.float32) / 32)) for _ in range(2))
     wd = rt.upload(f32_to_bf16(rng.standard_normal(fd.H * fd.L, dtype=np.float32) / 55))
     mlp = lambda: fd.mlp(mops, x, wu, wg, wd)
+    # The decoder's RMSNorm and MLP at the engine's own layouts (furiosa_hip/engine_mlp.py: SliceP4,
+    # SliceUG, SliceD and their switches), from the input already on SliceP4.
+    import furiosa_hip.engine_mlp as em
+
+    emops = em.ops(rt)
+    ex_dm = emops.move(ea.Val(x, fh.BF16, "1, H"), f"{em.P4}, H", True)
+    eg = ea.Val(rt.upload(np.full(fd.H, 0x3F80, np.uint16)), fh.BF16, "1, H")
+    ewu, ewg = ea.Val(wu, fh.BF16, "1, L, H"), ea.Val(wg, fh.BF16, "1, L, H")
+    ewd = ea.Val(wd, fh.BF16, "1, H, L")
+    rms_mlp_layouts = lambda: em.mlp(emops, em.rmsnorm(emops, ex_dm, eg), ewu, ewg, ewd).data
     # One whole layer of the decode step (projection, attention over two chunks, decoder) and the
     # final layer, at position T + 88, weights and caches resident, masks and RoPE row hoisted.
     sops = fd.SeamOps(rt, fd.STEP_SIZES)
@@ -591,6 +601,7 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
             ("attention_4x512_keys", attention, ops, dict(keys=4 * fd.T)),
             ("attention_4x512_keys_engine_layouts", attention_layouts, eops, dict(keys=4 * fd.T)),
             ("mlp_silu_h1024_l3072", mlp, mops, {}),
+            ("rmsnorm_mlp_engine_layouts", rms_mlp_layouts, emops, {}),
             # HBM floor: the layer's seven weights (15.7 M bf16) and two chunks of K and V read once
             ("layer_step_pos600", layer, sops, dict(hbm_bytes=2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q
                                                                    + 3 * fd.L * fd.H) + 2 * 2 * fd.T * fd.N * fd.D * 2)),

@@ -366,6 +366,14 @@ class Buffer:
         """Runs whatever the runtime still owes this buffer (zero fill, deferred cast or relayout)."""
         _check(_lib.fo_buffer_flush(self.rt.h, self.h))
 
+    def clone(self) -> "Buffer":
+        """Storage: Clone, and Backend::reshape: a device copy of the same bytes in a new buffer."""
+        h = _P()
+        _check(_lib.fo_buffer_clone(self.rt.h, self.h, C.byref(h)))
+        b = Buffer.__new__(Buffer)
+        b.h, b.rt, b.nbytes = h, self.rt, self.nbytes
+        return b
+
     def read(self, dtype, count: Optional[int] = None) -> np.ndarray:
         dt = np.dtype(NP_DTYPE[dtype] if isinstance(dtype, int) else dtype)
         n = self.nbytes // dt.itemsize if count is None else count

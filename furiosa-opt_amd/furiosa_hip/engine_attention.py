@@ -129,6 +129,12 @@ class EngineOps:
     def zero_tag(self, view):
         return Val(self._alloc(view, U8), U8, view)
 
+    def reshape(self, x, view):
+        """Backend::reshape (storage/buf.rs:580-585): the same wire image under mapping `view`, which
+        the caller has checked has x's size."""
+        self.calls += 1
+        return Val(x.data.clone(), x.t, view)
+
     def slots(self, x, tag, name, const=None, port=None, flags=0):
         self.calls += 1
         out = self._alloc(x.view, x.t)

@@ -326,6 +326,11 @@ def relayout_offsets(src: dict, dst: dict) -> Tuple[np.ndarray, np.ndarray]:
     Returns `(live, src_pos)` over dst wire positions: `live[p]` is the dst liveness
     (`iter_positions`), `src_pos[p]` the src wire position read for a live `p`.
     """
+    # Every src axis must be covered by the dst stream (buf.rs:280-281: `sequence(...)` under Carve
+    # "expect"s it); a dst without one of src's symbols would leave its coordinate undetermined.
+    missing = set(symbols(src)) - set(symbols(dst))
+    if missing:
+        raise ValueError(f"relayout: src axes {sorted(missing)} are not covered by the dst stream")
     dn = size(dst)
     dc, dsn = cells(dst, np.arange(dn, dtype=np.int64))
     live = dsn == LIVE

@@ -56,6 +56,11 @@ class CpuEngineOps:
     def zero_tag(self, view):
         return Val(np.zeros(self.size(view), np.uint8), fh.U8, view)
 
+    def reshape(self, x, view):
+        assert self.size(view) == self.size(x.view), "reshape keeps the size"
+        self.calls += 1
+        return Val(np.array(x.data, copy=True), x.t, view)
+
     def slots(self, x, tag, name, const=None, port=None, flags=0):
         self.calls += 1
         regs = [ALL] if const is not None else []

@@ -51,6 +51,10 @@ def test_unconsumed_memory_is_rejected():
     # a src axis the dst stream never reads (SequencerError::Unconsumed)
     with pytest.raises(fh.FoError, match="not covered"):
         fh.sequence(fh.m("A, B", A=4, B=4), fh.m("A", A=4, B=4))
+    # the oracle's transpose refuses it the same way (buf.rs:280-281 expects the src covered)
+    s = dict(A=4, B=4)
+    with pytest.raises(ValueError, match="not covered"):
+        mr.relayout_offsets(mr.parse("A, B", s), mr.parse("A", s))
 
 
 PAIRS = [
