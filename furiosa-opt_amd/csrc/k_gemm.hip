@@ -965,8 +965,8 @@ void gemm_launch_cfg(hipStream_t s, const GemmDesc& d, void* c, const void* a, c
 }
 
 // Tile choice: 256x256 when the problem is large -- four waves of 128x128 in 16x16 MFMA tiles
-// (k_gemm4) for bf16 and i8 with plain outputs, eight waves of 128x64 in 32x32 tiles (k_gemm) for
-// the 8-bit floats and the W8A8 dequant -- and 128x128 otherwise. FO_GEMM_TILE overrides it for
+// (k_gemm4) for bf16 and i8 (plain outputs and the W8A8 dequant), eight waves of 128x64 in 32x32
+// tiles (k_gemm) for the 8-bit floats -- and 128x128 otherwise. FO_GEMM_TILE overrides it for
 // measurement: 128, 256 (k_gemm, 4 waves of 128x128), 2568 (8 waves of 128x64), 25616 (16 waves)
 // or 4128 (k_gemm4).
 template <int KIND, int OUT>
@@ -982,9 +982,10 @@ void gemm_launch(hipStream_t s, const GemmDesc& d, void* c, const void* a, const
   // 64x64 exceed 128 VGPRs and spill (1850 TFLOP/s against 367); i8 (the W8A8 config) 2175-2186
   // against 2135-2142 TOP/s with the refill split in parts.
   constexpr bool k16 = (KIND == kBf16 || KIND == kI8) && OUT <= 4;  // kinds with a 16x16 MFMA form here
-  // The W8A8 dequant measured 2190 TOP/s on the eight-wave kernel against 2112 on the four-wave one
-  // (same box); bf16 1258-1273 against 1319 TFLOP/s, i8 -> i32 1660 against 1930 TOP/s.
-  constexpr bool k16_default = k16 && OUT != 4;
+  // Four waves of 128x128 for every kind with a 16x16 form: bf16 1258-1273 (eight-wave) against 1319
+  // TFLOP/s, i8 -> i32 1660 against 1930 TOP/s, the W8A8 dequant 2432-2442 against 2490 TOP/s (same
+  // boxes; before the four-wave kernel's refill interleave the W8A8 measured the other way round).
+  constexpr bool k16_default = k16;
   int choice = forced ? forced : (tiles256 >= 128 ? (k16_default ? 4128 : 2568) : 128);
   if constexpr (k16) {
     // four waves of 128x128 (16x16 MFMA tiles), 128-byte stages, A and B double-buffered. (A

@@ -429,6 +429,21 @@ def test_w8a8_config_sampled_rows(rt):
     assert np.array_equal(colsum, w.reshape(n, k).astype(np.int64) @ asum)
 
 
+def test_w8a8_ragged_four_wave_tiles(rt):
+    """Large enough for the four-wave 256x256 tiles, with M and N not multiples of 256 (partial
+    tiles at both edges): every accumulator and output exact."""
+    m, n, k = 2056, 4000, 512
+    rng = np.random.default_rng(37)
+    a = rng.integers(-127, 128, m * k, dtype=np.int8)
+    w = rng.integers(-127, 128, n * k, dtype=np.int8)
+    scale = rng.uniform(1e-3, 1e-2, n).astype(np.float32)
+    out, accb = rt.alloc(m * n * 2), rt.alloc(m * n * 4)
+    rt.gemm_w8a8_dequant(out, accb, rt.upload(a), rt.upload(w), rt.upload(scale), m, n, k)
+    want, acc = emu.w8a8(a, w, scale, m, n, k)
+    assert np.array_equal(accb.read(np.int32), acc)
+    assert np.array_equal(out.read(np.uint16), want)
+
+
 # ---- mapped GEMM (configs[1]) through the seam -------------------------------------------------------
 
 
