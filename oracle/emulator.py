@@ -401,15 +401,21 @@ def _decode(index: np.ndarray, n: int, div: int, axis_size: int) -> np.ndarray:
 
 
 def scatter(dst, src, index, elem_bytes: int, src_m: dict, key_m: dict, dst_m: dict, idx_m: dict, scaled: bool):
-    """BufStorage::scatter: payload = Src / Key, the indexed dst axis the first live axis of
-    Dst / payload; dst[(p, index[k])] = src[(p, k)] in serial (payload, key) order, so the last
-    key of a repeated index wins."""
+    """BufStorage::scatter (buf.rs:485-520): payload = Src / Key with its outer padding peeled
+    (interior padding kept), the indexed dst axis the first live axis of Dst / payload;
+    dst[(p, index[k])] = src[(p, k)] in serial (payload, key) order, so the last key of a repeated
+    index wins. A scaled index is a byte offset in blocks of the payload's full size, interior
+    padding included (decode_stride, buf.rs:816-822). A payload position inside an interior pad
+    repeats the writes of the pad's live position (its wheel has memory stride 0 on both sides),
+    so it is skipped: the result is the same."""
     payload = mr.remove_padding(mr.carve(src_m, key_m))
     axis = mr.first_axis(mr.carve(dst_m, payload))
     ks, asz, ps = mr.size(key_m), mr.size(axis), mr.size(payload)
     dec = _decode(index, ks, ps * elem_bytes if scaled else 1, asz)
-    src_off = mr.stream_offsets(src_m, mr.pair(payload, key_m)).reshape(ps, ks)
-    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, axis)).reshape(ps, asz)
+    src_off = mr.stream_offsets(src_m, mr.pair(payload, key_m), padded=True).reshape(ps, ks)
+    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, axis), padded=True).reshape(ps, asz)
+    live = src_off[:, 0] >= 0
+    src_off, dst_off = src_off[live], dst_off[live]
     out = np.array(dst, copy=True)
     for k in range(ks):  # ascending k: a later key overwrites an earlier one with the same index
         out[dst_off[:, dec[k]]] = np.asarray(src)[src_off[:, k]]
@@ -423,8 +429,10 @@ def gather(dst, src, index, elem_bytes: int, src_m: dict, dst_m: dict, idx_m: di
     axis = mr.first_axis(mr.carve(src_m, payload))
     rs, asz, ps = mr.size(idx_m), mr.size(axis), mr.size(payload)
     dec = _decode(index, rs, ps * elem_bytes if scaled else 1, asz)
-    src_off = mr.stream_offsets(src_m, mr.pair(payload, axis)).reshape(ps, asz)
-    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, idx_m)).reshape(ps, rs)
+    src_off = mr.stream_offsets(src_m, mr.pair(payload, axis), padded=True).reshape(ps, asz)
+    dst_off = mr.stream_offsets(dst_m, mr.pair(payload, idx_m), padded=True).reshape(ps, rs)
+    live = src_off[:, 0] >= 0  # interior payload padding: repeats of live positions, as in scatter
+    src_off, dst_off = src_off[live], dst_off[live]
     out = np.array(dst, copy=True)
     out[dst_off] = np.asarray(src)[src_off[:, dec]]
     return out

@@ -45,6 +45,27 @@ class CpuEngineOps:
         self.calls += 1
         dst.data[:] = emu.transpose(dst.data, x.data, self.view(x.view), self.view(dst.view))
 
+    def zeros(self, view, t):
+        return Val(np.zeros(self.size(view), fh.NP_DTYPE[t]), t, view)
+
+    def read_tile(self, x, view, offset, dst=None, broadcast=False):
+        self.calls += 1
+        dst = dst or view
+        out = np.zeros(self.size(dst), fh.NP_DTYPE[x.t])
+        return Val(emu.transpose(out, x.data, self.view(view), self.view(dst), src_map=self.view(x.view),
+                                 src_offset=offset), x.t, dst)
+
+    def write_tile(self, dst, x, view, offset):
+        self.calls += 1
+        dst.data[:] = emu.transpose(dst.data, x.data, self.view(x.view), self.view(view), dst_map=self.view(dst.view),
+                                    dst_offset=offset)
+
+    def scatter(self, dst, x, index, key="1"):
+        self.calls += 1
+        k = self.view(key)
+        dst.data[:] = emu.scatter(dst.data, x.data, index.data, np.dtype(fh.NP_DTYPE[x.t]).itemsize, self.view(x.view),
+                                  k, self.view(dst.view), self.view(index.view), True)
+
     def map(self, x, dst_t, name, flags=0, imm=0):
         self.calls += 1
         return Val(emu.map_(x.data, x.t, dst_t, fh.OP[name], flags, _bits(imm)), dst_t, x.view)

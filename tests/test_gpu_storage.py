@@ -994,6 +994,27 @@ def test_scatter_repeats_last_key_wins(rt, dt, npt):
     assert np.array_equal(out.read(npt), want)
 
 
+@pytest.mark.parametrize("off", [0, 5 * 8 * 128 * 2, 37 * 8 * 128 * 2, 3 * 8 * 32 * 128 * 2])
+def test_scatter_from_slice_placement_with_interior_pad(rt, off):
+    """The K / V cache row scatter of rope.rs:175 and projection.rs:111 at its own layout: src
+    [Chip, Cluster 1 # 2, N, 1 # 32, D], key m![1], dst [Chip, T, N, D]; the payload keeps its
+    interior pad, so the byte offset counts blocks of N * 32 * D elements (buf.rs:492-498, 816-822)."""
+    s = dict(N=8, D=128, T=512)
+    rng = np.random.default_rng(46)
+    src_t = "1, 1 # 2, N, 1 # 32, D"
+    data = rng.integers(0, 60000, 2 * 8 * 32 * 128).astype(np.uint16)
+    cache = rng.integers(0, 60000, 512 * 8 * 128).astype(np.uint16)
+    maps = [mr.parse(t, s) for t in (src_t, "1", "1, T, N, D", "1, 1")]
+    want = emu.scatter(cache, data, np.array([off], np.int32), 2, *maps, scaled=True)
+    out = rt.upload(cache)
+    rt.scatter(out, rt.upload(data), rt.upload(np.array([off], np.int32)), BF16,
+               *(fh.m(t, **s) for t in (src_t, "1", "1, T, N, D", "1, 1")), scaled=True)
+    got = out.read(np.uint16)
+    assert np.array_equal(got, want)
+    row = off // (8 * 32 * 128 * 2)
+    assert np.array_equal(got.reshape(512, 8, 128)[row], data.reshape(2, 8, 32, 128)[0, :, 0])
+
+
 GATHER_CASES = [
     # gather_minimal / gather_unaligned (scatter_gather.rs:72-98): rows of a [K, D] table
     (dict(K=512, D=128, G=512), "K, D", "G, D", "G", 512, 128 * 2),
