@@ -572,6 +572,26 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
     fops = fd.SeamOps(rt, fd.STEP_SIZES)
     lm, g = up(fd.WP * fd.H, 1 / 32), ones(fd.H)
     final = lambda: fd.final_layer(fops, xs, g, lm)
+    # The same step's kernels at the engine's own layouts (furiosa_hip/engine_step.py), HBM in and
+    # out: projection with both cache rows, decoder, final layer with the 19-tile lm_head.
+    import furiosa_hip.engine_step as es
+
+    hv = lambda b, view, t=fh.BF16: ea.Val(b, t, view)
+    pe, de, fe = es.ops(rt), es.ops(rt), es.ops(rt)
+    e_kc, e_vc = (hv(up(fd.T * fd.N * fd.D, 1.0), "1, T, N, D") for _ in range(2))
+    e_q = hv(rt.alloc(fd.Q * 2), "1, N, G, D")
+    e_off = hv(rt.upload(np.array([(pos % fd.T) * fd.ROW_STRIDE_ND], np.int32)), "1, 1", fh.I32)
+    projection_layouts = lambda: es.projection(
+        pe, hv(xs, "1, H"), hv(lw["q"], "1, Q, H"), hv(lw["k"], "1, P, H"), hv(lw["v"], "1, P, H"),
+        hv(lw["input_norm"], "1, H"), hv(lw["q_norm"], "1, D"), hv(lw["k_norm"], "1, D"), e_off, hv(cos, "1, D"),
+        hv(sin, "1, D"), e_kc, e_vc, e_q)
+    e_sum = hv(rt.upload(rng.uniform(0.5, 4.0, fd.N * fd.G).astype(np.float32)), "1, N, G", fh.F32)
+    e_att, e_rx = hv(up(fd.Q, 1.0), "1, N, G, D"), hv(up(fd.H, 1.0), "1, H")
+    decoder_layouts = lambda: es.decoder(de, e_att, e_sum, e_rx, hv(lw["o"], "1, H, Q"), hv(lw["post_norm"], "1, H"),
+                                         hv(lw["up"], "1, L, H"), hv(lw["gate"], "1, L, H"), hv(lw["down"], "1, H, L"))
+    e_logits = hv(rt.alloc(fd.WP * 2), "1, Wp")
+    final_layouts = lambda: es.final_layer(fe, hv(xs, "1, H"), hv(g, "1, H"), hv(lm, "1, Wp / 8192, Wp % 8192, H"),
+                                           e_logits)
 
     # A whole token of the Qwen3-0.6B-shaped model (28 layers, tied 151936-row embedding) through
     # the pipeline at position T + 88, every layer's caches holding two chunks.
@@ -606,6 +626,9 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
             ("layer_step_pos600", layer, sops, dict(hbm_bytes=2 * (fd.Q * fd.H + 2 * fd.P * fd.H + fd.H * fd.Q
                                                                    + 3 * fd.L * fd.H) + 2 * 2 * fd.T * fd.N * fd.D * 2)),
             ("final_layer_wp155648", final, fops, dict(hbm_bytes=2 * fd.WP * fd.H)),
+            ("projection_engine_layouts", projection_layouts, pe, {}),
+            ("decoder_engine_layouts", decoder_layouts, de, {}),
+            ("final_layer_engine_layouts", final_layouts, fe, dict(hbm_bytes=2 * fd.WP * fd.H)),
             ("token_28_layers_pos600", token, pops, dict(hbm_bytes=token_bytes)),
             ("token_28_layers_pos600_graph", token_graph, gops, dict(hbm_bytes=token_bytes, recorded=True))):
         if name.endswith("_graph") and not graph:

@@ -731,6 +731,28 @@ std::vector<fm::Wheel> live_only(const std::vector<fm::Wheel>& ws) {
   return out;
 }
 
+// Adjacent fully live wheels that are contiguous in every memory (inner stride x inner size = outer
+// stride) as one wheel: the same positions in the same order, fewer digits to decode. A residue
+// split by the out axes of a pre-reduce mapping (H / 32, then H % 32 past a lane axis) comes back
+// whole, and the kernels' unit-stride forms apply to it.
+std::vector<fm::Wheel> merge_contiguous(const std::vector<fm::Wheel>& ws) {
+  std::vector<fm::Wheel> out;
+  for (const auto& w : ws) {
+    if (!out.empty()) {
+      fm::Wheel& in = out.back();
+      bool ok = in.live == in.size && w.live == w.size && in.stride.size() == w.stride.size();
+      for (size_t k = 0; ok && k < w.stride.size(); ++k) ok = in.stride[k] * in.size == w.stride[k];
+      if (ok) {
+        in.size *= w.size;
+        in.live = in.size;
+        continue;
+      }
+    }
+    out.push_back(w);
+  }
+  return out;
+}
+
 std::vector<fm::Wheel> part(const fm::Joint& j, int p) {
   std::vector<fm::Wheel> out;
   for (auto& w : j.wheels)
@@ -2042,7 +2064,8 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
       fm::Factors pre = flat(pre_reduce, "pre_reduce"), o = flat(out_map, "out_map");
       fm::Factors contracted = fm::carve(pre, o);
       fm::Joint j = fm::sequence({l, r}, {o, contracted}, fm::Mode::Read);
-      return Plan{fm::size(l), fm::size(r), fm::size(o), part(j, 0), live_only(part(j, 1))};
+      return Plan{fm::size(l), fm::size(r), fm::size(o), merge_contiguous(part(j, 0)),
+                  merge_contiguous(live_only(part(j, 1)))};
     });
     const std::vector<fm::Wheel>& ow = plan.ow;
     const std::vector<fm::Wheel>& rw = plan.rw;
@@ -2135,16 +2158,17 @@ void contraction_impl(fo_runtime* rt, fo_buffer* out, const fo_buffer* lhs, cons
         }
       }
       if (x_narrowed) check_buf(wl.src, "lhs");
-      // Batched dot products (every out wheel reads both operands, or neither: padding): one lane
-      // folds each cell's two rows in k order.
+      // Batched dot products (out wheels read both operands, or the rhs only, or neither: padding;
+      // a batch of GEMVs such as a lane-broadcast TRF contraction per slice): one lane folds each
+      // cell's two rows in k order.
       const bool rows_repeat_only =
           std::all_of(mw.begin(), mw.end(), [](const Part& p) { return p.w.stride[0] == 0 && p.w.stride[1] == 0; });
-      if (unit_k && rows_repeat_only && nw.empty() && !bw.empty()) {
+      if (unit_k && rows_repeat_only && !bw.empty()) {
         const int64_t K = rw[0].size;
         if (max_live_offset(ow, 0) + K - 1 < lhs_len && max_live_offset(ow, 1) + K - 1 < rhs_len) {
           const int64_t eb = dtype_bytes(ct);
           bool vec = ((uintptr_t)L % 16) == 0 && ((uintptr_t)R % 16) == 0;
-          for (auto& p : bw) vec &= (p.w.stride[0] * eb) % 16 == 0 && (p.w.stride[1] * eb) % 16 == 0;
+          for (auto& w : ow) vec &= (w.stride[0] * eb) % 16 == 0 && (w.stride[1] * eb) % 16 == 0;
           const int mem[2] = {0, 1};
           if (launch_contraction_dot(rt->stream, O, L, R, ct, co, out_count, to_desc<2>(ow, mem), K, vec)) return;
         }
