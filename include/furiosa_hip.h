@@ -381,7 +381,10 @@ int32_t fo_transmute(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
  * Dst / payload (scatter_params, backend/op_prep.rs:45-54), writes
  *   dst[(p, index[k] / div)] = src[(p, k)]
  * for every payload position p and key position k; div = payload size * element bytes when
- * `scaled` (byte offsets of payload blocks), else 1. A repeated index keeps the last key's value,
+ * `scaled` (byte offsets of payload blocks; remove_padding peels only the outer padding, so an
+ * interior pad such as a [N, 1 # 32, D] slice placement's counts in that size), else 1. A pad
+ * position of the payload that no memory cell backs repeats the writes of its live position; a
+ * pad that memory backs is FO_ERR_INVALID. A repeated index keeps the last key's value,
  * as the serial loop does. `index` holds i32, at least |Key| cells. Indices are checked on the
  * device: one that is negative or past the axis is skipped (the valid ones are still written) and
  * the next fo_runtime_synchronize or fo_read on this runtime returns FO_ERR_INVALID (the
@@ -395,7 +398,8 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
  * (gather_params, backend/op_prep.rs:78-89), writes
  *   dst[(p, r)] = src[(p, index[r] / div)]
  * for every payload position p and index cell r (r walks the index tensor's mapping); dst cells
- * outside that stream keep their values. Same index decoding and (deferred) errors as fo_scatter. */
+ * outside that stream keep their values. Same index decoding, payload padding rule and (deferred)
+ * errors as fo_scatter. */
 int32_t fo_gather(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const fo_buffer* index, fo_dtype t,
                   const char* src_map, const char* dst_map, const char* idx_map, int32_t scaled);
 
