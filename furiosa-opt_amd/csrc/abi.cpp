@@ -224,6 +224,7 @@ struct RunScope {
 
 void materialize(const fo_buffer* b);
 void fill_pending(fo_runtime* rt, const fo_buffer* b);
+void mark_filled(fo_buffer* b);
 
 // One op's trace span: events recorded on the runtime's stream before and after its launches.
 struct TraceScope {
@@ -259,8 +260,24 @@ void run_deferred(const std::vector<WidenRecord>& rs) {
       launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, 4, 0, 0, (int64_t)r.n, r.wheels);
     } else if (is_xpose(r)) {
       TraceScope span(r.rt, "transpose");  // the recorded op's own span, when it runs
-      fill_pending(r.rt, r.dst);            // cells the views leave dead read as zero
-      launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, dtype_bytes(r.xt), 0, 0, r.count, r.wheels);
+      fo_buffer* d = const_cast<fo_buffer*>(r.dst);
+      const int64_t eb = dtype_bytes(r.xt);
+      const uint64_t cap = (d->capacity + 15) & ~15ull;  // the bytes a zero fill would clear
+      if (d->zero_pending && cap % (uint64_t)eb == 0 && cap / (uint64_t)eb < (1ull << 31)) {
+        // A fresh storage the views leave partly dead (a padded slice or cluster layout): one pass
+        // writes the live cells from the source and zero everywhere else the fill would have,
+        // instead of the fill and then the relayout.
+        Chain c;
+        c.n = 1;
+        c.zero_unwritten = 1;
+        c.total = (uint32_t)(cap / (uint64_t)eb);
+        c.step[0] = ChainStep{r.wheels, 0, (uint32_t)r.count};
+        mark_filled(d);
+        launch_relayout_chain(r.rt->stream, d->ptr, r.src->ptr, eb, c);
+      } else {
+        fill_pending(r.rt, r.dst);  // cells the views leave dead read as zero
+        launch_relayout(r.rt->stream, r.dst->ptr, r.src->ptr, eb, 0, 0, r.count, r.wheels);
+      }
     } else if (is_chain(r)) {
       for (int k = 0; k < r.pre.n; ++k)
         launch_map(r.rt->stream, r.dst->ptr, FO_F32, k == 0 ? r.src->ptr : r.dst->ptr, FO_F32, r.n, r.pre.op[k]);
@@ -1701,10 +1718,16 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     // pending zero fill is not needed; otherwise the fill goes first.
     bool all_live = true;
     for (auto& w : j.wheels) all_live &= w.live == w.size;
+    // A fresh storage written in part from position 0 (a padded layout): one pass writes the live
+    // cells and zero everywhere else the pending fill would have.
+    const uint64_t cap = (dst->capacity + 15) & ~15ull;
+    const bool fused_fill = count > 0 && dst_base == 0 && !narrow && dst->zero_pending && !dst->widen_pending &&
+                            cap % (uint64_t)eb == 0 && cap / (uint64_t)eb < (1ull << 31) &&
+                            !(all_live && count * eb >= (int64_t)dst->bytes);
     if (count > 0 && dst_base == 0 && all_live && count * eb >= (int64_t)dst->bytes) {
       set_device(rt);
       claim_out(rt, dst, dst->bytes);
-    } else {
+    } else if (!fused_fill) {
       check_buf(dst, "dst");
     }
     note_write(dst);
@@ -1715,6 +1738,16 @@ int32_t fo_transpose(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, fo_dt
     TraceScope trace_span(rt, "transpose");
     const int mem[1] = {0};
     const Wheels<1> w = to_desc<1>(j.wheels, mem);
+    if (fused_fill) {
+      Chain c;
+      c.n = 1;
+      c.zero_unwritten = 1;
+      c.total = (uint32_t)(cap / (uint64_t)eb);
+      c.step[0] = ChainStep{w, src_base, (uint32_t)count};
+      mark_filled(dst);
+      launch_relayout_chain(rt->stream, dst->ptr, src->ptr, eb, c);
+      return;
+    }
     if (narrow && launch_relayout_widen(rt->stream, (float*)dst->ptr, (const uint16_t*)wsrc.src->ptr, dst_base, src_base,
                                         count, w))
       return;
