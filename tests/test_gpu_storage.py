@@ -47,6 +47,39 @@ def run_transpose(rt, sizes, src_t, dst_t, dtype, npdt, seed=0, **kw):
     assert np.array_equal(got, want)
 
 
+FRESH_PADDED = [
+    # a slice placement with interior and outer pads (the engine's fresh storages)
+    (dict(N=8, D=128), "N, D", "1 # 2, N, 1 # 32, D"),
+    (dict(N=8, G=2, T=64), "N, G, T", "1 # 2, 1 # 256, N, G, T / 8, T % 8 # 16"),
+    (dict(A=12, B=5), "A, B", "B # 8, A # 16"),
+]
+
+
+@pytest.mark.parametrize("case", FRESH_PADDED, ids=[c[2] for c in FRESH_PADDED])
+@pytest.mark.parametrize("recorded", [True, False], ids=["recorded", "direct"])
+def test_transpose_into_fresh_padded_storage_zeroes_dead_cells(rt, case, recorded):
+    """Tensor::transpose into a fresh zeroed storage (tensor/mod.rs:302-306) whose layout is partly
+    dead: the live cells from the source, every other cell zero, also when the allocation reuses
+    a block that held other data (its fill and the relayout run as one pass). `direct` gives the
+    storage 32 cells more than the view, which takes the unrecorded path; they read zero too."""
+    sizes, src_t, dst_t = case
+    rng = np.random.default_rng(47)
+    so, do = mr.parse(src_t, sizes), mr.parse(dst_t, sizes)
+    n_dst = mr.size(do)
+    extra = 0 if recorded else 32
+    for _ in range(3):  # leave nonzero blocks of this size in the runtime's cache
+        junk = rt.upload(np.full(n_dst + extra, 0x7777, np.uint16))
+        junk.read(np.uint16)
+        del junk
+    src = rand_words(rng, mr.size(so), np.uint16)
+    want = np.concatenate([emu.transpose(np.zeros(n_dst, np.uint16), src, so, do), np.zeros(extra, np.uint16)])
+    d = rt.alloc((n_dst + extra) * 2)
+    rt.transpose(d, rt.upload(src), BF16, fh.m(src_t, **sizes), fh.m(dst_t, **sizes), allow_broadcast=True)
+    got = d.read(np.uint16)
+    assert np.array_equal(got, want)
+    assert (want[:n_dst] == 0).sum() > 0  # the layout has dead cells
+
+
 @pytest.mark.parametrize("case", PAIRS, ids=[f"{c[1]} -> {c[2]}" for c in PAIRS])
 @pytest.mark.parametrize("dt", [(I8, np.int8), (BF16, np.uint16), (I32, np.int32)], ids=["i8", "bf16", "i32"])
 def test_transpose_pairs(rt, case, dt):
