@@ -593,6 +593,29 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
     final_layouts = lambda: es.final_layer(fe, hv(xs, "1, H"), hv(g, "1, H"), hv(lm, "1, Wp / 8192, Wp % 8192, H"),
                                            e_logits)
 
+    # The same three streams recorded once each and launched per token (the NPU's compile-once,
+    # launch-per-call model, runtime.rs:157-177): the host's launch cost leaves the timed path.
+    def recorded(fn):
+        rt.graph_begin()
+        fn()
+        return rt.graph_end().launch
+
+    pg, dg, fg, ag = es.ops(rt), es.ops(rt), es.ops(rt), ea.EngineOps(rt)
+    if graph:
+        ast_ = ea.state(ag)  # the running state's buffers exist before the recording
+        attention_graph = recorded(lambda: ea.chunks(ag, eq, eks, evs, emasks, ast_))
+        projection_graph = recorded(lambda: es.projection(
+            pg, hv(xs, "1, H"), hv(lw["q"], "1, Q, H"), hv(lw["k"], "1, P, H"), hv(lw["v"], "1, P, H"),
+            hv(lw["input_norm"], "1, H"), hv(lw["q_norm"], "1, D"), hv(lw["k_norm"], "1, D"), e_off, hv(cos, "1, D"),
+            hv(sin, "1, D"), e_kc, e_vc, e_q))
+        decoder_graph = recorded(lambda: es.decoder(
+            dg, e_att, e_sum, e_rx, hv(lw["o"], "1, H, Q"), hv(lw["post_norm"], "1, H"), hv(lw["up"], "1, L, H"),
+            hv(lw["gate"], "1, L, H"), hv(lw["down"], "1, H, L")))
+        final_graph = recorded(lambda: es.final_layer(fg, hv(xs, "1, H"), hv(g, "1, H"),
+                                                      hv(lm, "1, Wp / 8192, Wp % 8192, H"), e_logits))
+    else:
+        attention_graph = projection_graph = decoder_graph = final_graph = None
+
     # A whole token of the Qwen3-0.6B-shaped model (28 layers, tied 151936-row embedding) through
     # the pipeline at position T + 88, every layer's caches holding two chunks.
     layers = 28
@@ -629,6 +652,10 @@ def bench_decode(fh, rt, steps, warmup, rng, graph=True):
             ("projection_engine_layouts", projection_layouts, pe, {}),
             ("decoder_engine_layouts", decoder_layouts, de, {}),
             ("final_layer_engine_layouts", final_layouts, fe, dict(hbm_bytes=2 * fd.WP * fd.H)),
+            ("attention_4x512_keys_engine_layouts_graph", attention_graph, ag, dict(keys=4 * fd.T, recorded=True)),
+            ("projection_engine_layouts_graph", projection_graph, pg, dict(recorded=True)),
+            ("decoder_engine_layouts_graph", decoder_graph, dg, dict(recorded=True)),
+            ("final_layer_engine_layouts_graph", final_graph, fg, dict(hbm_bytes=2 * fd.WP * fd.H, recorded=True)),
             ("token_28_layers_pos600", token, pops, dict(hbm_bytes=token_bytes)),
             ("token_28_layers_pos600_graph", token_graph, gops, dict(hbm_bytes=token_bytes, recorded=True))):
         if name.endswith("_graph") and not graph:

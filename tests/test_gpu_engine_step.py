@@ -104,3 +104,38 @@ def test_engine_layout_final_layer_matches_the_oracle(rt):
     assert np.array_equal(got, fd.proj(CPU, widen(st["y"]), lm, "Wp"))
     ok, rate = accepted(dc.final_model(x, g, lm), dc.f64(got[:fd.W]))
     assert ok, rate
+
+
+def test_engine_layout_projection_graph_replays_match_eager(rt):
+    """The projection's engine call stream recorded once (fo_graph_begin .. fo_graph_end, the NPU's
+    compile-once, launch-per-call model, runtime.rs:157-177) and launched three times, with eager
+    writes of its outputs and reads between the launches: every launch equals the eager stream."""
+    a, kc0, vc0 = model_projection_inputs(103)
+    pos = 37
+    cos, sin = fd.rope_row(pos)
+    print("engine-layout projection graph seed 103", flush=True)
+    e = es.ops(rt)
+    ins = (e.put(a["x"], BF16, "1, H"), e.put(a["wq"], BF16, "1, Q, H"), e.put(a["wk"], BF16, "1, P, H"),
+           e.put(a["wv"], BF16, "1, P, H"), e.put(a["g_in"], BF16, "1, H"), e.put(a["g_q"], BF16, "1, D"),
+           e.put(a["g_k"], BF16, "1, D"), e.put(np.array([pos * fd.ROW_STRIDE_ND], np.int32), I32, "1, 1"),
+           e.put(cos, BF16, "1, D"), e.put(sin, BF16, "1, D"))
+    outs = lambda: (e.put(kc0, BF16, "1, T, N, D"), e.put(vc0, BF16, "1, T, N, D"),
+                    e.put(np.zeros(fd.Q, np.uint16), BF16, "1, N, G, D"))
+    kc, vc, q = outs()
+    es.projection(e, *ins, kc, vc, q)
+    want = [e.get(v) for v in (q, kc, vc)]
+    kc, vc, q = outs()
+    rt.graph_begin()
+    es.projection(e, *ins, kc, vc, q)
+    g = rt.graph_end()
+    try:
+        for rep in range(3):
+            q.data.write(np.full(fd.Q, 0x7F7F, np.uint16))
+            kc.data.write(kc0)
+            vc.data.write(vc0)
+            g.launch()
+            got = [e.get(v) for v in (q, kc, vc)]
+            for name, x, y in zip(("q", "k cache", "v cache"), got, want):
+                assert np.array_equal(x, y), f"{name}, launch {rep}"
+    finally:
+        g.free()
