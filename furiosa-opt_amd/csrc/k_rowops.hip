@@ -166,15 +166,16 @@ __global__ void __launch_bounds__(64 * kDmaWaves) k_rmsnorm_softmax_dma(uint16_t
   // and note whether it holds a non-finite value or a magnitude of 2^120 or more (below that no y
   // can overflow once the row's sum of squares is finite: |x_i| <= sqrt(ss) and r >= sqrt(ss / cols)
   // give |y_i| <= sqrt(cols) * max|g| < 2^7 * 2^120).
-  for (int i = threadIdx.x; i < cols; i += blockDim.x) sg[i] = bf16_to_f32(gain[i]);
-  __syncthreads();
-  int bad_local = 0;  // each wave scans the staged row itself (no block-wide flag in LDS)
-  for (int i = lane * 4; i < cols; i += 256) {
-    f32x4_t gv = *(const f32x4_t*)(sg + i);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) bad_local |= !(__builtin_fabsf(gv[k]) < 0x1p120f);
+  // Each thread checks the gain values it stages; one workgroup reduction combines the checks (it
+  // also orders the staging before every wave's reads).
+  int bad_local = 0;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+    const float gv = bf16_to_f32(gain[i]);
+    sg[i] = gv;
+    bad_local |= !(__builtin_fabsf(gv) < 0x1p120f);
   }
-  const bool gain_bad = __any(bad_local);
+  __syncthreads();
+  const bool gain_bad = __syncthreads_or(bad_local) != 0;
   if (row >= rows) return;
   __builtin_amdgcn_s_waitcnt(waitcnt_vm0);
 
