@@ -633,7 +633,9 @@ __global__ void __launch_bounds__(256, 1) k_gemm4(GemmArgs g) {
   const int ntiles = g.tiles_m * g.tiles_n;
   int tile = blockIdx.x;
   if ((ntiles % 8) == 0) tile = (tile % 8) * (ntiles / 8) + tile / 8;
-  const int group = 8;
+  // Each XCD's 32 consecutive tiles form a 4 x 8 block at 4096^2 (4 A and 8 B panels into its L2;
+  // 97.96-98.24 against 98.8-99.2 us for the 8 x 4 block of group 8 on one box).
+  const int group = 4;
   const int gsize = group * g.tiles_n;
   const int first_m = (tile / gsize) * group;
   const int gm = min(g.tiles_m - first_m, group);
