@@ -36,7 +36,8 @@
 // measured 7% slower: the second S tile's 32 registers leave none for LDS reads in flight.)
 // Global loads for the next block are issued into registers before a step and written to LDS
 // after it, so one barrier per block suffices. Blocks below the last kBM / kBN are fully visible to
-// every query of the workgroup and run without mask code.
+// every query of the workgroup and run without mask code; of the last ones, a wave runs the mask
+// code only on a block that hides some key from one of its queries.
 #include <hip/hip_runtime.h>
 
 #include "runtime.hpp"
@@ -89,6 +90,11 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   f32x2_t v = {a, b};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+// f32 -> bf16 (round to nearest even) -> f32 in one instruction: the bf16 lands in the high half of
+// v_cvt_pk_bf16_f32's result above a zero low half, which read as f32 is the bf16 value itself
+// (against a packed pair and two unpacking instructions for two values).
+__device__ __forceinline__ float round_bf16(float x) { return __builtin_bit_cast(float, pack_bf16(0.f, x)); }
 
 template <int D>
 struct AttnCfg {
@@ -162,7 +168,7 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
     const LanePair b = half_pair(bmax);  // the query's other 32 keys live in lane ^ 32
     bmax = __builtin_fmaxf(b.lo, b.hi);
   }
-  bmax = __builtin_bit_cast(float, pack_bf16(bmax, 0.f) << 16);
+  bmax = round_bf16(bmax);
   // Online softmax step with a lazy reference max: O and the sum are rescaled only when some
   // lane's block max exceeds its reference max by more than kTau, so p = exp(s - m_run) stays
   // <= e^kTau = 256 and most blocks skip the rescale of the 64 O registers. The ratio O / sum
@@ -190,8 +196,7 @@ __device__ __forceinline__ void attn_step(const uint8_t* __restrict__ sK, const 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int r = 8 * h + 2 * e;
-        uint32_t w = pack_bf16(xs[kt][r], xs[kt][r + 1]);
-        float x0 = __builtin_bit_cast(float, w << 16), x1 = __builtin_bit_cast(float, w & 0xffff0000u);
+        const float x0 = round_bf16(xs[kt][r]), x1 = round_bf16(xs[kt][r + 1]);
         float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(x0, kL2E, -ms));
         float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(x1, kL2E, -ms));
         if (GIVEN) {
@@ -354,12 +359,19 @@ __global__ void __launch_bounds__(kNT, 2 * 4 / kWaves) k_attn_fwd(uint16_t* __re
     store_v((j + 1) & 1);
     __syncthreads();
   }
+  // In the last blocks a wave runs the mask code only where some key of the block is hidden from
+  // one of its queries: blocks wholly visible to its first query (and inside the sequence) run
+  // unmasked, blocks past its last query are skipped, so each wave masks one block of the diagonal
+  // (and, without causality, the sequence's last) instead of every block up to it.
+  const int vis = causal ? min(q0w, seq - 1) : seq - 1;  // last key every query of the wave sees
   for (; j < nblk; ++j) {
     const int kv0 = j * kBN;
     load_k(kv0 + kBN);
     load_v(kv0 + kBN);
     __builtin_amdgcn_sched_barrier(0);
-    if (!(causal && kv0 > q0w + 31))  // wave-uniform
+    if (kv0 + kBN - 1 <= vis)  // wave-uniform
+      attn_step<D, false, GIVEN>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
+    else if (!(causal && kv0 > q0w + 31))  // wave-uniform
       attn_step<D, true, GIVEN>(sK_of(j & 1), sVt_of(j & 1), qf, o, m_run, l_part, kv0, lim, inv_sd, g, col);
     store_k((j + 1) & 1);
     store_v((j + 1) & 1);
