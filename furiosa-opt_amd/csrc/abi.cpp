@@ -1931,29 +1931,32 @@ int32_t fo_scatter(fo_runtime* rt, fo_buffer* dst, const fo_buffer* src, const f
     int32_t* flag = error_word(rt);
     // Winner words: grown (and zeroed) when too short, and zeroed again when the 32-bit generation
     // wraps; otherwise each call only takes the next generation. A recorded scatter has words of its
-    // own, cleared by a kernel in the graph, so every launch starts from a clean generation.
-    uint64_t* win = rt->scatter_win;
+    // own, cleared by a kernel in the graph, so every launch starts from a clean generation. One key
+    // slot (a cache row append) writes no target twice and needs none: the copy checks the index.
+    uint64_t* win = nullptr;
     uint32_t gen = 0;
-    if (recording(rt)) {
-      auto blk = take_block(rt, (uint64_t)axis_size * 8);
-      launch_zero(rt->stream, blk.first, blk.second);
-      win = (uint64_t*)blk.first;
-      gen = 1;
-    } else if (rt->scatter_win_slots < (uint64_t)axis_size || rt->scatter_gen == UINT32_MAX) {
-      FO_HIP(hipStreamSynchronize(rt->stream));
-      if (rt->scatter_win_slots < (uint64_t)axis_size) {
-        if (rt->scatter_win) FO_HIP(hipFree(rt->scatter_win));
-        rt->scatter_win = nullptr;
-        rt->scatter_win_slots = 0;
-        FO_HIP(hipMalloc((void**)&rt->scatter_win, (size_t)axis_size * 8));
-        rt->scatter_win_slots = (uint64_t)axis_size;
+    if (keys > 1) {
+      if (recording(rt)) {
+        auto blk = take_block(rt, (uint64_t)axis_size * 8);
+        launch_zero(rt->stream, blk.first, blk.second);
+        win = (uint64_t*)blk.first;
+        gen = 1;
+      } else if (rt->scatter_win_slots < (uint64_t)axis_size || rt->scatter_gen == UINT32_MAX) {
+        FO_HIP(hipStreamSynchronize(rt->stream));
+        if (rt->scatter_win_slots < (uint64_t)axis_size) {
+          if (rt->scatter_win) FO_HIP(hipFree(rt->scatter_win));
+          rt->scatter_win = nullptr;
+          rt->scatter_win_slots = 0;
+          FO_HIP(hipMalloc((void**)&rt->scatter_win, (size_t)axis_size * 8));
+          rt->scatter_win_slots = (uint64_t)axis_size;
+        }
+        FO_HIP(hipMemsetAsync(rt->scatter_win, 0, (size_t)rt->scatter_win_slots * 8, rt->stream));
+        rt->scatter_gen = 0;
       }
-      FO_HIP(hipMemsetAsync(rt->scatter_win, 0, (size_t)rt->scatter_win_slots * 8, rt->stream));
-      rt->scatter_gen = 0;
-    }
-    if (!gen) {
-      gen = ++rt->scatter_gen;
-      win = rt->scatter_win;
+      if (!gen) {
+        gen = ++rt->scatter_gen;
+        win = rt->scatter_win;
+      }
     }
     const int mem[1] = {0};
     launch_scatter(rt->stream, dst->ptr, src->ptr, (const int32_t*)index->ptr, eb, np, keys, axis_size, (int32_t)div,

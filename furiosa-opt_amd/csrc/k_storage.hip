@@ -591,7 +591,7 @@ __global__ void __launch_bounds__(kBlock) k_scatter_vec(uint8_t* __restrict__ ds
                                                         int64_t eb, const int32_t* __restrict__ idx,
                                                         const uint64_t* __restrict__ win, uint64_t tag, uint32_t total,
                                                         FastDiv cdiv, uint32_t keys, uint32_t axis_size, int32_t div,
-                                                        Wheels<1> ws, Wheels<1> wd) {
+                                                        Wheels<1> ws, Wheels<1> wd, int32_t* __restrict__ flag) {
   typedef __attribute__((__vector_size__(4 * sizeof(int)))) int vec_t;
   constexpr int U = kChunkRuns;  // as in k_gather_vec; the data read does not wait for the index
   const uint64_t stride = (uint64_t)gridDim.x * kBlock;
@@ -609,9 +609,12 @@ __global__ void __launch_bounds__(kBlock) k_scatter_vec(uint8_t* __restrict__ ds
       if (t < total) v[u] = *(const vec_t*)(src + wheel_offset(ws, c[u] * V * keys + k[u]) * eb);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (a[u] >= 0 && win[a[u]] == (tag | k[u]))
+    for (int u = 0; u < U; ++u) {
+      if (a[u] >= 0 && (!win || win[a[u]] == (tag | k[u])))
         *(vec_t*)(dst + wheel_offset(wd, c[u] * V * axis_size + (uint32_t)a[u]) * eb) = v[u];
+      else if (!win && a[u] < 0 && t0 + u * stride < total)
+        *flag = 1;  // no winners pass ran to report it
+    }
   }
 }
 
@@ -646,11 +649,15 @@ template <typename T>
 __global__ void __launch_bounds__(kBlock) k_scatter(T* __restrict__ dst, const T* __restrict__ src,
                                                     const int32_t* __restrict__ idx, const uint64_t* __restrict__ win,
                                                     uint64_t tag, uint32_t total, FastDiv kdiv, uint32_t axis_size,
-                                                    int32_t div, Wheels<1> ws, Wheels<1> wd) {
+                                                    int32_t div, Wheels<1> ws, Wheels<1> wd, int32_t* __restrict__ flag) {
   for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < total; t += gridDim.x * kBlock) {
     uint32_t p = kdiv.div(t), k = t - p * kdiv.d;
     int32_t a = decode_index(idx, k, div, axis_size);
-    if (a < 0 || win[a] != (tag | k)) continue;
+    if (a < 0) {
+      if (!win) *flag = 1;  // no winners pass ran to report it
+      continue;
+    }
+    if (win && win[a] != (tag | k)) continue;
     dst[wheel_offset(wd, p * axis_size + (uint32_t)a)] = src[wheel_offset(ws, t)];
   }
 }
@@ -2037,9 +2044,11 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
                     const Wheels<1>& wd, int ws_slot_wheels, int wd_slot_wheels, uint64_t* win, uint32_t gen,
                     int32_t* flag) {
   const uint64_t tag = (uint64_t)gen << 32;
-  hipLaunchKernelGGL(k_scatter_winners, dim3(grid_for(keys)), dim3(kBlock), 0, s, idx, (uint32_t)keys,
-                     (uint32_t)axis_size, div, win, tag, flag);
-  FO_HIP(hipGetLastError());
+  if (win) {  // without winner words (one key slot: no target is written twice) the copy checks the indices
+    hipLaunchKernelGGL(k_scatter_winners, dim3(grid_for(keys)), dim3(kBlock), 0, s, idx, (uint32_t)keys,
+                       (uint32_t)axis_size, div, win, tag, flag);
+    FO_HIP(hipGetLastError());
+  }
   const int V = (int)(16 / elem_bytes);
   if (((uintptr_t)dst | (uintptr_t)src) % 16 == 0 && payload_vec_ok(ws, ws_slot_wheels, V) &&
       payload_vec_ok(wd, wd_slot_wheels, V)) {
@@ -2048,13 +2057,13 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
     const FastDiv cdiv(nch);
     if (V == 8)
       hipLaunchKernelGGL(k_scatter_vec<8>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, tag,
-                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd, flag);
     else if (V == 4)
       hipLaunchKernelGGL(k_scatter_vec<4>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win, tag,
-                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+                         total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd, flag);
     else
       hipLaunchKernelGGL(k_scatter_vec<16>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, elem_bytes, idx, win,
-                         tag, total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd);
+                         tag, total, cdiv, (uint32_t)keys, (uint32_t)axis_size, div, ws, wd, flag);
     FO_HIP(hipGetLastError());
     return;
   }
@@ -2064,15 +2073,15 @@ void launch_scatter(hipStream_t s, void* dst, const void* src, const int32_t* id
   switch (elem_bytes) {
     case 1:
       hipLaunchKernelGGL(k_scatter<uint8_t>, g, b, 0, s, (uint8_t*)dst, (const uint8_t*)src, idx, win, tag, total, kdiv,
-                         (uint32_t)axis_size, div, ws, wd);
+                         (uint32_t)axis_size, div, ws, wd, flag);
       break;
     case 2:
       hipLaunchKernelGGL(k_scatter<uint16_t>, g, b, 0, s, (uint16_t*)dst, (const uint16_t*)src, idx, win, tag, total, kdiv,
-                         (uint32_t)axis_size, div, ws, wd);
+                         (uint32_t)axis_size, div, ws, wd, flag);
       break;
     case 4:
       hipLaunchKernelGGL(k_scatter<uint32_t>, g, b, 0, s, (uint32_t*)dst, (const uint32_t*)src, idx, win, tag, total, kdiv,
-                         (uint32_t)axis_size, div, ws, wd);
+                         (uint32_t)axis_size, div, ws, wd, flag);
       break;
     default:
       throw InvalidArg("scatter: unsupported element size");

@@ -1112,6 +1112,29 @@ def test_scatter_gather_bad_index_is_an_error(rt, bad):
     assert np.all(got[[0, 3, 1]] == 1) and got.sum() == 3 * 5
 
 
+@pytest.mark.parametrize("dt,d", [(I32, 5), (fh.BF16, 16)])
+def test_scatter_single_key_slot(rt, dt, d):
+    """One key slot (the cache row append of transformer.py:432-435) runs without winner words, as
+    element copies (5 i32) or 16-byte chunks (16 bf16): rows land where the index says, later calls
+    over earlier ones, and a bad index writes nothing and is reported by the next synchronize."""
+    np_t = np.int32 if dt == I32 else np.uint16
+    s = dict(G=1, D=d, K=37)
+    maps = (fh.m("G, D", **s), fh.m("G", **s), fh.m("K, D", **s), fh.m("G", **s))
+    cache0 = np.arange(37 * d).astype(np_t)
+    cache = rt.upload(cache0)
+    want = cache0.reshape(37, d).copy()
+    for i, r in enumerate((0, 36, 11, 36)):
+        row = np.full(d, 1000 + i, np_t)
+        rt.scatter(cache, rt.upload(row), rt.upload(np.array([r], np.int32)), dt, *maps, scaled=False)
+        want[r] = row
+    assert np.array_equal(cache.read(np_t).reshape(37, d), want)
+    for bad in (-1, 37):
+        rt.scatter(cache, rt.upload(np.zeros(d, np_t)), rt.upload(np.array([bad], np.int32)), dt, *maps, scaled=False)
+        with pytest.raises(fh.FoError, match="scatter: an index"):
+            rt.sync()
+    assert np.array_equal(cache.read(np_t).reshape(37, d), want)
+
+
 # ---- safetensors loading (tensor/memory.rs:190-223) ------------------------------------------------
 
 
